@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention hot path on one MI355X.
+
+Workload ("c2"): FLUX-style joint attention at
+1024 px — B=1, H=24, D=128, S=4608 (512 txt + 64x64 img tokens), bf16.
+Raw Q/K ~ N(0,1) are QK-RMSNormed (scale 1+N(0,0.02)) and axial-roped (axes
+16/56/56, theta 1e4) by the fused prologue kernel once, outside the timed
+region; V, dO ~ N(0,1).  One step = attention forward (O + LSE) + backward
+(dQ, dK, dV) through libfoundry_attn.so, inputs resident in HBM.
+
+value = 14*B*H*S^2*D / step time (forward 4*B*H*S^2*D, backward 2.5x that).
+
+Prints ONE JSON line.  Besides the contract fields it carries:
+  roofline      for the kernel with the largest share of the step time
+                (HIP events on the launch stream, averaged over the timed steps)
+  cpu_baseline  the CPU oracle (restatement of the reference's Candle CPU path,
+                materialised f32 scores, 5-GEMM backward) timed on this host
+                on a bounded sample of the same workload
+  kernels       per-kernel times and rates
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "foundry-trainer_amd"))
+
+METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block steps/s"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c5"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound on the CPU baseline sample (0 = skip)")
+    return ap.parse_args()
+
+
+def make_inputs(cfg, torch, fa):
+    g = torch.Generator(device="cuda").manual_seed(20261028)
+    B, S, H, D = cfg.batch, cfg.seq, cfg.heads, cfg.head_dim
+    bf = torch.bfloat16
+    rq = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
+    rk = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
+    v = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
+    do = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
+    wq = (1 + 0.02 * torch.randn(D, device="cuda", generator=g)).to(bf)
+    wk = (1 + 0.02 * torch.randn(D, device="cuda", generator=g)).to(bf)
+    cos, sin = fa.rope_tables(cfg.positions(), cfg.axes, cfg.theta, dtype=bf)
+    q = torch.empty_like(rq)
+    k = torch.empty_like(rk)
+    fa.qk_prologue(rq, wq, cos, sin, cfg.axes, out=q)
+    fa.qk_prologue(rk, wk, cos, sin, cfg.axes, out=k)
+    keep = None
+    if cfg.key_keep() is not None:
+        keep = torch.from_numpy(cfg.key_keep()).to("cuda")
+        do = do * keep[:, :, None, None].to(bf)
+    return q, k, v, do, keep
+
+
+def cpu_baseline(cfg, budget_s: float):
+    """The oracle (port of the reference's Candle CPU path) on whole heads of
+    the same workload, f32 arithmetic on bf16-valued inputs, all host cores."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = oracle.default_threads()
+    rng = np.random.default_rng(0)
+    B, S, D = 1, cfg.seq, cfg.head_dim
+    mk = lambda: oracle.bf16_round(rng.standard_normal((B, S, 1, D)).astype(np.float32))
+    q, k, v, do = mk(), mk(), mk(), mk()
+    heads, t = 0, 0.0
+    while t < budget_s and heads < cfg.heads * cfg.batch:
+        t0 = time.perf_counter()
+        oracle.attn_fwd(q, k, v, scale=cfg.scale, bf16=True, nthreads=threads)
+        oracle.attn_bwd(q, k, v, do, scale=cfg.scale, bf16=True, nthreads=threads)
+        t += time.perf_counter() - t0
+        heads += 1
+    flops = 14.0 * S * S * D * heads
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{heads} head(s) of {cfg.name} (S={S}, D={D}) fwd+bwd, oracle "
+                      f"(materialised f32 scores, 5-GEMM backward), {t:.1f} s on {cpu_model}",
+            "ms_per_head": round(1e3 * t / heads, 1)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build is single-GPU; --gpus {args.gpus} is not supported "
+              "(the attention path shards over (B, H) across GPUs by design, see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import torch
+    import foundry_attn as fa
+    from foundry_attn.configs import CONFIGS
+
+    cfg = CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    q, k, v, do, keep = make_inputs(cfg, torch, fa)
+    lse = torch.empty((cfg.batch, cfg.heads, cfg.seq), dtype=torch.float32, device="cuda")
+    o = torch.empty_like(q)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(ev=None):
+        if ev:
+            ev[0].record(stream)
+        fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
+        if ev:
+            ev[1].record(stream)
+        g = fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws)
+        if ev:
+            ev[2].record(stream)
+        return g
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = 1e3 * wall / args.steps
+
+    # per-phase HIP-event timing (same stream as the launches), separate pass
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
+
+    f_fwd = cfg.fwd_flops()
+    f_all = f_fwd + cfg.bwd_flops()
+    value = f_all / (ms * 1e-3) / 1e12
+    fwd_tf = f_fwd / (fwd_ms * 1e-3) / 1e12
+    bwd_tf = cfg.bwd_flops() / (bwd_ms * 1e-3) / 1e12
+    dominant = "attn_bwd" if bwd_ms >= fwd_ms else "attn_fwd"
+    dom_ms = max(bwd_ms, fwd_ms)
+    dom_flops = cfg.bwd_flops() if dominant == "attn_bwd" else f_fwd
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V/dO; Q/K RMSNormed + axial RoPE by the prologue kernel)",
+        "config": {"workload": f"{cfg.name}: joint attention fwd+bwd, B={cfg.batch} H={cfg.heads} "
+                               f"S={cfg.seq} ({cfg.txt_len} txt + {cfg.img_rows}x{cfg.img_cols} img) "
+                               f"D={cfg.head_dim} bf16" + (", key-padding mask" if keep is not None else ""),
+                   "batch": cfg.batch, "heads": cfg.heads, "seq_len": cfg.seq,
+                   "head_dim": cfg.head_dim, "parallelism": "single GPU"},
+        "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "kernel": dominant,
+                     "achieved": round(dom_flops / (dom_ms * 1e-3) / 1e12, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(dom_flops / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "kernels": {"attn_fwd": {"ms": round(fwd_ms, 4), "tflops": round(fwd_tf, 2),
+                                 "pct_of_peak": round(100 * fwd_tf / PEAK_BF16_TFLOPS, 2)},
+                    "attn_bwd": {"ms": round(bwd_ms, 4), "tflops": round(bwd_tf, 2),
+                                 "pct_of_peak": round(100 * bwd_tf / PEAK_BF16_TFLOPS, 2)}},
+    }
+    if args.cpu_seconds > 0:
+        rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    else:
+        rec["cpu_baseline"] = None
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,420 @@
+// extern "C" boundary of libfoundry_attn.so (declared in include/foundry_attn.h).
+// Validates every argument before touching the device, maps failures to
+// fa_status codes with a thread-local message, and forwards to the kernel
+// launchers.  No C++ exception crosses the boundary.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "../../include/foundry_attn.h"
+#include "fa_kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+fa_status fail(fa_status code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+fa_status ok() {
+    g_err[0] = '\0';
+    return FA_OK;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_init_mu;
+int g_dev_state[kMaxDevices];  // 0 unknown, 1 ready, -1 unsupported
+bool g_prepared = false;
+
+fa_status hip_fail(hipError_t e, const char *what) {
+    return fail(FA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+fa_status init_device(int device) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(FA_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count || device >= kMaxDevices)
+        return fail(FA_ERR_INVALID_ARG, "device %d out of range (count %d)", device, count);
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    if (g_dev_state[device] == 0) {
+        hipDeviceProp_t prop;
+        hipError_t e = hipGetDeviceProperties(&prop, device);
+        if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+        g_dev_state[device] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+        if (g_dev_state[device] < 0)
+            return fail(FA_ERR_LOAD_FAILED, "device %d is %s; this library holds gfx950 code only",
+                        device, prop.gcnArchName);
+    }
+    if (g_dev_state[device] < 0) return fail(FA_ERR_LOAD_FAILED, "device %d is not gfx950", device);
+    if (!g_prepared) {
+        hipError_t e = fa::prepare_attn_kernels();
+        if (e != hipSuccess) return hip_fail(e, "kernel attribute setup");
+        g_prepared = true;
+    }
+    return FA_OK;
+}
+
+fa_status init_current() {
+    int dev = 0, count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(FA_ERR_NO_DEVICE, "no HIP device visible");
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    return init_device(dev);
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+const char *dtype_name(int32_t dt) { return dt == FA_DTYPE_BF16 ? "bf16" : "f32"; }
+
+// Checks a [B,S,H,D] view: non-null, non-negative strides, and alignment so
+// that every row start is 16-byte aligned for bf16 (vector loads) and 4-byte
+// aligned for f32.
+fa_status check_view(const char *name, const void *ptr, const fa_strides &st, int32_t dtype) {
+    if (!ptr) return fail(FA_ERR_INVALID_ARG, "%s is NULL", name);
+    if (st.b < 0 || st.s < 0 || st.h < 0)
+        return fail(FA_ERR_INVALID_ARG, "%s has a negative stride", name);
+    if (dtype == FA_DTYPE_BF16) {
+        if (!aligned(ptr, 16)) return fail(FA_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
+        if ((st.b | st.s | st.h) % 8)
+            return fail(FA_ERR_INVALID_ARG,
+                        "%s strides (%lld,%lld,%lld) must be multiples of 8 elements (bf16)", name,
+                        (long long)st.b, (long long)st.s, (long long)st.h);
+    } else if (!aligned(ptr, 4)) {
+        return fail(FA_ERR_INVALID_ARG, "%s is not 4-byte aligned", name);
+    }
+    return FA_OK;
+}
+
+fa_status check_attn_shape(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D, float scale) {
+    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32)
+        return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (B < 1 || S < 1 || H < 1)
+        return fail(FA_ERR_INVALID_ARG, "batch/seq/heads must be >= 1 (got %d/%d/%d)", B, S, H);
+    if (S > (1 << 22)) return fail(FA_ERR_INVALID_ARG, "seq %d exceeds 4194304", S);
+    if (D != 64 && D != 128)
+        return fail(FA_ERR_UNSUPPORTED, "head_dim %d: this build implements 64 and 128", D);
+    if (!isfinite(scale) || !(scale > 0.f))
+        return fail(FA_ERR_INVALID_ARG, "scale must be finite and > 0 (got %g)", (double)scale);
+    const int64_t tiles = (int64_t)B * H * ((S + 31) / 32);
+    if (tiles > 0x7fffffffLL) return fail(FA_ERR_INVALID_ARG, "B*H*S too large for one launch");
+    return FA_OK;
+}
+
+size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t bwd_workspace(int32_t B, int32_t S, int32_t H) {
+    return round256((size_t)B * H * S * sizeof(float));
+}
+
+#define FA_TRY(expr)                      \
+    do {                                  \
+        const fa_status st__ = (expr);    \
+        if (st__ != FA_OK) return st__;   \
+    } while (0)
+
+}  // namespace
+
+namespace fa {
+hipError_t prepare_fwd_kernels();
+hipError_t prepare_bwd_kernels();
+hipError_t prepare_attn_kernels() {
+    hipError_t e = prepare_fwd_kernels();
+    if (e != hipSuccess) return e;
+    return prepare_bwd_kernels();
+}
+}  // namespace fa
+
+extern "C" {
+
+int fa_version(void) { return FA_ABI_VERSION; }
+
+const char *fa_last_error(void) { return g_err; }
+
+const char *fa_op_name(void) { return "foundry-attn-bwd"; }
+
+fa_status fa_init(int device) {
+    FA_TRY(init_device(device));
+    return ok();
+}
+
+fa_status fa_attn_fwd(const fa_attn_fwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_attn_shape(a->dtype, a->batch, a->seq, a->heads, a->head_dim, a->scale));
+    FA_TRY(check_view("q", a->q, a->q_stride, a->dtype));
+    FA_TRY(check_view("k", a->k, a->k_stride, a->dtype));
+    FA_TRY(check_view("v", a->v, a->v_stride, a->dtype));
+    FA_TRY(check_view("o", a->o, a->o_stride, a->dtype));
+    if (!a->lse || !aligned(a->lse, 4)) return fail(FA_ERR_INVALID_ARG, "lse is NULL or misaligned");
+    FA_TRY(init_current());
+
+    fa::AttnFwdParams p{};
+    p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.lse = a->lse; p.keep = a->key_keep;
+    p.q_sb = a->q_stride.b; p.q_ss = a->q_stride.s; p.q_sh = a->q_stride.h;
+    p.k_sb = a->k_stride.b; p.k_ss = a->k_stride.s; p.k_sh = a->k_stride.h;
+    p.v_sb = a->v_stride.b; p.v_ss = a->v_stride.s; p.v_sh = a->v_stride.h;
+    p.o_sb = a->o_stride.b; p.o_ss = a->o_stride.s; p.o_sh = a->o_stride.h;
+    p.B = a->batch; p.S = a->seq; p.H = a->heads;
+    p.scale = a->scale;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const hipError_t e = a->dtype == FA_DTYPE_BF16 ? fa::launch_attn_fwd_bf16(p, a->head_dim, s)
+                                                   : fa::launch_attn_fwd_f32(p, a->head_dim, s);
+    if (e != hipSuccess) return hip_fail(e, "attention forward launch");
+    return ok();
+}
+
+size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *a) {
+    if (!a || a->batch < 1 || a->seq < 1 || a->heads < 1) return 0;
+    return bwd_workspace(a->batch, a->seq, a->heads);
+}
+
+fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_attn_shape(a->dtype, a->batch, a->seq, a->heads, a->head_dim, a->scale));
+    FA_TRY(check_view("q", a->q, a->q_stride, a->dtype));
+    FA_TRY(check_view("k", a->k, a->k_stride, a->dtype));
+    FA_TRY(check_view("v", a->v, a->v_stride, a->dtype));
+    FA_TRY(check_view("o", a->o, a->o_stride, a->dtype));
+    FA_TRY(check_view("dout", a->dout, a->do_stride, a->dtype));
+    FA_TRY(check_view("dq", a->dq, a->dq_stride, a->dtype));
+    FA_TRY(check_view("dk", a->dk, a->dk_stride, a->dtype));
+    FA_TRY(check_view("dv", a->dv, a->dv_stride, a->dtype));
+    if (!a->lse || !aligned(a->lse, 4)) return fail(FA_ERR_INVALID_ARG, "lse is NULL or misaligned");
+    const size_t need = bwd_workspace(a->batch, a->seq, a->heads);
+    if (!a->workspace || !aligned(a->workspace, 256))
+        return fail(FA_ERR_INVALID_ARG, "workspace is NULL or not 256-byte aligned");
+    if (a->workspace_bytes < need)
+        return fail(FA_ERR_INVALID_ARG, "workspace of %zu bytes is smaller than the %zu needed",
+                    a->workspace_bytes, need);
+    FA_TRY(init_current());
+
+    fa::AttnBwdParams p{};
+    p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
+    p.keep = a->key_keep; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
+    p.delta = static_cast<float *>(a->workspace);
+    p.q_sb = a->q_stride.b; p.q_ss = a->q_stride.s; p.q_sh = a->q_stride.h;
+    p.k_sb = a->k_stride.b; p.k_ss = a->k_stride.s; p.k_sh = a->k_stride.h;
+    p.v_sb = a->v_stride.b; p.v_ss = a->v_stride.s; p.v_sh = a->v_stride.h;
+    p.o_sb = a->o_stride.b; p.o_ss = a->o_stride.s; p.o_sh = a->o_stride.h;
+    p.do_sb = a->do_stride.b; p.do_ss = a->do_stride.s; p.do_sh = a->do_stride.h;
+    p.dq_sb = a->dq_stride.b; p.dq_ss = a->dq_stride.s; p.dq_sh = a->dq_stride.h;
+    p.dk_sb = a->dk_stride.b; p.dk_ss = a->dk_stride.s; p.dk_sh = a->dk_stride.h;
+    p.dv_sb = a->dv_stride.b; p.dv_ss = a->dv_stride.s; p.dv_sh = a->dv_stride.h;
+    p.B = a->batch; p.S = a->seq; p.H = a->heads;
+    p.scale = a->scale;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const hipError_t e = a->dtype == FA_DTYPE_BF16 ? fa::launch_attn_bwd_bf16(p, a->head_dim, s)
+                                                   : fa::launch_attn_bwd_f32(p, a->head_dim, s);
+    if (e != hipSuccess) return hip_fail(e, "attention backward launch");
+    return ok();
+}
+
+}  // extern "C"
+
+static fa_status check_prologue(const fa_qk_prologue_args *a) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)
+        return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", a->dtype);
+    if (a->batch < 1 || a->tokens < 1 || a->heads < 1)
+        return fail(FA_ERR_INVALID_ARG, "batch/tokens/heads must be >= 1");
+    if (a->head_dim != 64 && a->head_dim != 128)
+        return fail(FA_ERR_UNSUPPORTED, "head_dim %d: this build implements 64 and 128", a->head_dim);
+    if (!(a->eps >= 0.f) || !isfinite(a->eps)) return fail(FA_ERR_INVALID_ARG, "eps must be finite, >= 0");
+    if (a->n_axes < 1 || a->n_axes > FA_MAX_ROPE_AXES)
+        return fail(FA_ERR_INVALID_ARG, "n_axes %d outside 1..%d", a->n_axes, FA_MAX_ROPE_AXES);
+    int sum = 0;
+    for (int i = 0; i < a->n_axes; ++i) {
+        if (a->axes[i] <= 0 || (a->axes[i] & 1))
+            return fail(FA_ERR_INVALID_ARG, "rope axis %d width %d must be even and > 0", i, a->axes[i]);
+        sum += a->axes[i];
+    }
+    if (sum != a->head_dim)
+        return fail(FA_ERR_INVALID_ARG, "rope axes sum to %d, head_dim is %d", sum, a->head_dim);
+    if (a->y_seq_offset < 0) return fail(FA_ERR_INVALID_ARG, "y_seq_offset < 0");
+    FA_TRY(check_view("x", a->x, a->x_stride, a->dtype));
+    FA_TRY(check_view("y", a->y, a->y_stride, a->dtype));
+    const size_t elt = a->dtype == FA_DTYPE_BF16 ? 2 : 4;
+    if (!a->weight || !aligned(a->weight, elt)) return fail(FA_ERR_INVALID_ARG, "weight is NULL or misaligned");
+    if (!a->cos || !a->sin || !aligned(a->cos, elt) || !aligned(a->sin, elt))
+        return fail(FA_ERR_INVALID_ARG, "cos/sin table is NULL or misaligned");
+    if (a->dtype == FA_DTYPE_F32 && ((a->x_stride.b | a->x_stride.s | a->x_stride.h |
+                                      a->y_stride.b | a->y_stride.s | a->y_stride.h) % 4 ||
+                                     !aligned(a->x, 16) || !aligned(a->y, 16)))
+        return fail(FA_ERR_INVALID_ARG, "f32 prologue rows must be 16-byte aligned");
+    return FA_OK;
+}
+
+static void fill_prologue(const fa_qk_prologue_args *a, fa::QkPrologueParams &p) {
+    p.x = a->x; p.x_sb = a->x_stride.b; p.x_ss = a->x_stride.s; p.x_sh = a->x_stride.h;
+    p.w = a->weight; p.cos = a->cos; p.sin = a->sin;
+    p.y = a->y; p.y_sb = a->y_stride.b; p.y_ss = a->y_stride.s; p.y_sh = a->y_stride.h;
+    p.y_off = a->y_seq_offset;
+    p.B = a->batch; p.T = a->tokens; p.H = a->heads; p.D = a->head_dim; p.eps = a->eps;
+    p.n_axes = a->n_axes;
+    for (int i = 0; i < FA_MAX_ROPE_AXES; ++i) p.axes[i] = i < a->n_axes ? a->axes[i] : 0;
+}
+
+static fa_status check_lora(const fa_lora_args *a) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)
+        return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", a->dtype);
+    if (a->tokens < 1 || a->in_features < 1 || a->out_features < 1)
+        return fail(FA_ERR_INVALID_ARG, "tokens/in_features/out_features must be >= 1");
+    if (a->rank < 1 || a->rank > 32)
+        return fail(FA_ERR_UNSUPPORTED, "rank %d: this build implements 1..32", a->rank);
+    if (!isfinite(a->scale)) return fail(FA_ERR_INVALID_ARG, "scale must be finite");
+    const int kmul = a->dtype == FA_DTYPE_BF16 ? 16 : 2;
+    if (a->in_features % kmul || a->out_features % kmul)
+        return fail(FA_ERR_UNSUPPORTED, "in/out features must be multiples of %d", kmul);
+    const size_t elt = a->dtype == FA_DTYPE_BF16 ? 2 : 4;
+    if (!a->x || !aligned(a->x, 16) || a->ldx < a->in_features || (a->ldx * (int64_t)elt) % 16)
+        return fail(FA_ERR_INVALID_ARG, "x is NULL, misaligned, or ldx < in_features");
+    if (!a->a || !aligned(a->a, 16)) return fail(FA_ERR_INVALID_ARG, "a is NULL or misaligned");
+    if (!a->b || !aligned(a->b, elt)) return fail(FA_ERR_INVALID_ARG, "b is NULL or misaligned");
+    if (!a->u || !aligned(a->u, 4)) return fail(FA_ERR_INVALID_ARG, "u is NULL or misaligned");
+    return FA_OK;
+}
+
+static void fill_lora(const fa_lora_args *a, fa::LoraParams &p) {
+    p.x = a->x; p.ldx = a->ldx; p.a = a->a; p.b = a->b; p.u = a->u; p.y = a->y; p.ldy = a->ldy;
+    p.N = a->tokens; p.K = a->in_features; p.M = a->out_features; p.r = a->rank; p.scale = a->scale;
+}
+
+namespace fa {
+size_t lora_bwd_workspace_bytes(int N, int K, int M, int r, int elt);
+}
+
+extern "C" {
+
+fa_status fa_qk_prologue_fwd(const fa_qk_prologue_args *a, void *stream) {
+    FA_TRY(check_prologue(a));
+    FA_TRY(init_current());
+    fa::QkPrologueParams p{};
+    fill_prologue(a, p);
+    const hipError_t e = fa::launch_qk_prologue_fwd(p, a->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "qk prologue forward launch");
+    return ok();
+}
+
+fa_status fa_qk_prologue_bwd(const fa_qk_prologue_bwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_prologue(&a->fwd));
+    FA_TRY(check_view("dy", a->dy, a->fwd.y_stride, a->fwd.dtype));
+    FA_TRY(check_view("dx", a->dx, a->dx_stride, a->fwd.dtype));
+    if (a->fwd.dtype == FA_DTYPE_F32 &&
+        ((a->dx_stride.b | a->dx_stride.s | a->dx_stride.h) % 4 || !aligned(a->dx, 16) ||
+         !aligned(a->dy, 16)))
+        return fail(FA_ERR_INVALID_ARG, "f32 prologue rows must be 16-byte aligned");
+    FA_TRY(init_current());
+    fa::QkPrologueParams p{};
+    fill_prologue(&a->fwd, p);
+    p.dy = a->dy; p.dx = a->dx;
+    p.dx_sb = a->dx_stride.b; p.dx_ss = a->dx_stride.s; p.dx_sh = a->dx_stride.h;
+    const hipError_t e = fa::launch_qk_prologue_bwd(p, a->fwd.dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "qk prologue backward launch");
+    return ok();
+}
+
+static uint16_t to_bf16_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+fa_status fa_rope_tables_host(const float *positions, int32_t n_pos, int32_t n_axes,
+                              const int32_t *axes, float theta, int32_t dtype, void *cos_out,
+                              void *sin_out) {
+    if (!positions || !axes || !cos_out || !sin_out) return fail(FA_ERR_INVALID_ARG, "NULL pointer");
+    if (n_pos < 0 || n_axes < 1 || n_axes > FA_MAX_ROPE_AXES)
+        return fail(FA_ERR_INVALID_ARG, "bad n_pos / n_axes");
+    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32)
+        return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (!isfinite(theta) || !(theta > 0.f)) return fail(FA_ERR_INVALID_ARG, "theta must be > 0");
+    int D = 0;
+    for (int a = 0; a < n_axes; ++a) {
+        if (axes[a] <= 0 || (axes[a] & 1)) return fail(FA_ERR_INVALID_ARG, "axis widths must be even, > 0");
+        D += axes[a];
+    }
+    for (int p = 0; p < n_pos; ++p) {
+        int off = 0;
+        for (int a = 0; a < n_axes; ++a) {
+            const int w = axes[a], half = w / 2;
+            for (int j = 0; j < half; ++j) {
+                const float inv = powf(theta, -2.0f * (float)j / (float)w);
+                const float f = positions[(int64_t)p * n_axes + a] * inv;
+                const float c = cosf(f), s = sinf(f);
+                for (int rep = 0; rep < 2; ++rep) {
+                    const int64_t i = (int64_t)p * D + off + rep * half + j;
+                    if (dtype == FA_DTYPE_F32) {
+                        static_cast<float *>(cos_out)[i] = c;
+                        static_cast<float *>(sin_out)[i] = s;
+                    } else {
+                        static_cast<uint16_t *>(cos_out)[i] = to_bf16_bits(c);
+                        static_cast<uint16_t *>(sin_out)[i] = to_bf16_bits(s);
+                    }
+                }
+            }
+            off += w;
+        }
+    }
+    return ok();
+}
+
+fa_status fa_lora_fwd(const fa_lora_args *a, void *stream) {
+    FA_TRY(check_lora(a));
+    const size_t elt = a->dtype == FA_DTYPE_BF16 ? 2 : 4;
+    if (!a->y || !aligned(a->y, elt) || a->ldy < a->out_features)
+        return fail(FA_ERR_INVALID_ARG, "y is NULL, misaligned, or ldy < out_features");
+    FA_TRY(init_current());
+    fa::LoraParams p{};
+    fill_lora(a, p);
+    const hipError_t e = fa::launch_lora_fwd(p, a->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lora forward launch");
+    return ok();
+}
+
+size_t fa_lora_bwd_workspace_size(const fa_lora_bwd_args *a) {
+    if (!a || a->fwd.tokens < 1 || a->fwd.rank < 1 || a->fwd.in_features < 1 || a->fwd.out_features < 1)
+        return 0;
+    return fa::lora_bwd_workspace_bytes(a->fwd.tokens, a->fwd.in_features, a->fwd.out_features,
+                                        a->fwd.rank, a->fwd.dtype == FA_DTYPE_BF16 ? 2 : 4);
+}
+
+fa_status fa_lora_bwd(const fa_lora_bwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_lora(&a->fwd));
+    const size_t elt = a->fwd.dtype == FA_DTYPE_BF16 ? 2 : 4;
+    if (!a->dy || !aligned(a->dy, 16) || a->ldy < a->fwd.out_features || (a->ldy * (int64_t)elt) % 16)
+        return fail(FA_ERR_INVALID_ARG, "dy is NULL, misaligned, or ldy < out_features");
+    if (!a->da || !a->db || !aligned(a->da, 4) || !aligned(a->db, 4))
+        return fail(FA_ERR_INVALID_ARG, "da/db is NULL or misaligned");
+    if (a->dx && (!aligned(a->dx, elt) || a->ldx < a->fwd.in_features))
+        return fail(FA_ERR_INVALID_ARG, "dx misaligned or ldx < in_features");
+    const size_t need = fa_lora_bwd_workspace_size(a);
+    if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < need)
+        return fail(FA_ERR_INVALID_ARG, "workspace missing, misaligned or smaller than %zu bytes", need);
+    FA_TRY(init_current());
+    fa::LoraParams p{};
+    fill_lora(&a->fwd, p);
+    p.dy = a->dy; p.lddy = a->ldy; p.da = a->da; p.db = a->db; p.dx = a->dx; p.lddx = a->ldx;
+    p.work = static_cast<float *>(a->workspace);
+    const hipError_t e = fa::launch_lora_bwd(p, a->fwd.dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lora backward launch");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,109 @@
+// Device-side helpers shared by the gfx950 kernels: vector types, the
+// bf16 MFMA wrappers, conversions, LDS swizzles and the XCD-aware block map.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// v_mfma_f32_32x32x16_bf16.  Operand lane layout (wave64):
+//   A[m][k]: lane = m + 32*(k/8), element k%8     (m, k < 32, 16)
+//   B[k][n]: lane = n + 32*(k/8), element k%8
+//   C[m][n]: lane = n + 32*((m/4)%2), element (m/8)*4 + m%4
+// Only the m/n placement matters to the kernels: any k permutation applied
+// identically to A and B leaves the product unchanged.
+__device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x2_f32: A[m][k] lane = m + 32*k, B[k][n] lane = n + 32*k.
+__device__ __forceinline__ f32x16 mfma_32x32x2_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row index (within a 32-row tile) of accumulator element r of `lane`.
+__device__ __forceinline__ int acc_row(int r, int lane) {
+    return (r >> 2) * 8 + ((lane >> 5) << 2) + (r & 3);
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ __forceinline__ float bf16_to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ bf16 f32_to_bf16(float x) { return (bf16)x; }  // RNE
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2 v = {(bf16)lo, (bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ u32x4 ld_global_16(const void *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ __forceinline__ void st_global_16(void *p, u32x4 v) {
+    *reinterpret_cast<u32x4 *>(p) = v;
+}
+__device__ __forceinline__ u32x4 ld_lds_16(const char *smem, int byte_off) {
+    return *reinterpret_cast<const u32x4 *>(smem + byte_off);
+}
+__device__ __forceinline__ void st_lds_16(char *smem, int byte_off, u32x4 v) {
+    *reinterpret_cast<u32x4 *>(smem + byte_off) = v;
+}
+__device__ __forceinline__ void st_lds_4(char *smem, int byte_off, uint32_t v) {
+    *reinterpret_cast<uint32_t *>(smem + byte_off) = v;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(u32x4, v); }
+
+// Swap values between lane l and lane l^32.
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// Map a linear block id to a logical work id so that consecutive logical ids
+// land on the same XCD.  Workgroups are dispatched round-robin over the 8
+// XCDs (bid % 8); tiles of one (b, h) then share that XCD's L2 for K and V.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    const int q = nblocks >> 3, r = nblocks & 7;
+    const int x = bid & 7, i = bid >> 3;
+    return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+}
+
+// ---- row-major tile with XOR-swizzled 16-byte chunks ----------------------
+// A tile of `rows` x DCH 16-byte chunks (DCH = D/8 for bf16).  Chunk c of row
+// r is stored at chunk position c ^ (r % DCH): 8 consecutive rows read at the
+// same logical chunk hit 8 distinct bank groups.
+template <int DCH>
+__device__ __forceinline__ int swz_off(int row, int chunk) {
+    return (row * DCH + (chunk ^ (row & (DCH - 1)))) * 16;
+}
+
+// ---- transposed tile ("key-major -> feature-major") -----------------------
+// T[f][key] for a 64-key tile, 128 bytes per feature row (8 chunks of 8 keys).
+// Within each 16-key group the keys are stored in MFMA-operand order so that
+// lane half g reads its 8 keys {4g..4g+3, 8+4g..8+4g+3} as one 16-byte chunk;
+// the chunk index is XOR-swizzled with (f % 8).  Returns the byte offset of
+// the 4-byte word holding keys (key, key+1), key even.
+__device__ __forceinline__ int tr64_pair_off(int f, int key) {
+    const int grp = key >> 4, kk = key & 15;
+    const int g = (kk >> 2) & 1, t = ((kk >> 3) << 2) | (kk & 3);
+    const int chunk = (grp * 2 + g) ^ (f & 7);
+    return f * 128 + chunk * 16 + t * 2;
+}
+// Byte offset of the 16-byte chunk lane-half g reads for MFMA k-step ks
+// (keys ks*16 .. ks*16+15) of feature row f.
+__device__ __forceinline__ int tr64_read_off(int f, int ks, int g) {
+    return f * 128 + (((ks * 2 + g) ^ (f & 7)) * 16);
+}
+
+}  // namespace fa

@@ -1,0 +1,90 @@
+// Kernel parameter blocks and host-side launchers (defined next to each
+// kernel).  The C ABI layer (fa_abi.cpp) validates arguments, fills these
+// blocks and calls the launchers; nothing here is exported.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+struct AttnFwdParams {
+    const void *q, *k, *v;
+    void *o;
+    float *lse;
+    const uint8_t *keep;  // [B,S] or nullptr
+    int64_t q_sb, q_ss, q_sh;
+    int64_t k_sb, k_ss, k_sh;
+    int64_t v_sb, v_ss, v_sh;
+    int64_t o_sb, o_ss, o_sh;
+    int B, S, H;
+    float scale;       // softmax scale
+    float scale_log2;  // scale * log2(e)
+};
+
+struct AttnBwdParams {
+    const void *q, *k, *v, *o, *dout;
+    const float *lse;
+    const uint8_t *keep;
+    void *dq, *dk, *dv;
+    float *delta;  // workspace: [B,H,S] rowsum(dO * O)
+    int64_t q_sb, q_ss, q_sh;
+    int64_t k_sb, k_ss, k_sh;
+    int64_t v_sb, v_ss, v_sh;
+    int64_t o_sb, o_ss, o_sh;
+    int64_t do_sb, do_ss, do_sh;
+    int64_t dq_sb, dq_ss, dq_sh;
+    int64_t dk_sb, dk_ss, dk_sh;
+    int64_t dv_sb, dv_ss, dv_sh;
+    int B, S, H;
+    float scale, scale_log2;
+};
+
+// Returns hipSuccess or the launch error.  `D` is 64 or 128.
+hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s);
+hipError_t launch_attn_fwd_f32(const AttnFwdParams &p, int D, hipStream_t s);
+hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, hipStream_t s);
+hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, hipStream_t s);
+
+// One-time per-process kernel attribute setup (dynamic LDS limits).
+hipError_t prepare_attn_kernels();
+
+struct QkPrologueParams {
+    const void *x;
+    int64_t x_sb, x_ss, x_sh;
+    const void *w, *cos, *sin;
+    void *y;
+    int64_t y_sb, y_ss, y_sh;
+    int y_off;
+    const void *dy;  // bwd only (y strides)
+    void *dx;        // bwd only
+    int64_t dx_sb, dx_ss, dx_sh;
+    int B, T, H, D;
+    float eps;
+    int n_axes;
+    int axes[8];
+};
+
+hipError_t launch_qk_prologue_fwd(const QkPrologueParams &p, int dtype, hipStream_t s);
+hipError_t launch_qk_prologue_bwd(const QkPrologueParams &p, int dtype, hipStream_t s);
+
+struct LoraParams {
+    const void *x;
+    int64_t ldx;
+    const void *a, *b;
+    float *u;
+    void *y;
+    int64_t ldy;
+    const void *dy;
+    int64_t lddy;
+    float *da, *db;
+    void *dx;
+    int64_t lddx;
+    float *work;  // bwd: [N, r] f32 (dy B)
+    int N, K, M, r;
+    float scale;
+};
+
+hipError_t launch_lora_fwd(const LoraParams &p, int dtype, hipStream_t s);
+hipError_t launch_lora_bwd(const LoraParams &p, int dtype, hipStream_t s);
+
+}  // namespace fa

@@ -1,0 +1,12 @@
+"""foundry_attn — MI355X (gfx950) attention hot path for foundry-spike.
+
+Host-side mirror of the reference's op surface over libfoundry_attn.so; see
+ops.py.  Importing this package loads nothing; the first op call loads the
+library and fails loudly if it is missing.
+"""
+from ._abi import FoundryAttnError, LIB_PATH, lib
+from .ops import (AttnBwd, attention, attn_bwd, attn_fwd, lora_bwd, lora_fwd, qk_prologue,
+                  qk_prologue_bwd, rope_tables)
+
+__all__ = ["AttnBwd", "attention", "attn_fwd", "attn_bwd", "qk_prologue", "qk_prologue_bwd",
+           "rope_tables", "lora_fwd", "lora_bwd", "FoundryAttnError", "LIB_PATH", "lib"]

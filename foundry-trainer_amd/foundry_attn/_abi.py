@@ -1,0 +1,140 @@
+"""ctypes view of include/foundry_attn.h (libfoundry_attn.so).
+
+The structures below are field-for-field copies of the C header; tests check
+that every symbol the header declares is exported.  Loading fails loudly: if
+the shared library is missing there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_PKG_DIR), "libfoundry_attn.so")
+
+FA_OK, FA_ERR_INVALID_ARG, FA_ERR_UNSUPPORTED, FA_ERR_NO_DEVICE, FA_ERR_LOAD_FAILED, FA_ERR_HIP = range(6)
+STATUS_NAMES = {0: "OK", 1: "INVALID_ARG", 2: "UNSUPPORTED", 3: "NO_DEVICE", 4: "LOAD_FAILED",
+                5: "HIP_ERROR"}
+FA_DTYPE_BF16, FA_DTYPE_F32 = 0, 1
+FA_MAX_ROPE_AXES = 8
+
+EXPORTED = [
+    "fa_version", "fa_last_error", "fa_op_name", "fa_init",
+    "fa_attn_fwd", "fa_attn_bwd_workspace_size", "fa_attn_bwd",
+    "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
+    "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
+]
+
+
+class FoundryAttnError(RuntimeError):
+    """A non-OK fa_status, with the library's thread-local message."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+
+
+class Strides(ctypes.Structure):
+    _fields_ = [("b", ctypes.c_int64), ("s", ctypes.c_int64), ("h", ctypes.c_int64)]
+
+
+class AttnFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("seq", ctypes.c_int32),
+        ("heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p), ("key_keep", ctypes.c_void_p),
+        ("q_stride", Strides), ("k_stride", Strides), ("v_stride", Strides), ("o_stride", Strides),
+    ]
+
+
+class AttnBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("seq", ctypes.c_int32),
+        ("heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("dout", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("key_keep", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dv", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("q_stride", Strides), ("k_stride", Strides), ("v_stride", Strides), ("o_stride", Strides),
+        ("do_stride", Strides), ("dq_stride", Strides), ("dk_stride", Strides),
+        ("dv_stride", Strides),
+    ]
+
+
+class QkPrologueArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("batch", ctypes.c_int32), ("tokens", ctypes.c_int32),
+        ("heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("eps", ctypes.c_float),
+        ("x", ctypes.c_void_p), ("x_stride", Strides),
+        ("weight", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+        ("n_axes", ctypes.c_int32), ("axes", ctypes.c_int32 * FA_MAX_ROPE_AXES),
+        ("y", ctypes.c_void_p), ("y_stride", Strides), ("y_seq_offset", ctypes.c_int32),
+    ]
+
+
+class QkPrologueBwdArgs(ctypes.Structure):
+    _fields_ = [("fwd", QkPrologueArgs), ("dy", ctypes.c_void_p), ("dx", ctypes.c_void_p),
+                ("dx_stride", Strides)]
+
+
+class LoraArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("tokens", ctypes.c_int32), ("in_features", ctypes.c_int32),
+        ("out_features", ctypes.c_int32), ("rank", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("x", ctypes.c_void_p), ("ldx", ctypes.c_int64), ("a", ctypes.c_void_p),
+        ("b", ctypes.c_void_p), ("u", ctypes.c_void_p), ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+    ]
+
+
+class LoraBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", LoraArgs), ("dy", ctypes.c_void_p), ("ldy", ctypes.c_int64),
+        ("da", ctypes.c_void_p), ("db", ctypes.c_void_p), ("dx", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libfoundry_attn.so (built by `make -C foundry-trainer_amd`)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FoundryAttnError(FA_ERR_LOAD_FAILED,
+                               f"{LIB_PATH} is missing; build it with __graft_entry__.build() "
+                               "or `make -C foundry-trainer_amd`")
+    L = ctypes.CDLL(LIB_PATH)
+    L.fa_version.restype = ctypes.c_int
+    L.fa_last_error.restype = ctypes.c_char_p
+    L.fa_op_name.restype = ctypes.c_char_p
+    L.fa_init.restype = ctypes.c_int
+    L.fa_init.argtypes = [ctypes.c_int]
+    for name, st in (("fa_attn_fwd", AttnFwdArgs), ("fa_attn_bwd", AttnBwdArgs),
+                     ("fa_qk_prologue_fwd", QkPrologueArgs),
+                     ("fa_qk_prologue_bwd", QkPrologueBwdArgs),
+                     ("fa_lora_fwd", LoraArgs), ("fa_lora_bwd", LoraBwdArgs)):
+        fn = getattr(L, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+    L.fa_attn_bwd_workspace_size.restype = ctypes.c_size_t
+    L.fa_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnBwdArgs)]
+    L.fa_lora_bwd_workspace_size.restype = ctypes.c_size_t
+    L.fa_lora_bwd_workspace_size.argtypes = [ctypes.POINTER(LoraBwdArgs)]
+    L.fa_rope_tables_host.restype = ctypes.c_int
+    L.fa_rope_tables_host.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                      ctypes.c_void_p, ctypes.c_float, ctypes.c_int32,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    _lib = L
+    return L
+
+
+def check(status: int) -> None:
+    if status != FA_OK:
+        raise FoundryAttnError(status, lib().fa_last_error().decode(errors="replace"))

@@ -1,0 +1,229 @@
+/*
+ * foundry_attn.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in boundary for erikerikerik/foundry-trainer's `foundry-spike` crate:
+ * the Candle `CustomOp3` `AttnBwd` (crates/foundry-spike/src/lib.rs:151-264)
+ * and the memory-bound ops around it (rms_norm lib.rs:45-58, rope_tables_dtype
+ * lib.rs:77-105, apply_rope lib.rs:122-129, linear_scaled lib.rs:270-287).
+ * Each entry point below names the reference interface it replaces.
+ *
+ * Conventions
+ *   - Every device buffer is owned by the caller; nothing on the hot path
+ *     allocates.  Scratch memory comes in through a caller workspace.
+ *   - Launches go on the caller's HIP stream (`stream`, a hipStream_t, NULL =
+ *     the null stream) and are asynchronous.
+ *   - Attention tensors are [B, S, H, D] views given by element strides for
+ *     b, s and h; the head-dim stride is 1.  B = 1 with contiguous strides is
+ *     the reference's per-sample (S, H, D) layout.  Base pointers and strides
+ *     must keep every row 16-byte aligned.
+ *   - The joint sequence is txt first, then img (lib.rs:363-365).
+ *   - No exception or C++ type crosses this boundary.  On failure a call
+ *     returns a non-zero fa_status and fa_last_error() (thread-local) says why.
+ *     Arguments are validated before any device work.
+ *   - Calls on distinct streams may run concurrently.
+ */
+#ifndef FOUNDRY_ATTN_H
+#define FOUNDRY_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+typedef enum fa_status {
+    FA_OK = 0,
+    FA_ERR_INVALID_ARG = 1, /* bad shape, stride, pointer, scale or workspace      */
+    FA_ERR_UNSUPPORTED = 2, /* valid request this build does not implement          */
+    FA_ERR_NO_DEVICE = 3,   /* no HIP device visible                                */
+    FA_ERR_LOAD_FAILED = 4, /* device is not gfx950 / code object cannot be used    */
+    FA_ERR_HIP = 5          /* a HIP runtime call or kernel launch failed           */
+} fa_status;
+
+typedef enum fa_dtype {
+    FA_DTYPE_BF16 = 0, /* bf16 storage, f32 arithmetic and accumulation */
+    FA_DTYPE_F32 = 1   /* f32 storage and arithmetic (the reference's CPU dtype) */
+} fa_dtype;
+
+/* Element strides of a [B, S, H, D] view; the D stride is 1. */
+typedef struct fa_strides {
+    int64_t b, s, h;
+} fa_strides;
+
+/* ------------------------------------------------------------------------- */
+/* Library                                                                   */
+/* ------------------------------------------------------------------------- */
+
+/* ABI version (FA_ABI_VERSION). */
+int fa_version(void);
+
+/* Reason for the last failure on this thread ("" if none). */
+const char *fa_last_error(void);
+
+/* Name of the op, as CustomOp3::name returns it (lib.rs:154-156):
+ * "foundry-attn-bwd". */
+const char *fa_op_name(void);
+
+/* Checks that `device` is a gfx950 GPU and prepares the kernels for it
+ * (LDS limits).  Idempotent and thread-safe; the attention entry points call
+ * it for the current device on first use.  Replaces the CUDA device/NVRTC
+ * setup the reference does through cudarc (src/main.rs:16-38). */
+fa_status fa_init(int device);
+
+/* ------------------------------------------------------------------------- */
+/* Attention (AttnBwd)                                                       */
+/* ------------------------------------------------------------------------- */
+
+typedef struct fa_attn_fwd_args {
+    int32_t dtype;           /* fa_dtype of q, k, v and o                          */
+    int32_t batch;           /* B >= 1                                            */
+    int32_t seq;             /* S >= 1 (queries and keys: joint self-attention)   */
+    int32_t heads;           /* H >= 1                                            */
+    int32_t head_dim;        /* D: 64 or 128                                      */
+    float scale;             /* softmax scale, finite and > 0; the reference
+                                hard-codes 1/sqrt(128) (lib.rs:138)               */
+    const void *q, *k, *v;   /* [B,S,H,D]                                         */
+    void *o;                 /* [B,S,H,D] output                                  */
+    float *lse;              /* [B,H,S] contiguous f32 output: natural-log
+                                logsumexp of the scaled scores of each query row;
+                                -inf for a row whose keys are all masked          */
+    const uint8_t *key_keep; /* NULL (no mask) or [B,S] contiguous: 0 = key is
+                                excluded from every row's softmax                 */
+    fa_strides q_stride, k_stride, v_stride, o_stride;
+} fa_attn_fwd_args;
+
+/* O = softmax(Q K^T * scale) V per (b, h), scores and softmax in f32, P cast to
+ * the storage dtype before P V (lib.rs:131-149), plus the per-row LSE that the
+ * backward uses to recompute P.  A fully masked row gives O = 0, LSE = -inf.
+ * Replaces AttnBwd::cuda_fwd (lib.rs:189-214) and AttnBwd::cpu_fwd
+ * (lib.rs:158-187). */
+fa_status fa_attn_fwd(const fa_attn_fwd_args *args, void *stream);
+
+typedef struct fa_attn_bwd_args {
+    int32_t dtype, batch, seq, heads, head_dim; /* as in fa_attn_fwd_args        */
+    float scale;                                /* the forward's scale           */
+    const void *q, *k, *v;                      /* forward inputs                */
+    const void *o;                              /* forward output (`res`)        */
+    const void *dout;                           /* upstream gradient dL/dO       */
+    const float *lse;                           /* forward LSE [B,H,S]           */
+    const uint8_t *key_keep;                    /* the forward's mask or NULL    */
+    void *dq, *dk, *dv;                         /* [B,S,H,D] outputs             */
+    void *workspace;                            /* device scratch, 256-B aligned */
+    size_t workspace_bytes;                     /* >= fa_attn_bwd_workspace_size */
+    fa_strides q_stride, k_stride, v_stride, o_stride, do_stride;
+    fa_strides dq_stride, dk_stride, dv_stride;
+} fa_attn_bwd_args;
+
+/* Bytes of workspace fa_attn_bwd needs for these shapes (0 on bad args). */
+size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
+
+/* dQ, dK, dV of the forward above: P is recomputed from Q, K and the saved
+ * LSE; dS = P * (dP - rowsum(dO * O)) * scale; dQ = dS K, dK = dS^T Q,
+ * dV = P^T dO, f32 accumulation, deterministic (no atomics).
+ * Replaces AttnBwd::bwd (lib.rs:216-263). */
+fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* QK prologue: RMSNorm -> axial RoPE -> joint buffer                        */
+/* ------------------------------------------------------------------------- */
+
+#define FA_MAX_ROPE_AXES 8
+
+typedef struct fa_qk_prologue_args {
+    int32_t dtype;          /* fa_dtype of x, y, weight, cos, sin             */
+    int32_t batch;          /* B                                              */
+    int32_t tokens;         /* tokens of this stream (txt or img)             */
+    int32_t heads;          /* H                                              */
+    int32_t head_dim;       /* D: 64 or 128, == sum(axes)                     */
+    float eps;              /* RMSNorm epsilon (reference: 1e-6, lib.rs:26)   */
+    const void *x;          /* [B,tokens,H,D] view: q or k linear output      */
+    fa_strides x_stride;
+    const void *weight;     /* [D] learned RMSNorm scale                      */
+    const void *cos, *sin;  /* [tokens, D] tables, contiguous                 */
+    int32_t n_axes;         /* rotate-half segments, 1..FA_MAX_ROPE_AXES      */
+    int32_t axes[FA_MAX_ROPE_AXES]; /* even widths summing to D               */
+    void *y;                /* joint [B,S,H,D] buffer                         */
+    fa_strides y_stride;
+    int32_t y_seq_offset;   /* first joint row this stream writes (txt: 0,
+                               img: txt_len)                                  */
+} fa_qk_prologue_args;
+
+/* y[:, off:off+tokens] = apply_rope(rms_norm(x, weight, eps), cos, sin), with
+ * the reference's cast points (stats f32; normalised value cast to dtype, then
+ * * weight in dtype; rotation in f32, cast back).  Fuses lib.rs:45-58,
+ * lib.rs:122-129 and the txt||img concatenation lib.rs:363-365. */
+fa_status fa_qk_prologue_fwd(const fa_qk_prologue_args *args, void *stream);
+
+typedef struct fa_qk_prologue_bwd_args {
+    fa_qk_prologue_args fwd; /* the forward's arguments (x, weight, tables)    */
+    const void *dy;          /* gradient wrt the joint buffer, fwd.y_stride,
+                                read at rows fwd.y_seq_offset..+tokens        */
+    void *dx;                /* [B,tokens,H,D] output, dx_stride              */
+    fa_strides dx_stride;
+} fa_qk_prologue_bwd_args;
+
+/* dx of the fused prologue (chain rule through RoPE then RMSNorm, f32).
+ * The norm weight is frozen, so no weight gradient is produced. */
+fa_status fa_qk_prologue_bwd(const fa_qk_prologue_bwd_args *args, void *stream);
+
+/* Host helper: RoPE tables exactly as rope_tables_dtype (lib.rs:77-105):
+ * inv_j = theta^(-2j/d_a), f = pos[a]*inv_j in f32, cos/sin duplicated per
+ * axis segment, then cast to `dtype` (bf16 tables are written as uint16 bf16
+ * bits).  positions: [n_pos, n_axes] host f32; cos_out/sin_out: host buffers
+ * of n_pos * sum(axes) elements of `dtype`.  No device work. */
+fa_status fa_rope_tables_host(const float *positions, int32_t n_pos, int32_t n_axes,
+                              const int32_t *axes, float theta, int32_t dtype, void *cos_out,
+                              void *sin_out);
+
+/* ------------------------------------------------------------------------- */
+/* LoRA down/up (linear_scaled's adapter term)                               */
+/* ------------------------------------------------------------------------- */
+
+typedef struct fa_lora_args {
+    int32_t dtype;        /* fa_dtype of x, a, b, y, dy, dx                    */
+    int32_t tokens;       /* N rows of x and y                                 */
+    int32_t in_features;  /* K                                                 */
+    int32_t out_features; /* M                                                 */
+    int32_t rank;         /* r: 1..32                                          */
+    float scale;          /* alpha / r (reference fixture 2.0, harness 1.0)    */
+    const void *x;        /* [N, K] rows of stride ldx                         */
+    int64_t ldx;
+    const void *a;        /* [r, K] contiguous (LoRA down, `lora_a`)           */
+    const void *b;        /* [M, r] contiguous (LoRA up, `lora_b`)             */
+    float *u;             /* [N, r] f32: x A^T (written by fwd, read by bwd)   */
+    void *y;              /* [N, M] rows of stride ldy (fwd: in/out)           */
+    int64_t ldy;
+} fa_lora_args;
+
+/* y += scale * (x A^T) B^T, with u = x A^T kept in f32 for the backward.
+ * y holds the base linear x W^T (+ bias) on entry.  Replaces the adapter
+ * term of linear_scaled (lib.rs:280-285). */
+fa_status fa_lora_fwd(const fa_lora_args *args, void *stream);
+
+typedef struct fa_lora_bwd_args {
+    fa_lora_args fwd;  /* the forward's arguments (x, a, b, u; y unused)       */
+    const void *dy;    /* [N, M] rows of stride ldy                            */
+    int64_t ldy;
+    float *da;         /* [r, K] f32 output: scale * (dy B)^T x                */
+    float *db;         /* [M, r] f32 output: scale * dy^T u                    */
+    void *dx;          /* NULL, or [N, K] rows of stride ldx: dx += scale *
+                          (dy B) A (the adapter's share of the input grad)     */
+    int64_t ldx;
+    void *workspace;   /* device scratch, 256-B aligned                        */
+    size_t workspace_bytes;
+} fa_lora_bwd_args;
+
+size_t fa_lora_bwd_workspace_size(const fa_lora_bwd_args *args);
+
+/* LoRA gradients of linear_scaled's adapter term (Candle autograd through
+ * lib.rs:280-285): dB = s dy^T u, dA = s (dy B)^T x, optional dx += s (dy B) A.
+ * Deterministic. */
+fa_status fa_lora_bwd(const fa_lora_bwd_args *args, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FOUNDRY_ATTN_H */

@@ -1,0 +1,168 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, validates arguments before any device work, and reports
+NO_DEVICE cleanly where no GPU is visible.  No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, gpu_available
+from foundry_attn import _abi
+from foundry_attn._abi import lib
+
+HEADER = os.path.join(ROOT, "include", "foundry_attn.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib()
+    declared = header_functions()
+    assert set(declared) == set(_abi.EXPORTED), declared
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_version_and_name():
+    assert lib().fa_version() == 1
+    # CustomOp3::name of the reference op (lib.rs:154-156)
+    assert lib().fa_op_name() == b"foundry-attn-bwd"
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """Compile the header with gcc and compare every field offset and struct
+    size with the ctypes mirrors."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    structs = {"fa_strides": _abi.Strides, "fa_attn_fwd_args": _abi.AttnFwdArgs,
+               "fa_attn_bwd_args": _abi.AttnBwdArgs, "fa_qk_prologue_args": _abi.QkPrologueArgs,
+               "fa_qk_prologue_bwd_args": _abi.QkPrologueBwdArgs, "fa_lora_args": _abi.LoraArgs,
+               "fa_lora_bwd_args": _abi.LoraBwdArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    for line in out.splitlines():
+        cname, what, val = line.split()
+        py = structs[cname]
+        want = ctypes.sizeof(py) if what == "size" else getattr(py, what).offset
+        assert int(val) == want, (cname, what, val, want)
+
+
+def _fwd_args(**kw):
+    fake = 1 << 20  # aligned non-null placeholder; validation fails before any use
+    a = _abi.AttnFwdArgs(dtype=0, batch=1, seq=128, heads=2, head_dim=128, scale=0.088,
+                         q=fake, k=fake, v=fake, o=fake, lse=fake,
+                         q_stride=_abi.Strides(128 * 256, 256, 128),
+                         k_stride=_abi.Strides(128 * 256, 256, 128),
+                         v_stride=_abi.Strides(128 * 256, 256, 128),
+                         o_stride=_abi.Strides(128 * 256, 256, 128))
+    for k_, v_ in kw.items():
+        setattr(a, k_, v_)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 96, _abi.FA_ERR_UNSUPPORTED),
+    ("head_dim", 0, _abi.FA_ERR_UNSUPPORTED),
+    ("seq", 0, _abi.FA_ERR_INVALID_ARG),
+    ("batch", -1, _abi.FA_ERR_INVALID_ARG),
+    ("scale", 0.0, _abi.FA_ERR_INVALID_ARG),
+    ("scale", float("nan"), _abi.FA_ERR_INVALID_ARG),
+    ("dtype", 7, _abi.FA_ERR_INVALID_ARG),
+    ("q", None, _abi.FA_ERR_INVALID_ARG),
+    ("lse", None, _abi.FA_ERR_INVALID_ARG),
+    ("k", (1 << 20) + 2, _abi.FA_ERR_INVALID_ARG),          # misaligned bf16 base
+    ("q_stride", _abi.Strides(8, 252, 128), _abi.FA_ERR_INVALID_ARG),  # not 16-B rows
+])
+def test_fwd_validation_errors(field, value, code):
+    a = _fwd_args(**{field: value})
+    assert lib().fa_attn_fwd(ctypes.byref(a), None) == code
+    assert len(lib().fa_last_error()) > 0
+
+
+def test_null_args_pointer():
+    assert lib().fa_attn_fwd(None, None) == _abi.FA_ERR_INVALID_ARG
+    assert lib().fa_attn_bwd(None, None) == _abi.FA_ERR_INVALID_ARG
+
+
+def test_bwd_workspace_size_and_validation():
+    fake = 1 << 20
+    st = _abi.Strides(128 * 256, 256, 128)
+    a = _abi.AttnBwdArgs(dtype=0, batch=2, seq=100, heads=3, head_dim=128, scale=0.1,
+                         q=fake, k=fake, v=fake, o=fake, dout=fake, lse=fake, dq=fake, dk=fake,
+                         dv=fake, q_stride=st, k_stride=st, v_stride=st, o_stride=st,
+                         do_stride=st, dq_stride=st, dk_stride=st, dv_stride=st)
+    need = lib().fa_attn_bwd_workspace_size(ctypes.byref(a))
+    assert need >= 2 * 3 * 100 * 4 and need % 256 == 0
+    a.workspace, a.workspace_bytes = fake, need - 256
+    assert lib().fa_attn_bwd(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
+    assert b"workspace" in lib().fa_last_error()
+
+
+@pytest.mark.skipif(gpu_available(), reason="checks the GPU-less error path")
+def test_valid_call_without_device_reports_no_device():
+    a = _fwd_args()
+    assert lib().fa_attn_fwd(ctypes.byref(a), None) == _abi.FA_ERR_NO_DEVICE
+    assert lib().fa_init(0) == _abi.FA_ERR_NO_DEVICE
+
+
+def test_prologue_validation():
+    fake = 1 << 20
+    st = _abi.Strides(0, 3072, 128)
+    ax = (ctypes.c_int32 * 8)(16, 56, 50, 0, 0, 0, 0, 0)
+    a = _abi.QkPrologueArgs(dtype=0, batch=1, tokens=4, heads=24, head_dim=128, eps=1e-6, x=fake,
+                            x_stride=st, weight=fake, cos=fake, sin=fake, n_axes=3, axes=ax,
+                            y=fake, y_stride=st, y_seq_offset=0)
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
+    assert b"sum" in lib().fa_last_error()
+    a.axes[2] = 55  # odd width
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
+
+
+def test_lora_validation():
+    fake = 1 << 20
+    a = _abi.LoraArgs(dtype=0, tokens=8, in_features=3072, out_features=9216, rank=64, scale=1.0,
+                      x=fake, ldx=3072, a=fake, b=fake, u=fake, y=fake, ldy=9216)
+    assert lib().fa_lora_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+    a.rank = 16
+    a.in_features = 3000  # not a multiple of 16
+    assert lib().fa_lora_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_rope_tables_host_matches_oracle(bf16):
+    """fa_rope_tables_host is host code: it runs here and must equal the
+    oracle's rope_tables_dtype restatement bit for bit."""
+    import oracle
+    from foundry_attn.configs import C2
+    pos = np.ascontiguousarray(C2.positions()[::37])
+    n = pos.shape[0]
+    code = _abi.FA_DTYPE_BF16 if bf16 else _abi.FA_DTYPE_F32
+    dt = np.uint16 if bf16 else np.float32
+    cos = np.empty((n, 128), dt)
+    sin = np.empty((n, 128), dt)
+    ax = (ctypes.c_int32 * 3)(16, 56, 56)
+    assert lib().fa_rope_tables_host(pos.ctypes.data, n, 3, ctypes.addressof(ax), 1e4, code,
+                                     cos.ctypes.data, sin.ctypes.data) == 0
+    if bf16:
+        cos = (cos.astype(np.uint32) << 16).view(np.float32)
+        sin = (sin.astype(np.uint32) << 16).view(np.float32)
+    oc, os_ = oracle.rope_tables(pos, [16, 56, 56], 1e4, bf16=bf16)
+    np.testing.assert_array_equal(cos, oc)
+    np.testing.assert_array_equal(sin, os_)

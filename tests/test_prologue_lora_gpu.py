@@ -1,0 +1,151 @@
+"""GPU parity of the fused QK prologue and the LoRA kernels (through the C
+ABI) against the oracle and the reference's fixtures."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from foundry_attn import lora_bwd, lora_fwd, qk_prologue, qk_prologue_bwd, rope_tables
+from foundry_attn.configs import C2
+from helpers import BF16_MAX_ABS, BF16_REL_L2, load_golden, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device="cuda", dtype=dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prologue_fwd_joint_buffer_matches_oracle(dtype):
+    """c2 shapes: txt stream (512 tokens) at joint offset 0 and img stream
+    (64x64) at offset 512, each RMSNormed and roped into one joint buffer."""
+    bf = dtype == "bf16"
+    tdt = torch.bfloat16 if bf else torch.float32
+    rng = np.random.default_rng(4)
+    H, D, T_txt = C2.heads, C2.head_dim, C2.txt_len
+    T_img = C2.seq - T_txt
+    rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
+    xt = rnd(rng.standard_normal((1, T_txt, H, D)).astype(np.float32))
+    xi = rnd(rng.standard_normal((1, T_img, H, D)).astype(np.float32) * 3)
+    w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    pos = C2.positions()
+    cos, sin = oracle.rope_tables(pos, C2.axes, C2.theta, bf16=bf)
+    want = np.concatenate(
+        [oracle.apply_rope(oracle.rms_norm(xt[0], w, bf16=bf), cos[:T_txt], sin[:T_txt], C2.axes, bf16=bf),
+         oracle.apply_rope(oracle.rms_norm(xi[0], w, bf16=bf), cos[T_txt:], sin[T_txt:], C2.axes, bf16=bf)])
+    tc, ts = rope_tables(pos, C2.axes, C2.theta, dtype=tdt)
+    assert np.array_equal(host(tc), cos) and np.array_equal(host(ts), sin)
+    joint = torch.empty((1, C2.seq, H, D), dtype=tdt, device="cuda")
+    tw = dev(w, tdt)
+    qk_prologue(dev(xt, tdt), tw, tc[:T_txt].contiguous(), ts[:T_txt].contiguous(), C2.axes,
+                out=joint, seq_offset=0)
+    qk_prologue(dev(xi, tdt), tw, tc[T_txt:].contiguous(), ts[T_txt:].contiguous(), C2.axes,
+                out=joint, seq_offset=T_txt)
+    got = host(joint)[0]
+    if bf:
+        # same cast points as the reference; stats summed in another order can
+        # move a value by one bf16 ulp
+        ulp = np.abs(want) * 2.0 ** -7 + 1e-30
+        assert np.mean(got != want) < 1e-3
+        assert np.all(np.abs(got - want) <= ulp)
+        assert max_abs(got, want) <= BF16_MAX_ABS and rel_l2(got, want) <= 1e-3
+    else:
+        assert rel_l2(got, want) <= 1e-6
+
+
+def test_prologue_fixture_replay():
+    """double.q of the reference fixture: linear (oracle, host) -> fused
+    RMSNorm + RoPE kernel, bf16 and fp32."""
+    axes = [32, 32, 32, 32]
+    rows, cols = np.arange(16) // 4, np.arange(16) % 4
+    z = np.zeros(16)
+    pos = np.stack([rows, cols, z, z], -1).astype(np.float32)
+    for tag, tdt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        f = load_golden(tag)
+        bf = tag == "bf16"
+        W = lambda p: f.get(f"weights/double.img.to_q.{p}")
+        h = oracle.linear_lora(f["double.img_norm1"], W("weight"), W("bias"), W("lora_a"),
+                               W("lora_b"), scale=2.0, bf16=bf).reshape(1, 16, 2, 128)
+        tc, ts = rope_tables(pos, axes, 1e4, dtype=tdt)
+        y = qk_prologue(dev(h, tdt), dev(f["weights/double.img_q_norm.weight"], tdt), tc, ts, axes)
+        rl = rel_l2(host(y)[0], f["double.q"])
+        print(f"  {tag}: rel_l2={rl:.3e}", flush=True)
+        assert rl <= (1e-6 if not bf else 2e-3)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prologue_bwd_matches_oracle(dtype):
+    bf = dtype == "bf16"
+    tdt = torch.bfloat16 if bf else torch.float32
+    rng = np.random.default_rng(8)
+    T, H, D = 300, 4, 128
+    rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
+    x = rnd(rng.standard_normal((T, H, D)).astype(np.float32))
+    w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    pos = np.stack([np.zeros(T), np.arange(T) // 20, np.arange(T) % 20], -1).astype(np.float32)
+    axes = [16, 56, 56]
+    cos, sin = oracle.rope_tables(pos, axes, 1e4, bf16=bf)
+    dy_joint = rnd(rng.standard_normal((1, T + 50, H, D)).astype(np.float32))
+    want = oracle.qk_prologue_bwd(x, w, cos, sin, dy_joint[0, 50:], axes)
+    dx = qk_prologue_bwd(dev(x, tdt), dev(w, tdt), dev(cos, tdt), dev(sin, tdt), axes,
+                         dev(dy_joint, tdt), seq_offset=50)
+    got = host(dx)
+    if bf:
+        assert max_abs(got, want) <= BF16_MAX_ABS and rel_l2(got, want) <= BF16_REL_L2
+    else:
+        assert rel_l2(got, want) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_lora_fwd_bwd_match_oracle(dtype):
+    bf = dtype == "bf16"
+    tdt = torch.bfloat16 if bf else torch.float32
+    rng = np.random.default_rng(3)
+    N, K, M, r, s = 600, 256, 384, 16, 1.0
+    rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
+    x = rnd(rng.standard_normal((N, K)).astype(np.float32))
+    Wb = rnd(0.02 * rng.standard_normal((M, K)).astype(np.float32))
+    A = rnd(rng.standard_normal((r, K)).astype(np.float32) / r)
+    B = rnd(0.05 * rng.standard_normal((M, r)).astype(np.float32))
+    dy = rnd(rng.standard_normal((N, M)).astype(np.float32))
+    base = oracle.linear_lora(x, Wb, bf16=bf)
+    want = oracle.linear_lora(x, Wb, None, A, B, scale=s, bf16=bf)
+    y = dev(base, tdt)
+    u = lora_fwd(dev(x, tdt), dev(A, tdt), dev(B, tdt), y, s)
+    got = host(y)
+    if bf:
+        assert max_abs(got, want) <= BF16_MAX_ABS and rel_l2(got, want) <= BF16_REL_L2
+    else:
+        assert rel_l2(got, want) <= 1e-5
+    np.testing.assert_allclose(host(u), x.astype(np.float64) @ A.T.astype(np.float64),
+                               rtol=1e-4, atol=1e-3)
+    dx_base = np.zeros((N, K), np.float32)
+    dx = dev(dx_base, tdt)
+    dA, dB = lora_bwd(dev(x, tdt), dev(A, tdt), dev(B, tdt), u, dev(dy, tdt), s, dx=dx)
+    _, wA, wB = oracle.linear_lora_bwd(x, Wb, A, B, dy, scale=s, bf16=False, want_dx=False)
+    # adapter share of dx: s * (dy B) A
+    want_dx = (s * (dy.astype(np.float64) @ B) @ A).astype(np.float32)
+    tol = 1e-2 if bf else 1e-5
+    assert rel_l2(host(dA), wA) <= tol and rel_l2(host(dB), wB) <= tol
+    assert rel_l2(host(dx), want_dx) <= tol
+
+
+def test_lora_grads_fixture_replay():
+    """LoRA dA/dB of double.img.to_v from the reference fixture (PyTorch
+    autograd), seeded with the fixture's dL/dv (fp32)."""
+    f = load_golden("fp32")
+    x = f["double.img_norm1"]
+    W = lambda p: f[f"weights/double.img.to_v.{p}"]
+    dy = f["grad/attn/double.v"][8:].reshape(16, 256)
+    y = dev(np.zeros((16, 256), np.float32), torch.float32)
+    u = lora_fwd(dev(x, torch.float32), dev(W("lora_a"), torch.float32),
+                 dev(W("lora_b"), torch.float32), y, 2.0)
+    dA, dB = lora_bwd(dev(x, torch.float32), dev(W("lora_a"), torch.float32),
+                      dev(W("lora_b"), torch.float32), u, dev(dy, torch.float32), 2.0)
+    assert rel_l2(host(dA), f["grad/double.img.to_v.lora_a"]) <= 1e-5
+    assert rel_l2(host(dB), f["grad/double.img.to_v.lora_b"]) <= 1e-5
