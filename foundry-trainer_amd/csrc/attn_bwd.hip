@@ -55,9 +55,11 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(AttnBwdParams p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)c[e];
         } else {
+            // bit-cast the whole vector: a bit cast of a vector-element lvalue
+            // (ov[e]) reads element 0 whatever e is
+            const f32x4 a = __builtin_bit_cast(f32x4, ov), c = __builtin_bit_cast(f32x4, dv);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                acc += __builtin_bit_cast(float, ov[e]) * __builtin_bit_cast(float, dv[e]);
+            for (int e = 0; e < 4; ++e) acc += a[e] * c[e];
         }
     }
 #pragma unroll
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p
             u32x4 rq[Tile64<D>::PAIR_LOADS], rd[Tile64<D>::PAIR_LOADS];
             tile_load_pairs<D>(rq, qbase, p.q_ss, q0, S, tid);
             tile_load_pairs<D>(rd, dobase, p.do_ss, q0, S, tid);
-            float lv = 0.f, dlt = 0.f;
+            float lv = INFINITY, dlt = 0.f;  // rows past S contribute P = 0
             if (tid < kQB && q0 + tid < S) {
                 const float l = lse[q0 + tid];
                 // a row with every key masked has LSE = -inf and P = 0

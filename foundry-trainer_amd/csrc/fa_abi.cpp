@@ -77,22 +77,21 @@ bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 const char *dtype_name(int32_t dt) { return dt == FA_DTYPE_BF16 ? "bf16" : "f32"; }
 
-// Checks a [B,S,H,D] view: non-null, non-negative strides, and alignment so
-// that every row start is 16-byte aligned for bf16 (vector loads) and 4-byte
-// aligned for f32.
+// Checks a [B,S,H,D] view: non-null, non-negative strides, and every row
+// start 16-byte aligned (the kernels move rows with 16-byte vector loads):
+// base pointer 16-byte aligned, strides multiples of 8 (bf16) or 4 (f32)
+// elements.
 fa_status check_view(const char *name, const void *ptr, const fa_strides &st, int32_t dtype) {
     if (!ptr) return fail(FA_ERR_INVALID_ARG, "%s is NULL", name);
     if (st.b < 0 || st.s < 0 || st.h < 0)
         return fail(FA_ERR_INVALID_ARG, "%s has a negative stride", name);
-    if (dtype == FA_DTYPE_BF16) {
-        if (!aligned(ptr, 16)) return fail(FA_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
-        if ((st.b | st.s | st.h) % 8)
-            return fail(FA_ERR_INVALID_ARG,
-                        "%s strides (%lld,%lld,%lld) must be multiples of 8 elements (bf16)", name,
-                        (long long)st.b, (long long)st.s, (long long)st.h);
-    } else if (!aligned(ptr, 4)) {
-        return fail(FA_ERR_INVALID_ARG, "%s is not 4-byte aligned", name);
-    }
+    const int64_t mult = dtype == FA_DTYPE_BF16 ? 8 : 4;
+    if (!aligned(ptr, 16)) return fail(FA_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
+    if (st.b % mult || st.s % mult || st.h % mult)
+        return fail(FA_ERR_INVALID_ARG,
+                    "%s strides (%lld,%lld,%lld) must be multiples of %lld elements (%s)", name,
+                    (long long)st.b, (long long)st.s, (long long)st.h, (long long)mult,
+                    dtype_name(dtype));
     return FA_OK;
 }
 
@@ -249,10 +248,6 @@ static fa_status check_prologue(const fa_qk_prologue_args *a) {
     if (!a->weight || !aligned(a->weight, elt)) return fail(FA_ERR_INVALID_ARG, "weight is NULL or misaligned");
     if (!a->cos || !a->sin || !aligned(a->cos, elt) || !aligned(a->sin, elt))
         return fail(FA_ERR_INVALID_ARG, "cos/sin table is NULL or misaligned");
-    if (a->dtype == FA_DTYPE_F32 && ((a->x_stride.b | a->x_stride.s | a->x_stride.h |
-                                      a->y_stride.b | a->y_stride.s | a->y_stride.h) % 4 ||
-                                     !aligned(a->x, 16) || !aligned(a->y, 16)))
-        return fail(FA_ERR_INVALID_ARG, "f32 prologue rows must be 16-byte aligned");
     return FA_OK;
 }
 
@@ -313,10 +308,6 @@ fa_status fa_qk_prologue_bwd(const fa_qk_prologue_bwd_args *a, void *stream) {
     FA_TRY(check_prologue(&a->fwd));
     FA_TRY(check_view("dy", a->dy, a->fwd.y_stride, a->fwd.dtype));
     FA_TRY(check_view("dx", a->dx, a->dx_stride, a->fwd.dtype));
-    if (a->fwd.dtype == FA_DTYPE_F32 &&
-        ((a->dx_stride.b | a->dx_stride.s | a->dx_stride.h) % 4 || !aligned(a->dx, 16) ||
-         !aligned(a->dy, 16)))
-        return fail(FA_ERR_INVALID_ARG, "f32 prologue rows must be 16-byte aligned");
     FA_TRY(init_current());
     fa::QkPrologueParams p{};
     fill_prologue(&a->fwd, p);

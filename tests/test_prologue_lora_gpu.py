@@ -48,11 +48,12 @@ def test_prologue_fwd_joint_buffer_matches_oracle(dtype):
                 out=joint, seq_offset=T_txt)
     got = host(joint)[0]
     if bf:
-        # same cast points as the reference; stats summed in another order can
-        # move a value by one bf16 ulp
-        ulp = np.abs(want) * 2.0 ** -7 + 1e-30
+        # same cast points as the reference; the RMS statistic summed in another
+        # order can move a normalised input by one bf16 ulp, which moves the
+        # rotated output by at most ~2 ulp of the row's largest input
+        row_max = np.abs(want).max(-1, keepdims=True)
         assert np.mean(got != want) < 1e-3
-        assert np.all(np.abs(got - want) <= ulp)
+        assert np.all(np.abs(got - want) <= row_max * 2.0 ** -6)
         assert max_abs(got, want) <= BF16_MAX_ABS and rel_l2(got, want) <= 1e-3
     else:
         assert rel_l2(got, want) <= 1e-6
