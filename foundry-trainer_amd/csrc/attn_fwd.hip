@@ -13,59 +13,48 @@
 //     operand) stays in registers for the whole kernel.  In the S^T
 //     accumulator every lane holds 16 keys of ONE query (lane % 32), so the
 //     row max / row sum need a single cross-lane step (lane ^ 32).
-//   - O^T = V^T P^T is the second MFMA: V^T (A operand) comes from a
-//     transposed LDS tile, P^T (B operand) is the S^T accumulator converted to
-//     bf16 in registers — no LDS round trip for P.
-//   - K and V^T tiles are double-buffered in LDS; the next block's global
-//     loads are in flight while the current block computes (one barrier per
-//     block).
+//   - O^T = V^T P^T is the second MFMA: V^T is the A operand, P^T (B operand)
+//     is the S^T accumulator converted to bf16 in registers — no LDS round
+//     trip for P; the row sum comes from v_dot2 over the packed P.
+//   - K and V tiles are loaded straight into LDS (buffer_load ... lds, no
+//     register staging), double-buffered: the next block's loads are in
+//     flight while the current block computes (one barrier per block).  V^T
+//     operands come from the row-major V tile through ds_read_b64_tr_b16.
+//   - The running max is rescaled lazily (only when it grows by > 2^8), so
+//     the O rescale leaves the inner loop.
 //   - Workgroups are remapped so the 8 XCDs each take contiguous runs of
 //     (b, h) query tiles and share K/V in their own L2.
 #include <math.h>
 
 #include "fa_device.hpp"
 #include "fa_kernels.hpp"
-#include "fa_tiles.hpp"
+#include "fa_lds.hpp"
 
 namespace fa {
 namespace {
 
-constexpr int kBM = 128;  // queries per workgroup
+constexpr int kBM = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kBN = 64;   // keys per block
 constexpr int kThreads = 256;
+// Lazy rescaling: the running max used as the exp2 reference only moves when
+// a row's max grows by more than 2^8 in the exp2 domain, so P <= 256 and the
+// O / l rescale (64 + 1 multiplies per lane) runs in a handful of blocks.
+constexpr float kRescaleLog2 = 8.f;
 
 template <int D>
 struct FwdTile {
-    static constexpr int K_BYTES = Tile64<D>::BYTES;  // K tile, row-major swizzled
-    static constexpr int V_BYTES = Tile64<D>::BYTES;  // V^T tile
-    static constexpr int STAGE = K_BYTES + V_BYTES;
-    static constexpr int SMEM = 2 * STAGE;
+    using T = LdsTile<D, kBN>;
+    static constexpr int K_OFF = 0;                  // K tile, row-major
+    static constexpr int V_OFF = T::BYTES;           // V tile, row-major
+    static constexpr int STAGE = 2 * T::BYTES;
+    static constexpr int SMEM = 2 * STAGE;           // double buffered
+    static constexpr int WI = T::WAVE_INSTS / 4;     // wave-instructions per wave per tile
 };
 
 template <int D>
-struct TileRegs {
-    u32x4 k[Tile64<D>::RM_LOADS];
-    u32x4 v[Tile64<D>::PAIR_LOADS];
-};
-
-// Global -> registers for key block kb (rows >= S read as zero).
-template <int D>
-__device__ __forceinline__ void load_tile(TileRegs<D> &t, const bf16 *kbase, const bf16 *vbase,
-                                          int64_t k_ss, int64_t v_ss, int kb, int S, int tid) {
-    tile_load_rm<D>(t.k, kbase, k_ss, kb * kBN, S, tid);
-    tile_load_pairs<D>(t.v, vbase, v_ss, kb * kBN, S, tid);
-}
-
-// Registers -> LDS stage: K swizzled row-major, V transposed to V^T.
-template <int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D> &t, char *stage, int tid) {
-    tile_store_rm<D>(t.k, stage, tid);
-    tile_store_tr<D>(t.v, stage + FwdTile<D>::K_BYTES, tid);
-}
-
-template <int D>
-__global__ __launch_bounds__(kThreads) void attn_fwd_bf16_kernel(AttnFwdParams p) {
-    using T = FwdTile<D>;
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
+    using F = FwdTile<D>;
+    using T = typename F::T;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, g = lane >> 5;
@@ -81,6 +70,37 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_bf16_kernel(AttnFwdParams p
     const uint8_t *keep = p.keep ? p.keep + (int64_t)b * S : nullptr;
     const int qi = qt * kBM + wave * 32 + n;  // this lane's query row
 
+    // K and V tiles go straight from HBM/L2 into LDS; rows >= S read as zero
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(((S - 1) * p.k_ss + D) * 2));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(((S - 1) * p.v_ss + D) * 2));
+    uint32_t kvo[F::WI], vvo[F::WI];
+#pragma unroll
+    for (int i = 0; i < F::WI; ++i) {
+        kvo[i] = tile_src_off<D>(i * 4 + wave, lane, p.k_ss);
+        vvo[i] = tile_src_off<D>(i * 4 + wave, lane, p.v_ss);
+    }
+    const uint32_t kstep = (uint32_t)(kBN * p.k_ss * 2), vstep = (uint32_t)(kBN * p.v_ss * 2);
+    auto issue = [&](int kb, int buf) {
+        char *st = smem + buf * F::STAGE;
+#pragma unroll
+        for (int i = 0; i < F::WI; ++i)
+            buffer_to_lds_16(krs, st + F::K_OFF + (i * 4 + wave) * 1024, kvo[i], kb * kstep);
+#pragma unroll
+        for (int i = 0; i < F::WI; ++i)
+            buffer_to_lds_16(vrs, st + F::V_OFF + (i * 4 + wave) * 1024, vvo[i], kb * vstep);
+    };
+
+    // loop-invariant LDS operand offsets
+    uint32_t koff[D / 16];
+#pragma unroll
+    for (int kd = 0; kd < D / 16; ++kd) koff[kd] = row_frag_off<D>(n, kd, g);
+    uint32_t voff[D / 32][2];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        voff[dt][0] = col_frag_off<D>(0, 0, dt, lane);
+        voff[dt][1] = col_frag_off<D>(0, 1, dt, lane);
+    }
+
     // Q^T fragments (B operand): lane holds Q[qi][kd*16 + g*8 .. +8].
     bf16x8 qf[D / 16];
 #pragma unroll
@@ -93,26 +113,24 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_bf16_kernel(AttnFwdParams p
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_run = -INFINITY, m_sc = 0.f, l_run = 0.f;
     const float c = p.scale_log2;
+    const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
 
     const int nkb = (S + kBN - 1) / kBN;
-    TileRegs<D> regs;
-    load_tile<D>(regs, kbase, vbase, p.k_ss, p.v_ss, 0, S, tid);
-    store_tile<D>(regs, smem, tid);
-    __syncthreads();
-
+    issue(0, 0);
     for (int kb = 0; kb < nkb; ++kb) {
-        const char *stage = smem + (kb & 1) * T::STAGE;
-        if (kb + 1 < nkb) load_tile<D>(regs, kbase, vbase, p.k_ss, p.v_ss, kb + 1, S, tid);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // tile kb landed for every wave; tile kb-1 fully consumed
+        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
+        const char *ks_t = smem + (kb & 1) * F::STAGE + F::K_OFF;
+        const char *vs_t = smem + (kb & 1) * F::STAGE + F::V_OFF;
 
         // key-keep bits of this block (uniform over the workgroup)
         uint64_t km = ~0ull;
-        const bool tail = (kb + 1) * kBN > S;
-        if (keep || tail) {
+        if (keep || (kb + 1) * kBN > S) {
             const int key = kb * kBN + lane;
-            const bool kept = key < S && (!keep || keep[key]);
-            km = __ballot(kept);
+            km = __ballot(key < S && (!keep || keep[key]));
         }
 
         // S^T = K Q^T : two 32-key tiles
@@ -121,8 +139,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_bf16_kernel(AttnFwdParams p
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
 #pragma unroll
         for (int kd = 0; kd < D / 16; ++kd) {
-            const bf16x8 a0 = rm_frag<D>(stage, n, kd, g);
-            const bf16x8 a1 = rm_frag<D>(stage, 32 + n, kd, g);
+            const bf16x8 a0 = lds_read_row_frag(ks_t, koff[kd]);
+            const bf16x8 a1 = lds_read_row_frag(ks_t, koff[kd] + 32 * T::ROWB);
             s0 = mfma_32x32x16(a0, qf[kd], s0);
             s1 = mfma_32x32x16(a1, qf[kd], s1);
         }
@@ -135,46 +153,52 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_bf16_kernel(AttnFwdParams p
             }
         }
 
-        // online softmax (exp2 domain; m_run in raw score units)
+        // online softmax, exp2 domain, lazily rescaled
         float mx = fmaxf(s0[0], s1[0]);
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
         mx = fmaxf(mx, xor32(mx));
         const float m_new = fmaxf(m_run, mx);
-        const float m_sc = m_new == -INFINITY ? 0.f : m_new * c;
-        const float alpha = exp2_fast(m_run * c - m_sc);
-        m_run = m_new;
-        float psum = 0.f;
+        if (__any((m_new - m_run) * c > kRescaleLog2)) {
+            const float m_sc_new = m_new == -INFINITY ? 0.f : m_new * c;
+            const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_sc - m_sc_new);
+            m_run = m_new;
+            m_sc = m_sc_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        }
         bf16x8 pf[4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p0 = exp2_fast(s0[r] * c - m_sc);
-            const float p1 = exp2_fast(s1[r] * c - m_sc);
-            psum += p0 + p1;
-            pf[r >> 3][r & 7] = f32_to_bf16(p0);
-            pf[2 + (r >> 3)][r & 7] = f32_to_bf16(p1);
+        for (int ks = 0; ks < 4; ++ks) {
+            const f32x16 &sv = (ks >> 1) ? s1 : s0;
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = (ks & 1) * 8 + 2 * e;
+                const uint32_t word =
+                    pack_bf16x2(exp2_fast(sv[r] * c - m_sc), exp2_fast(sv[r + 1] * c - m_sc));
+                w[e] = word;
+                // row sum of the bf16 P actually multiplied into O
+                l_run = __builtin_amdgcn_fdot2_f32_bf16(u32_as_bf16x2(word), ones, l_run, false);
+            }
+            pf[ks] = as_bf16x8(w);
         }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
 
-        // O^T += V^T P^T
-        const char *vt = stage + T::K_BYTES;
+        // O^T += V^T P^T  (V^T fragments by transpose reads of the row-major V tile)
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8 a = tr_frag(vt, dt * 32 + n, ks, g);
+                const bf16x8 a = lds_read_col_frag(vs_t, voff[dt][0] + ks * 16 * T::ROWB,
+                                                   voff[dt][1] + ks * 16 * T::ROWB);
                 o[dt] = mfma_32x32x16(a, pf[ks], o[dt]);
             }
-
-        if (kb + 1 < nkb) store_tile<D>(regs, smem + ((kb + 1) & 1) * T::STAGE, tid);
-        __syncthreads();
     }
 
-    // finalize: O = O / l, LSE = m*scale + ln(l)
+    // finalize: O = O / l, LSE = m*scale + ln(l)   (P and l share the reference m_run)
     const float l_tot = l_run + xor32(l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (qi < S) {

@@ -110,6 +110,20 @@ fa_status check_attn_shape(int32_t dtype, int32_t B, int32_t S, int32_t H, int32
     return FA_OK;
 }
 
+// The bf16 kernels address K/V (and the backward's Q/dO) through 32-bit
+// buffer offsets and rely on rows of one head not overlapping, so rows past S
+// fall outside the buffer range and read as zero.
+fa_status check_buffer_view(const char *name, const fa_strides &st, int32_t S, int32_t D) {
+    if (st.s < D)
+        return fail(FA_ERR_INVALID_ARG, "%s sequence stride %lld is smaller than head_dim %d", name,
+                    (long long)st.s, D);
+    const int64_t bytes = ((int64_t)(S - 1) * st.s + D) * 2 + (int64_t)64 * st.s * 2;
+    if (bytes >= (int64_t(1) << 31))
+        return fail(FA_ERR_UNSUPPORTED, "%s spans %lld bytes per head; this build addresses < 2 GiB",
+                    name, (long long)bytes);
+    return FA_OK;
+}
+
 size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
 
 size_t bwd_workspace(int32_t B, int32_t S, int32_t H) {
@@ -155,6 +169,10 @@ fa_status fa_attn_fwd(const fa_attn_fwd_args *a, void *stream) {
     FA_TRY(check_view("v", a->v, a->v_stride, a->dtype));
     FA_TRY(check_view("o", a->o, a->o_stride, a->dtype));
     if (!a->lse || !aligned(a->lse, 4)) return fail(FA_ERR_INVALID_ARG, "lse is NULL or misaligned");
+    if (a->dtype == FA_DTYPE_BF16) {
+        FA_TRY(check_buffer_view("k", a->k_stride, a->seq, a->head_dim));
+        FA_TRY(check_buffer_view("v", a->v_stride, a->seq, a->head_dim));
+    }
     FA_TRY(init_current());
 
     fa::AttnFwdParams p{};

@@ -64,7 +64,10 @@ __device__ __forceinline__ void st_lds_4(char *smem, int byte_off, uint32_t v) {
     *reinterpret_cast<uint32_t *>(smem + byte_off) = v;
 }
 
+// Bit casts take their operand BY VALUE: clang's __builtin_bit_cast applied
+// directly to a vector-element lvalue (v[i]) reads element 0 whatever i is.
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x2 u32_as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
 __device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
 // Swap values between lane l and lane l^32.

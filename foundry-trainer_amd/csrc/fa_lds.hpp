@@ -1,0 +1,103 @@
+// LDS movement for gfx950 attention kernels: direct buffer->LDS tile loads
+// and the operand reads that consume them.
+//
+// Tile layout: R rows x D bf16 features, row-major, 2*D bytes per row, the
+// 16-byte chunks of row r stored at chunk position (c ^ (r % (D/8))).
+//
+// Loads: `buffer_load_dwordx4 ... lds` writes lane l's 16 bytes to
+// LDS[M0 + 16*l], so a wave-instruction fills 1 KiB of the tile; each lane
+// picks the global chunk that belongs at its LDS slot (this is where the
+// swizzle is applied).  The buffer resource's num_records bounds the tensor:
+// rows past the end read as zero, with 32-bit offsets only.
+//
+// Operand reads:
+//   row fragment  (ds_read_b128): 8 consecutive features of one row — the
+//                 MFMA operand whose lanes index rows (Q/K/V/dO as stored).
+//   col fragment  (2 x ds_read_b64_tr_b16): 8 rows of one feature — the
+//                 operand whose lanes index features and whose elements run
+//                 along rows (V^T, dO^T, Q^T, K^T).  Within each 16-lane
+//                 group the instruction hands lane i element (i % 4) of the
+//                 8 bytes addressed by lane 4e + i/4 (e = 0..3); pointing lane
+//                 j at row base + j/4, features f0 + 4*(j % 4) gives lane i the
+//                 four values X[base + e][f0 + i].
+#pragma once
+#include "fa_device.hpp"
+
+namespace fa {
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    // raw buffer, stride 0, 32-bit data format (GFX9 word 3)
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+// One wave-instruction: 16 bytes per lane from rsrc at (voff + soff) to
+// LDS[dst + 16*lane].  dst must be wave-uniform.
+__device__ __forceinline__ void buffer_to_lds_16(__amdgpu_buffer_rsrc_t rsrc, char *dst, uint32_t voff,
+                                                 uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)dst, 16,
+                                             voff, soff, 0, 0);
+}
+
+// Tile geometry for a D-feature bf16 tile of `ROWS` rows.
+template <int D, int ROWS>
+struct LdsTile {
+    static constexpr int ROWB = 2 * D;               // bytes per row
+    static constexpr int DCH = D / 8;                // chunks per row
+    static constexpr int BYTES = ROWS * ROWB;
+    static constexpr int WAVE_INSTS = BYTES / 1024;  // wave-instructions per tile
+};
+
+// Byte offset (relative to the tensor row base of the tile's first row) of
+// the global chunk that lane `lane` of wave-instruction `inst` must fetch.
+template <int D>
+__device__ __forceinline__ uint32_t tile_src_off(int inst, int lane, int64_t row_stride_elems) {
+    constexpr int DCH = D / 8;
+    const int c = inst * 64 + lane;              // physical chunk index in the tile
+    const int row = c / DCH, phys = c % DCH;
+    const int logical = phys ^ (row & (DCH - 1));
+    return (uint32_t)((row * row_stride_elems + logical * 8) * 2);
+}
+
+// Row fragment: row `row`, features kd*16 + g*8 .. +8.
+template <int D>
+__device__ __forceinline__ uint32_t row_frag_off(int row, int kd, int g) {
+    constexpr int DCH = D / 8;
+    return (uint32_t)(row * 2 * D + (((kd * 2 + g) ^ (row & (DCH - 1))) << 4));
+}
+
+__device__ __forceinline__ bf16x8 lds_read_row_frag(const char *smem, uint32_t off) {
+    return as_bf16x8(*reinterpret_cast<const u32x4 *>(smem + off));
+}
+
+// Column-fragment lane address for the 4-row half `half` (0: rows +0..3 of
+// the lane half's group, 1: rows +8..11) of a 16-row k-step, feature tile
+// `ft` (32 features).  lane -> group G = lane/16, j = lane%16, g = lane/32.
+template <int D>
+__device__ __forceinline__ uint32_t col_frag_off(int ks, int half, int ft, int lane) {
+    constexpr int DCH = D / 8;
+    const int j = lane & 15, G = lane >> 4;
+    const int g = G >> 1, dhalf = G & 1;
+    const int row = ks * 16 + half * 8 + g * 4 + (j >> 2);
+    const int f = ft * 32 + dhalf * 16 + 4 * (j & 3);
+    return (uint32_t)(row * 2 * D + (((f >> 3) ^ (row & (DCH - 1))) << 4) + (f & 7) * 2);
+}
+
+__device__ __forceinline__ i16x4 lds_read_tr16(const char *smem, uint32_t off) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4 *)(smem + off));
+}
+
+// Column fragment from two transpose reads: elements 0..3 from `off0`
+// (rows +g*4+0..3), 4..7 from `off1` (rows +8+g*4+0..3).  This is the k order
+// of an S^T / dS^T accumulator used as the other MFMA operand.
+__device__ __forceinline__ bf16x8 lds_read_col_frag(const char *smem, uint32_t off0, uint32_t off1) {
+    const i16x4 a = lds_read_tr16(smem, off0), b = lds_read_tr16(smem, off1);
+    typedef short i16x8 __attribute__((ext_vector_type(8)));
+    const i16x8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+}  // namespace fa
