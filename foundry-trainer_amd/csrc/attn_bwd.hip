@@ -19,19 +19,23 @@
 //   3. dq:     one workgroup per 128 queries (4 waves x 32), looping over
 //              64-key LDS stages.  S^T = K Q^T puts queries on the lanes, so
 //              dS^T feeds dQ^T = K^T dS^T as the B operand.
+// Tiles move HBM -> LDS with buffer_load ... lds (double-buffered, zero fill
+// past S); every transposed operand (dO^T, Q^T, K^T) is read from the same
+// row-major tile with ds_read_b64_tr_b16.
 // All GEMMs run on v_mfma_f32_32x32x16_bf16 (bf16 storage) or
 // v_mfma_f32_32x32x2_f32 (f32 storage) with f32 accumulation.
 #include <math.h>
 
 #include "fa_device.hpp"
 #include "fa_kernels.hpp"
-#include "fa_tiles.hpp"
+#include "fa_lds.hpp"
 
 namespace fa {
 namespace {
 
 // ---------------------------------------------------------------------------
-// 1. delta = rowsum(dO * O) in f32, written [B,H,S]
+// 1. delta = rowsum(dO * O) in f32, written [B,H,S]; also lse2 = LSE*log2(e)
+//    (+inf for a fully masked row, so P = exp2(s*c - lse2) = 0 there)
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(AttnBwdParams p) {
@@ -64,29 +68,40 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(AttnBwdParams p) {
     }
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (row < rows && part == 0) p.delta[((int64_t)b * p.H + h) * p.S + s] = acc;
+    if (row < rows && part == 0) {
+        const int64_t i = ((int64_t)b * p.H + h) * p.S + s;
+        p.delta[i] = acc;
+        const float l = p.lse[i];
+        p.lse2[i] = l == -INFINITY ? INFINITY : l * kLog2e;
+    }
 }
 
 // ---------------------------------------------------------------------------
-// 2. dK / dV (bf16)
+// 2. dK / dV (bf16): a workgroup owns 128 keys (4 waves x 32); it streams the
+//    queries in 64-row stages (Q, dO, lse2, delta) straight into LDS,
+//    double-buffered.  S = Q K^T and dP = dO V^T put the wave's keys on the
+//    accumulator lanes, so P^T and dS^T are A operands from registers; dO^T
+//    and Q^T come from the row-major tiles by transpose reads.
 // ---------------------------------------------------------------------------
 constexpr int kKT = 128;  // keys per workgroup
 constexpr int kQB = 64;   // queries per LDS stage
 
 template <int D>
-struct DkvSmem {
-    static constexpr int Q_RM = 0;
-    static constexpr int Q_TR = Q_RM + Tile64<D>::BYTES;
-    static constexpr int DO_RM = Q_TR + Tile64<D>::BYTES;
-    static constexpr int DO_TR = DO_RM + Tile64<D>::BYTES;
-    static constexpr int LSE = DO_TR + Tile64<D>::BYTES;  // 64 f32: lse * log2(e)
-    static constexpr int DELTA = LSE + kQB * 4;          // 64 f32
-    static constexpr int BYTES = DELTA + kQB * 4;
+struct DkvTile {
+    using T = LdsTile<D, kQB>;
+    static constexpr int Q_OFF = 0;
+    static constexpr int DO_OFF = T::BYTES;
+    static constexpr int LSE_OFF = 2 * T::BYTES;        // 64 f32
+    static constexpr int DELTA_OFF = LSE_OFF + kQB * 4;  // 64 f32
+    static constexpr int STAGE = DELTA_OFF + kQB * 4;
+    static constexpr int SMEM = 2 * STAGE;
+    static constexpr int WI = T::WAVE_INSTS / 4;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
-    using L = DkvSmem<D>;
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
+    using F = DkvTile<D>;
+    using T = typename F::T;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, g = lane >> 5;
@@ -100,12 +115,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p
     const bf16 *kbase = static_cast<const bf16 *>(p.k) + b * p.k_sb + h * p.k_sh;
     const bf16 *vbase = static_cast<const bf16 *>(p.v) + b * p.v_sb + h * p.v_sh;
     const bf16 *dobase = static_cast<const bf16 *>(p.dout) + b * p.do_sb + h * p.do_sh;
-    const float *lse = p.lse + ((int64_t)b * H + h) * S;
-    const float *delta = p.delta + ((int64_t)b * H + h) * S;
+    const int64_t row0 = ((int64_t)b * H + h) * S;
     const int kj = kt * kKT + wave * 32 + n;  // this lane's key
     const bool key_kept = kj < S && (!p.keep || p.keep[(int64_t)b * S + kj]);
 
-    // K^T and V^T B-operand fragments: lane holds row kj, features kd*16+g*8..+8
+    // K and V rows of this lane's key (B operands): features kd*16 + g*8 .. +8
     bf16x8 kf[D / 16], vf[D / 16];
 #pragma unroll
     for (int kd = 0; kd < D / 16; ++kd) {
@@ -113,6 +127,34 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p
         kf[kd] = as_bf16x8(in ? ld_global_16(kbase + kj * p.k_ss + kd * 16 + g * 8) : u32x4{0, 0, 0, 0});
         vf[kd] = as_bf16x8(in ? ld_global_16(vbase + kj * p.v_ss + kd * 16 + g * 8) : u32x4{0, 0, 0, 0});
     }
+
+    // stage loads: Q and dO tiles (rows >= S read as zero), lse2 and delta
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qbase, (uint32_t)(((S - 1) * p.q_ss + D) * 2));
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(dobase, (uint32_t)(((S - 1) * p.do_ss + D) * 2));
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(p.lse2 + row0, (uint32_t)(S * 4));
+    const __amdgpu_buffer_rsrc_t drs = make_rsrc(p.delta + row0, (uint32_t)(S * 4));
+    const uint32_t qvo = tile_src_off<D>(wave, lane, p.q_ss);
+    const uint32_t ovo = tile_src_off<D>(wave, lane, p.do_ss);
+    const uint32_t qi_step = tile_inst_row_step<D>(p.q_ss), oi_step = tile_inst_row_step<D>(p.do_ss);
+    const uint32_t qstep = (uint32_t)(kQB * p.q_ss * 2), ostep = (uint32_t)(kQB * p.do_ss * 2);
+    auto issue = [&](int qb, int buf) {
+        char *st = smem + buf * F::STAGE;
+#pragma unroll
+        for (int i = 0; i < F::WI; ++i)
+            buffer_to_lds_16(qrs, st + F::Q_OFF + (i * 4 + wave) * 1024, qvo, qb * qstep + i * qi_step);
+#pragma unroll
+        for (int i = 0; i < F::WI; ++i)
+            buffer_to_lds_16(ors, st + F::DO_OFF + (i * 4 + wave) * 1024, ovo, qb * ostep + i * oi_step);
+        if (wave == 0)
+            buffer_to_lds_4(lrs, st + F::LSE_OFF, lane * 4, qb * kQB * 4);
+        else if (wave == 1)
+            buffer_to_lds_4(drs, st + F::DELTA_OFF, lane * 4, qb * kQB * 4);
+    };
+
+    // loop-invariant LDS operand offsets
+    const RowFragAddr ra = row_frag_addr<D>(n, g);
+    const ColFragAddr ca0 = col_frag_addr<D>(0, lane), ca1 = col_frag_addr<D>(1, lane);
+
     f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
@@ -121,67 +163,63 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p
     const float c = p.scale_log2;
 
     const int nqb = (S + kQB - 1) / kQB;
+    issue(0, 0);
     for (int qb = 0; qb < nqb; ++qb) {
-        const int q0 = qb * kQB;
-        {
-            u32x4 rq[Tile64<D>::PAIR_LOADS], rd[Tile64<D>::PAIR_LOADS];
-            tile_load_pairs<D>(rq, qbase, p.q_ss, q0, S, tid);
-            tile_load_pairs<D>(rd, dobase, p.do_ss, q0, S, tid);
-            float lv = INFINITY, dlt = 0.f;  // rows past S contribute P = 0
-            if (tid < kQB && q0 + tid < S) {
-                const float l = lse[q0 + tid];
-                // a row with every key masked has LSE = -inf and P = 0
-                lv = l == -INFINITY ? INFINITY : l * kLog2e;
-                dlt = delta[q0 + tid];
-            }
-            __syncthreads();  // previous stage fully consumed
-            tile_store_rm_pairs<D>(rq, smem + L::Q_RM, tid);
-            tile_store_tr<D>(rq, smem + L::Q_TR, tid);
-            tile_store_rm_pairs<D>(rd, smem + L::DO_RM, tid);
-            tile_store_tr<D>(rd, smem + L::DO_TR, tid);
-            if (tid < kQB) {
-                reinterpret_cast<float *>(smem + L::LSE)[tid] = lv;
-                reinterpret_cast<float *>(smem + L::DELTA)[tid] = dlt;
-            }
-            __syncthreads();
-        }
-        const float *lse_s = reinterpret_cast<const float *>(smem + L::LSE);
-        const float *dlt_s = reinterpret_cast<const float *>(smem + L::DELTA);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (qb + 1 < nqb) issue(qb + 1, (qb + 1) & 1);
+        const char *st = smem + (qb & 1) * F::STAGE;
+        const char *qs_t = st + F::Q_OFF, *os_t = st + F::DO_OFF;
+        const float *lse_s = reinterpret_cast<const float *>(st + F::LSE_OFF);
+        const float *dlt_s = reinterpret_cast<const float *>(st + F::DELTA_OFF);
 
-#pragma unroll
+#pragma unroll 1
         for (int sub = 0; sub < kQB / 32; ++sub) {
-            // S = Q K^T and dP = dO V^T for 32 queries x this lane-column's key
-            f32x16 s, dp;
+            // S = Q K^T, dP = dO V^T : 32 queries x this lane's key
+            f32x16 sa, dp;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+            for (int r = 0; r < 16; ++r) sa[r] = dp[r] = 0.f;
 #pragma unroll
             for (int kd = 0; kd < D / 16; ++kd) {
-                s = mfma_32x32x16(rm_frag<D>(smem + L::Q_RM, sub * 32 + n, kd, g), kf[kd], s);
-                dp = mfma_32x32x16(rm_frag<D>(smem + L::DO_RM, sub * 32 + n, kd, g), vf[kd], dp);
+                const uint32_t o = row_frag_at(ra, kd) + sub * 32 * T::ROWB;
+                sa = mfma_32x32x16(lds_read_row_frag(qs_t, o), kf[kd], sa);
+                dp = mfma_32x32x16(lds_read_row_frag(os_t, o), vf[kd], dp);
             }
             bf16x8 pf[2], df[2];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int qi = sub * 32 + acc_row(r, lane);
-                float pv = exp2_fast(s[r] * c - lse_s[qi]);
-                pv = key_kept ? pv : 0.f;
-                const float ds = pv * (dp[r] - dlt_s[qi]);
-                pf[r >> 3][r & 7] = f32_to_bf16(pv);
-                df[r >> 3][r & 7] = f32_to_bf16(ds);
+            for (int grp = 0; grp < 4; ++grp) {
+                // queries sub*32 + grp*8 + g*4 + 0..3 of elements r = grp*4 + 0..3
+                const f32x4 l4 = *reinterpret_cast<const f32x4 *>(lse_s + sub * 32 + grp * 8 + g * 4);
+                const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dlt_s + sub * 32 + grp * 8 + g * 4);
+                float pv[4], dsv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = grp * 4 + e;
+                    pv[e] = key_kept ? exp2_fast(sa[r] * c - l4[e]) : 0.f;
+                    dsv[e] = pv[e] * (dp[r] - d4[e]);
+                }
+                u32x2 pw, dw;
+                pw[0] = pack_bf16x2(pv[0], pv[1]);
+                pw[1] = pack_bf16x2(pv[2], pv[3]);
+                dw[0] = pack_bf16x2(dsv[0], dsv[1]);
+                dw[1] = pack_bf16x2(dsv[2], dsv[3]);
+                set_half(pf[grp >> 1], grp & 1, pw);
+                set_half(df[grp >> 1], grp & 1, dw);
             }
             // dV += P^T dO, dK += dS^T Q  (contraction over the 32 queries)
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const int f = dt * 32 + n;
-                    dv[dt] = mfma_32x32x16(pf[ks], tr_frag(smem + L::DO_TR, f, sub * 2 + ks, g), dv[dt]);
-                    dk[dt] = mfma_32x32x16(df[ks], tr_frag(smem + L::Q_TR, f, sub * 2 + ks, g), dk[dt]);
+                    const uint32_t o0 = col_frag_at(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
+                    const uint32_t o1 = col_frag_at(ca1, dt) + (sub * 2 + ks) * 16 * T::ROWB;
+                    dv[dt] = mfma_32x32x16(pf[ks], lds_read_col_frag(os_t, o0, o1), dv[dt]);
+                    dk[dt] = mfma_32x32x16(df[ks], lds_read_col_frag(qs_t, o0, o1), dk[dt]);
                 }
         }
     }
 
-    // dk/dv accumulators: element r of lane = (key kt*128 + wave*32 + acc_row(r), d = dt*32 + n)
+    // accumulators: element r of lane = (key kt*128 + wave*32 + acc_row(r), d = dt*32 + n)
     bf16 *dkb = static_cast<bf16 *>(p.dk) + b * p.dk_sb + h * p.dk_sh;
     bf16 *dvb = static_cast<bf16 *>(p.dv) + b * p.dv_sb + h * p.dv_sh;
 #pragma unroll
@@ -198,22 +236,28 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p
 }
 
 // ---------------------------------------------------------------------------
-// 3. dQ (bf16)
+// 3. dQ (bf16): a workgroup owns 128 queries (4 waves x 32) and streams K/V in
+//    64-key stages straight into LDS, double-buffered.  S^T = K Q^T and
+//    dP^T = V dO^T put the wave's queries on the lanes; dQ^T = K^T dS^T takes
+//    K^T from the row-major K tile by transpose reads.
 // ---------------------------------------------------------------------------
 constexpr int kQT = 128;  // queries per workgroup
 constexpr int kKB = 64;   // keys per LDS stage
 
 template <int D>
-struct DqSmem {
-    static constexpr int K_RM = 0;
-    static constexpr int K_TR = K_RM + Tile64<D>::BYTES;
-    static constexpr int V_RM = K_TR + Tile64<D>::BYTES;
-    static constexpr int BYTES = V_RM + Tile64<D>::BYTES;
+struct DqTile {
+    using T = LdsTile<D, kKB>;
+    static constexpr int K_OFF = 0;
+    static constexpr int V_OFF = T::BYTES;
+    static constexpr int STAGE = 2 * T::BYTES;
+    static constexpr int SMEM = 2 * STAGE;
+    static constexpr int WI = T::WAVE_INSTS / 4;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
-    using L = DqSmem<D>;
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
+    using F = DqTile<D>;
+    using T = typename F::T;
     extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, g = lane >> 5;
@@ -230,6 +274,25 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) 
     const uint8_t *keep = p.keep ? p.keep + (int64_t)b * S : nullptr;
     const int qi = qt * kQT + wave * 32 + n;
 
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(((S - 1) * p.k_ss + D) * 2));
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(((S - 1) * p.v_ss + D) * 2));
+    const uint32_t kvo = tile_src_off<D>(wave, lane, p.k_ss);
+    const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
+    const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
+    const uint32_t kstep = (uint32_t)(kKB * p.k_ss * 2), vstep = (uint32_t)(kKB * p.v_ss * 2);
+    auto issue = [&](int kb, int buf) {
+        char *st = smem + buf * F::STAGE;
+#pragma unroll
+        for (int i = 0; i < F::WI; ++i)
+            buffer_to_lds_16(krs, st + F::K_OFF + (i * 4 + wave) * 1024, kvo, kb * kstep + i * ki_step);
+#pragma unroll
+        for (int i = 0; i < F::WI; ++i)
+            buffer_to_lds_16(vrs, st + F::V_OFF + (i * 4 + wave) * 1024, vvo, kb * vstep + i * vi_step);
+    };
+
+    const RowFragAddr ra = row_frag_addr<D>(n, g);
+    const ColFragAddr ca0 = col_frag_addr<D>(0, lane), ca1 = col_frag_addr<D>(1, lane);
+
     bf16x8 qf[D / 16], of[D / 16];
 #pragma unroll
     for (int kd = 0; kd < D / 16; ++kd) {
@@ -239,8 +302,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) 
     }
     float lse2 = INFINITY, dlt = 0.f;
     if (qi < S) {
-        const float l = p.lse[((int64_t)b * H + h) * S + qi];
-        lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
+        lse2 = p.lse2[((int64_t)b * H + h) * S + qi];
         dlt = p.delta[((int64_t)b * H + h) * S + qi];
     }
     f32x16 dq[D / 32];
@@ -251,52 +313,60 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) 
     const float c = p.scale_log2;
 
     const int nkb = (S + kKB - 1) / kKB;
+    issue(0, 0);
     for (int kb = 0; kb < nkb; ++kb) {
-        const int k0 = kb * kKB;
-        {
-            u32x4 rk[Tile64<D>::PAIR_LOADS], rv[Tile64<D>::RM_LOADS];
-            tile_load_pairs<D>(rk, kbase, p.k_ss, k0, S, tid);
-            tile_load_rm<D>(rv, vbase, p.v_ss, k0, S, tid);
-            __syncthreads();
-            tile_store_rm_pairs<D>(rk, smem + L::K_RM, tid);
-            tile_store_tr<D>(rk, smem + L::K_TR, tid);
-            tile_store_rm<D>(rv, smem + L::V_RM, tid);
-            __syncthreads();
-        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
+        const char *ks_t = smem + (kb & 1) * F::STAGE + F::K_OFF;
+        const char *vs_t = smem + (kb & 1) * F::STAGE + F::V_OFF;
         uint64_t km = ~0ull;
-        if (keep || k0 + kKB > S) {
-            const int key = k0 + lane;
+        if (keep || (kb + 1) * kKB > S) {
+            const int key = kb * kKB + lane;
             km = __ballot(key < S && (!keep || keep[key]));
         }
-        // S^T = K Q^T and dP^T = V dO^T: two 32-key tiles each
-        f32x16 s[2], dp[2];
+        // one 32-key tile at a time: S^T = K Q^T, dP^T = V dO^T, dS^T, then
+        // dQ^T += K^T dS^T over the tile's two 16-key steps
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t) {
+            f32x16 sa, dp;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[t][r] = dp[t][r] = 0.f;
+            for (int r = 0; r < 16; ++r) sa[r] = dp[r] = 0.f;
 #pragma unroll
-        for (int kd = 0; kd < D / 16; ++kd)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                s[t] = mfma_32x32x16(rm_frag<D>(smem + L::K_RM, t * 32 + n, kd, g), qf[kd], s[t]);
-                dp[t] = mfma_32x32x16(rm_frag<D>(smem + L::V_RM, t * 32 + n, kd, g), of[kd], dp[t]);
+            for (int kd = 0; kd < D / 16; ++kd) {
+                const uint32_t o = row_frag_at(ra, kd) + t * 32 * T::ROWB;
+                sa = mfma_32x32x16(lds_read_row_frag(ks_t, o), qf[kd], sa);
+                dp = mfma_32x32x16(lds_read_row_frag(vs_t, o), of[kd], dp);
             }
-        bf16x8 df[4];
+            bf16x8 df[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int h4 = 0; h4 < 4; ++h4) {
+                u32x2 w;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int kk = t * 32 + acc_row(r, lane);
-                float pv = exp2_fast(s[t][r] * c - lse2);
-                pv = ((km >> kk) & 1) ? pv : 0.f;
-                df[t * 2 + (r >> 3)][r & 7] = f32_to_bf16(pv * (dp[t][r] - dlt));
+                for (int e = 0; e < 2; ++e) {
+                    float d2[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int r = h4 * 4 + 2 * e + u;
+                        const int kk = t * 32 + acc_row(r, lane);
+                        float pv = exp2_fast(sa[r] * c - lse2);
+                        pv = ((km >> kk) & 1) ? pv : 0.f;
+                        d2[u] = pv * (dp[r] - dlt);
+                    }
+                    w[e] = pack_bf16x2(d2[0], d2[1]);
+                }
+                set_half(df[h4 >> 1], h4 & 1, w);
             }
-        // dQ^T += K^T dS^T
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+            for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                dq[dt] = mfma_32x32x16(tr_frag(smem + L::K_TR, dt * 32 + n, ks, g), df[ks], dq[dt]);
+                for (int ks = 0; ks < 2; ++ks) {
+                    const uint32_t kso = (t * 2 + ks) * 16 * T::ROWB;
+                    dq[dt] = mfma_32x32x16(
+                        lds_read_col_frag(ks_t, col_frag_at(ca0, dt) + kso, col_frag_at(ca1, dt) + kso),
+                        df[ks], dq[dt]);
+                }
+        }
     }
 
     if (qi < S) {
@@ -492,13 +562,13 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, hipStream_t s) {
     const int nk = (p.S + kKT - 1) / kKT, nq = (p.S + kQT - 1) / kQT;
     const dim3 gk(p.B * p.H * nk), gq(p.B * p.H * nq), block(256);
     if (D == 128) {
-        hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, gk, block, DkvSmem<128>::BYTES, s, p);
+        hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, gk, block, DkvTile<128>::SMEM, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<128>, gq, block, DqSmem<128>::BYTES, s, p);
+        hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<128>, gq, block, DqTile<128>::SMEM, s, p);
     } else {
-        hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, gk, block, DkvSmem<64>::BYTES, s, p);
+        hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, gk, block, DkvTile<64>::SMEM, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<64>, gq, block, DqSmem<64>::BYTES, s, p);
+        hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<64>, gq, block, DqTile<64>::SMEM, s, p);
     }
     return hipGetLastError();
 }
@@ -524,18 +594,18 @@ hipError_t prepare_bwd_kernels() {
     hipError_t e;
     if ((e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<128>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 DkvSmem<128>::BYTES)) != hipSuccess)
+                                 DkvTile<128>::SMEM)) != hipSuccess)
         return e;
     if ((e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<64>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 DkvSmem<64>::BYTES)) != hipSuccess)
+                                 DkvTile<64>::SMEM)) != hipSuccess)
         return e;
     if ((e = hipFuncSetAttribute((const void *)attn_bwd_dq_bf16_kernel<128>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 DqSmem<128>::BYTES)) != hipSuccess)
+                                 DqTile<128>::SMEM)) != hipSuccess)
         return e;
     return hipFuncSetAttribute((const void *)attn_bwd_dq_bf16_kernel<64>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, DqSmem<64>::BYTES);
+                               hipFuncAttributeMaxDynamicSharedMemorySize, DqTile<64>::SMEM);
 }
 
 }  // namespace fa

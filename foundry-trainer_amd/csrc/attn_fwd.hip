@@ -73,21 +73,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParam
     // K and V tiles go straight from HBM/L2 into LDS; rows >= S read as zero
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(((S - 1) * p.k_ss + D) * 2));
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(((S - 1) * p.v_ss + D) * 2));
-    uint32_t kvo[F::WI], vvo[F::WI];
-#pragma unroll
-    for (int i = 0; i < F::WI; ++i) {
-        kvo[i] = tile_src_off<D>(i * 4 + wave, lane, p.k_ss);
-        vvo[i] = tile_src_off<D>(i * 4 + wave, lane, p.v_ss);
-    }
+    const uint32_t kvo = tile_src_off<D>(wave, lane, p.k_ss);
+    const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
+    const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
     const uint32_t kstep = (uint32_t)(kBN * p.k_ss * 2), vstep = (uint32_t)(kBN * p.v_ss * 2);
     auto issue = [&](int kb, int buf) {
         char *st = smem + buf * F::STAGE;
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(krs, st + F::K_OFF + (i * 4 + wave) * 1024, kvo[i], kb * kstep);
+            buffer_to_lds_16(krs, st + F::K_OFF + (i * 4 + wave) * 1024, kvo, kb * kstep + i * ki_step);
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(vrs, st + F::V_OFF + (i * 4 + wave) * 1024, vvo[i], kb * vstep);
+            buffer_to_lds_16(vrs, st + F::V_OFF + (i * 4 + wave) * 1024, vvo, kb * vstep + i * vi_step);
     };
 
     // loop-invariant LDS operand offsets

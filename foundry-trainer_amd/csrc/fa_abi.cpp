@@ -126,8 +126,9 @@ fa_status check_buffer_view(const char *name, const fa_strides &st, int32_t S, i
 
 size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// backward workspace: delta [B,H,S] f32, then lse2 [B,H,S] f32
 size_t bwd_workspace(int32_t B, int32_t S, int32_t H) {
-    return round256((size_t)B * H * S * sizeof(float));
+    return 2 * round256((size_t)B * H * S * sizeof(float));
 }
 
 #define FA_TRY(expr)                      \
@@ -208,6 +209,12 @@ fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
     FA_TRY(check_view("dk", a->dk, a->dk_stride, a->dtype));
     FA_TRY(check_view("dv", a->dv, a->dv_stride, a->dtype));
     if (!a->lse || !aligned(a->lse, 4)) return fail(FA_ERR_INVALID_ARG, "lse is NULL or misaligned");
+    if (a->dtype == FA_DTYPE_BF16) {
+        FA_TRY(check_buffer_view("q", a->q_stride, a->seq, a->head_dim));
+        FA_TRY(check_buffer_view("k", a->k_stride, a->seq, a->head_dim));
+        FA_TRY(check_buffer_view("v", a->v_stride, a->seq, a->head_dim));
+        FA_TRY(check_buffer_view("dout", a->do_stride, a->seq, a->head_dim));
+    }
     const size_t need = bwd_workspace(a->batch, a->seq, a->heads);
     if (!a->workspace || !aligned(a->workspace, 256))
         return fail(FA_ERR_INVALID_ARG, "workspace is NULL or not 256-byte aligned");
@@ -220,6 +227,8 @@ fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
     p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
     p.keep = a->key_keep; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
     p.delta = static_cast<float *>(a->workspace);
+    p.lse2 = reinterpret_cast<float *>(static_cast<char *>(a->workspace) +
+                                       round256((size_t)a->batch * a->heads * a->seq * sizeof(float)));
     p.q_sb = a->q_stride.b; p.q_ss = a->q_stride.s; p.q_sh = a->q_stride.h;
     p.k_sb = a->k_stride.b; p.k_ss = a->k_stride.s; p.k_sh = a->k_stride.h;
     p.v_sb = a->v_stride.b; p.v_ss = a->v_stride.s; p.v_sh = a->v_stride.h;

@@ -27,6 +27,7 @@ struct AttnBwdParams {
     const uint8_t *keep;
     void *dq, *dk, *dv;
     float *delta;  // workspace: [B,H,S] rowsum(dO * O)
+    float *lse2;   // workspace: [B,H,S] LSE * log2(e), +inf for fully masked rows
     int64_t q_sb, q_ss, q_sh;
     int64_t k_sb, k_ss, k_sh;
     int64_t v_sb, v_ss, v_sh;

@@ -41,6 +41,21 @@ __device__ __forceinline__ void buffer_to_lds_16(__amdgpu_buffer_rsrc_t rsrc, ch
                                              voff, soff, 0, 0);
 }
 
+// 4 bytes per lane to LDS[dst + 4*lane] (a 64-entry f32 vector per wave).
+__device__ __forceinline__ void buffer_to_lds_4(__amdgpu_buffer_rsrc_t rsrc, char *dst, uint32_t voff,
+                                                uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)dst, 4,
+                                             voff, soff, 0, 0);
+}
+
+// Replace elements 4*half .. 4*half+3 of an MFMA operand with two packed words.
+__device__ __forceinline__ void set_half(bf16x8 &v, int half, u32x2 w) {
+    u32x4 u = as_u32x4(v);
+    u[2 * half] = w[0];
+    u[2 * half + 1] = w[1];
+    v = as_bf16x8(u);
+}
+
 // Tile geometry for a D-feature bf16 tile of `ROWS` rows.
 template <int D, int ROWS>
 struct LdsTile {
@@ -59,6 +74,50 @@ __device__ __forceinline__ uint32_t tile_src_off(int inst, int lane, int64_t row
     const int row = c / DCH, phys = c % DCH;
     const int logical = phys ^ (row & (DCH - 1));
     return (uint32_t)((row * row_stride_elems + logical * 8) * 2);
+}
+
+// Wave-instruction `inst` of a tile covers rows inst*(1024/ROWB) ..; for a
+// 64-row tile the 4 instructions of one wave are 16 rows apart, where the
+// XOR swizzle repeats, so they share one per-lane offset and differ only by
+// the uniform row step (added to the scalar offset).
+template <int D>
+__device__ __forceinline__ uint32_t tile_inst_row_step(int64_t row_stride_elems) {
+    return (uint32_t)(4 * (1024 / (2 * D)) * row_stride_elems * 2);
+}
+
+// Row-fragment addressing split into a per-lane base and an XOR key:
+//   offset(kd) = base + (((kd*2) ^ key) << 4)
+// for row `row` (lane's row), lane half g.
+struct RowFragAddr {
+    uint32_t base, key;
+};
+template <int D>
+__device__ __forceinline__ RowFragAddr row_frag_addr(int row, int g) {
+    constexpr int DCH = D / 8;
+    return {(uint32_t)(row * 2 * D), (uint32_t)(g ^ (row & (DCH - 1)))};
+}
+__device__ __forceinline__ uint32_t row_frag_at(RowFragAddr a, int kd) {
+    return a.base + (((uint32_t)(kd * 2) ^ a.key) << 4);
+}
+
+// Column-fragment addressing for half `half`: offset(ft) = base + (((ft*4) ^ key) << 4)
+// (valid for D = 128, where chunk = ft*4 + x with x < 4; for D = 64 the same
+// form holds with ft*4 < 8).
+struct ColFragAddr {
+    uint32_t base, key;
+};
+template <int D>
+__device__ __forceinline__ ColFragAddr col_frag_addr(int half, int lane) {
+    constexpr int DCH = D / 8;
+    const int j = lane & 15, G = lane >> 4;
+    const int g = G >> 1, dhalf = G & 1;
+    const int row = half * 8 + g * 4 + (j >> 2);
+    const int f = dhalf * 16 + 4 * (j & 3);  // feature within the 32-feature tile
+    const int x = f >> 3;                    // chunk within the tile, < 4
+    return {(uint32_t)(row * 2 * D + (f & 7) * 2), (uint32_t)(x ^ (row & (DCH - 1)))};
+}
+__device__ __forceinline__ uint32_t col_frag_at(ColFragAddr a, int ft) {
+    return a.base + (((uint32_t)(ft * 4) ^ a.key) << 4);
 }
 
 // Row fragment: row `row`, features kd*16 + g*8 .. +8.
