@@ -33,6 +33,10 @@ sys.path.insert(0, os.path.join(ROOT, "foundry-trainer_amd"))
 METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block steps/s"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# HBM bytes per launch of a kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE
+# counter runs scaled by a copy kernel of known size (recorded in
+# profiles/; None until measured for that kernel and workload)
+TRAFFIC = {}
 
 
 def parse():
@@ -121,16 +125,25 @@ def main():
     ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
     stream = torch.cuda.current_stream()
 
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(q)
+    dv = torch.empty_like(q)
+    grads = (dq, dk, dv)
+    ph = [(fa._abi.FA_BWD_PREPASS, None), (fa._abi.FA_BWD_DKDV, None), (fa._abi.FA_BWD_DQ, None)]
+
     def step(ev=None):
-        if ev:
-            ev[0].record(stream)
+        """One fwd+bwd.  With `ev`, HIP events bracket each launch on the
+        launch stream (the ABI launches on torch's current stream)."""
+        if ev is None:
+            fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
+            fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws, out=grads)
+            return
+        ev[0].record(stream)
         fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
-        if ev:
-            ev[1].record(stream)
-        g = fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws)
-        if ev:
-            ev[2].record(stream)
-        return g
+        ev[1].record(stream)
+        for i, p_ in enumerate(ph):
+            fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws, out=grads, phases=[p_])
+            ev[2 + i].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -142,22 +155,40 @@ def main():
     wall = time.perf_counter() - t0
     ms = 1e3 * wall / args.steps
 
-    # per-phase HIP-event timing (same stream as the launches), separate pass
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # per-kernel HIP-event timing in a separate pass over the same steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
     for e in evs:
         step(e)
     torch.cuda.synchronize()
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
+    names = ["attn_fwd", "attn_bwd_prepass", "attn_bwd_dkdv", "attn_bwd_dq"]
+    kms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / len(evs) for i, nm in enumerate(names)}
 
+    B, H, S, D = cfg.batch, cfg.heads, cfg.seq, cfg.head_dim
+    unit = cfg.fwd_flops() / 2.0  # one S x S x D GEMM (2*B*H*S_q*S_kv*D)
+    # algorithmic FLOPs per launch: fwd = QK^T + PV; dk/dv = S recompute, dP,
+    # dV, dK; dq = dQ only (its S/dP recompute is redundant work)
+    kflops = {"attn_fwd": 2 * unit, "attn_bwd_dkdv": 4 * unit, "attn_bwd_dq": 1 * unit}
+    # pre-pass bytes: read O and dO, read LSE, write delta and lse2
+    pre_bytes = 2 * B * S * H * D * 2 + 3 * B * H * S * 4
     f_fwd = cfg.fwd_flops()
     f_all = f_fwd + cfg.bwd_flops()
     value = f_all / (ms * 1e-3) / 1e12
-    fwd_tf = f_fwd / (fwd_ms * 1e-3) / 1e12
+    kernels = {}
+    for nm in names:
+        t = kms[nm]
+        if nm in kflops:
+            tf = kflops[nm] / (t * 1e-3) / 1e12
+            kernels[nm] = {"ms": round(t, 4), "tflops": round(tf, 2),
+                           "pct_of_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
+        else:
+            gbs = pre_bytes / (t * 1e-3) / 1e9
+            kernels[nm] = {"ms": round(t, 4), "gbs": round(gbs, 1),
+                           "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
+    dominant = max(kflops, key=lambda nm: kms[nm])
+    dom_tf = kflops[dominant] / (kms[dominant] * 1e-3) / 1e12
+    fwd_tf = f_fwd / (kms["attn_fwd"] * 1e-3) / 1e12
+    bwd_ms = kms["attn_bwd_prepass"] + kms["attn_bwd_dkdv"] + kms["attn_bwd_dq"]
     bwd_tf = cfg.bwd_flops() / (bwd_ms * 1e-3) / 1e12
-    dominant = "attn_bwd" if bwd_ms >= fwd_ms else "attn_fwd"
-    dom_ms = max(bwd_ms, fwd_ms)
-    dom_flops = cfg.bwd_flops() if dominant == "attn_bwd" else f_fwd
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -177,15 +208,15 @@ def main():
                    "batch": cfg.batch, "heads": cfg.heads, "seq_len": cfg.seq,
                    "head_dim": cfg.head_dim, "parallelism": "single GPU"},
         "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "fwd": {"ms": round(kms["attn_fwd"], 4), "tflops": round(fwd_tf, 2),
+                "pct_of_peak": round(100 * fwd_tf / PEAK_BF16_TFLOPS, 2)},
+        "bwd": {"ms": round(bwd_ms, 4), "tflops": round(bwd_tf, 2),
+                "pct_of_peak": round(100 * bwd_tf / PEAK_BF16_TFLOPS, 2)},
         "roofline": {"bound": "mfma", "kernel": dominant,
-                     "achieved": round(dom_flops / (dom_ms * 1e-3) / 1e12, 2),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(dom_flops / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
-        "kernels": {"attn_fwd": {"ms": round(fwd_ms, 4), "tflops": round(fwd_tf, 2),
-                                 "pct_of_peak": round(100 * fwd_tf / PEAK_BF16_TFLOPS, 2)},
-                    "attn_bwd": {"ms": round(bwd_ms, 4), "tflops": round(bwd_tf, 2),
-                                 "pct_of_peak": round(100 * bwd_tf / PEAK_BF16_TFLOPS, 2)}},
+                     "achieved": round(dom_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
+                     "traffic": TRAFFIC.get((cfg.name, dominant))},
+        "kernels": kernels,
     }
     if args.cpu_seconds > 0:
         rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)

@@ -99,15 +99,13 @@ struct DkvTile {
 };
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
+__device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, char *smem) {
     using F = DkvTile<D>;
     using T = typename F::T;
-    extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nk = (S + kKT - 1) / kKT;
-    const int work = xcd_remap(blockIdx.x, gridDim.x);
     const int kt = work % nk, bh = work / nk;
     const int h = bh % H, b = bh / H;
 
@@ -254,16 +252,18 @@ struct DqTile {
     static constexpr int WI = T::WAVE_INSTS / 4;
 };
 
+constexpr int kFusedSmem128 =
+    DkvTile<128>::SMEM > DqTile<128>::SMEM ? DkvTile<128>::SMEM : DqTile<128>::SMEM;
+constexpr int kFusedSmem64 = DkvTile<64>::SMEM > DqTile<64>::SMEM ? DkvTile<64>::SMEM : DqTile<64>::SMEM;
+
 template <int D>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
+__device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work, char *smem) {
     using F = DqTile<D>;
     using T = typename F::T;
-    extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nq = (S + kQT - 1) / kQT;
-    const int work = xcd_remap(blockIdx.x, gridDim.x);
     const int qt = work % nq, bh = work / nq;
     const int h = bh % H, b = bh / H;
 
@@ -382,6 +382,31 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams 
                 *reinterpret_cast<u32x2 *>(row + d) = w;
             }
     }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
+    extern __shared__ __align__(16) char smem[];
+    dkdv_block<D>(p, xcd_remap(blockIdx.x, gridDim.x), smem);
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
+    extern __shared__ __align__(16) char smem[];
+    dq_block<D>(p, xcd_remap(blockIdx.x, gridDim.x), smem);
+}
+
+// dK/dV and dQ in one launch: the first n_kv workgroups take dK/dV key tiles,
+// the rest dQ query tiles, so the shorter dQ tiles fill the last partial
+// wave of dK/dV workgroups instead of leaving CUs idle between two launches.
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_bwd_fused_bf16_kernel(AttnBwdParams p, int n_kv) {
+    extern __shared__ __align__(16) char smem[];
+    const int bid = blockIdx.x;
+    if (bid < n_kv)
+        dkdv_block<D>(p, xcd_remap(bid, n_kv), smem);
+    else
+        dq_block<D>(p, xcd_remap(bid - n_kv, (int)gridDim.x - n_kv), smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -556,41 +581,73 @@ hipError_t launch_delta(const AttnBwdParams &p, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, hipStream_t s) {
-    hipError_t e = D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
-    if (e != hipSuccess) return e;
-    const int nk = (p.S + kKT - 1) / kKT, nq = (p.S + kQT - 1) / kQT;
-    const dim3 gk(p.B * p.H * nk), gq(p.B * p.H * nq), block(256);
-    if (D == 128) {
-        hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, gk, block, DkvTile<128>::SMEM, s, p);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<128>, gq, block, DqTile<128>::SMEM, s, p);
-    } else {
-        hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, gk, block, DkvTile<64>::SMEM, s, p);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<64>, gq, block, DqTile<64>::SMEM, s, p);
+hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
+    hipError_t e = hipSuccess;
+    if (phase == 0 || phase == 1) {
+        e = D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
+        if (e != hipSuccess) return e;
     }
-    return hipGetLastError();
+    const dim3 block(256);
+    const int n_kv = p.B * p.H * ((p.S + kKT - 1) / kKT);
+    const int n_q = p.B * p.H * ((p.S + kQT - 1) / kQT);
+    if (phase == 0) {
+        const dim3 grid(n_kv + n_q);
+        if (D == 128)
+            hipLaunchKernelGGL(attn_bwd_fused_bf16_kernel<128>, grid, block, kFusedSmem128, s, p, n_kv);
+        else
+            hipLaunchKernelGGL(attn_bwd_fused_bf16_kernel<64>, grid, block, kFusedSmem64, s, p, n_kv);
+        return hipGetLastError();
+    }
+    if (phase == 2) {
+        if (D == 128)
+            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, dim3(n_kv), block, DkvTile<128>::SMEM, s, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, dim3(n_kv), block, DkvTile<64>::SMEM, s, p);
+        e = hipGetLastError();
+    }
+    if (phase == 3) {
+        if (D == 128)
+            hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<128>, dim3(n_q), block, DqTile<128>::SMEM, s, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<64>, dim3(n_q), block, DqTile<64>::SMEM, s, p);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
-hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, hipStream_t s) {
-    hipError_t e = D == 128 ? launch_delta<float, 128>(p, s) : launch_delta<float, 64>(p, s);
-    if (e != hipSuccess) return e;
-    const int n32 = (p.S + 31) / 32;
-    const dim3 grid(p.B * p.H * n32), block(64);
-    if (D == 128) {
-        hipLaunchKernelGGL(attn_bwd_dkdv_f32_kernel<128>, grid, block, 0, s, p);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, grid, block, 0, s, p);
-    } else {
-        hipLaunchKernelGGL(attn_bwd_dkdv_f32_kernel<64>, grid, block, 0, s, p);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<64>, grid, block, 0, s, p);
+hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
+    hipError_t e = hipSuccess;
+    if (phase == 0 || phase == 1) {
+        e = D == 128 ? launch_delta<float, 128>(p, s) : launch_delta<float, 64>(p, s);
+        if (e != hipSuccess) return e;
     }
-    return hipGetLastError();
+    const dim3 grid(p.B * p.H * ((p.S + 31) / 32)), block(64);
+    if (phase == 0 || phase == 2) {
+        if (D == 128)
+            hipLaunchKernelGGL(attn_bwd_dkdv_f32_kernel<128>, grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dkdv_f32_kernel<64>, grid, block, 0, s, p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (phase == 0 || phase == 3) {
+        if (D == 128)
+            hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<64>, grid, block, 0, s, p);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 hipError_t prepare_bwd_kernels() {
+    {
+        hipError_t e = hipFuncSetAttribute((const void *)attn_bwd_fused_bf16_kernel<128>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kFusedSmem128);
+        if (e != hipSuccess) return e;
+        e = hipFuncSetAttribute((const void *)attn_bwd_fused_bf16_kernel<64>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kFusedSmem64);
+        if (e != hipSuccess) return e;
+    }
     hipError_t e;
     if ((e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<128>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize,

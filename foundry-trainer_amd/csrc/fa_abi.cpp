@@ -198,7 +198,13 @@ size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *a) {
 }
 
 fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
+    return fa_attn_bwd_phase(a, FA_BWD_ALL, stream);
+}
+
+fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stream) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (phase < FA_BWD_ALL || phase > FA_BWD_DQ)
+        return fail(FA_ERR_INVALID_ARG, "unknown backward phase %d", phase);
     FA_TRY(check_attn_shape(a->dtype, a->batch, a->seq, a->heads, a->head_dim, a->scale));
     FA_TRY(check_view("q", a->q, a->q_stride, a->dtype));
     FA_TRY(check_view("k", a->k, a->k_stride, a->dtype));
@@ -241,8 +247,9 @@ fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
     p.scale = a->scale;
     p.scale_log2 = a->scale * 1.4426950408889634f;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const hipError_t e = a->dtype == FA_DTYPE_BF16 ? fa::launch_attn_bwd_bf16(p, a->head_dim, s)
-                                                   : fa::launch_attn_bwd_f32(p, a->head_dim, s);
+    const hipError_t e = a->dtype == FA_DTYPE_BF16
+                             ? fa::launch_attn_bwd_bf16(p, a->head_dim, phase, s)
+                             : fa::launch_attn_bwd_f32(p, a->head_dim, phase, s);
     if (e != hipSuccess) return hip_fail(e, "attention backward launch");
     return ok();
 }

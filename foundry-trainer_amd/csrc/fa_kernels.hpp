@@ -43,8 +43,9 @@ struct AttnBwdParams {
 // Returns hipSuccess or the launch error.  `D` is 64 or 128.
 hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s);
 hipError_t launch_attn_fwd_f32(const AttnFwdParams &p, int D, hipStream_t s);
-hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, hipStream_t s);
-hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, hipStream_t s);
+// phase: 0 all, 1 pre-pass, 2 dK/dV, 3 dQ
+hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStream_t s);
+hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStream_t s);
 
 // One-time per-process kernel attribute setup (dynamic LDS limits).
 hipError_t prepare_attn_kernels();

@@ -16,11 +16,12 @@ FA_OK, FA_ERR_INVALID_ARG, FA_ERR_UNSUPPORTED, FA_ERR_NO_DEVICE, FA_ERR_LOAD_FAI
 STATUS_NAMES = {0: "OK", 1: "INVALID_ARG", 2: "UNSUPPORTED", 3: "NO_DEVICE", 4: "LOAD_FAILED",
                 5: "HIP_ERROR"}
 FA_DTYPE_BF16, FA_DTYPE_F32 = 0, 1
+FA_BWD_ALL, FA_BWD_PREPASS, FA_BWD_DKDV, FA_BWD_DQ = 0, 1, 2, 3
 FA_MAX_ROPE_AXES = 8
 
 EXPORTED = [
     "fa_version", "fa_last_error", "fa_op_name", "fa_init",
-    "fa_attn_fwd", "fa_attn_bwd_workspace_size", "fa_attn_bwd",
+    "fa_attn_fwd", "fa_attn_bwd_workspace_size", "fa_attn_bwd", "fa_attn_bwd_phase",
     "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
 ]
@@ -123,6 +124,8 @@ def lib() -> ctypes.CDLL:
         fn = getattr(L, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+    L.fa_attn_bwd_phase.restype = ctypes.c_int
+    L.fa_attn_bwd_phase.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_attn_bwd_workspace_size.restype = ctypes.c_size_t
     L.fa_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnBwdArgs)]
     L.fa_lora_bwd_workspace_size.restype = ctypes.c_size_t

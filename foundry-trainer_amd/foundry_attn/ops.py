@@ -102,8 +102,14 @@ def attn_fwd(q, k, v, scale: Optional[float] = None, key_keep=None, out=None, ls
 
 
 def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None,
-             workspace: Optional[torch.Tensor] = None):
-    """dq, dk, dv via fa_attn_bwd (P recomputed from the saved LSE)."""
+             workspace: Optional[torch.Tensor] = None, phases=None, out=None):
+    """dq, dk, dv via fa_attn_bwd (P recomputed from the saved LSE).
+
+    phases: None runs the whole backward in one call; otherwise an iterable of
+    (phase, stream_or_None) pairs issued in order through fa_attn_bwd_phase
+    (FA_BWD_PREPASS must come first), e.g. to time the launches separately.
+    out: optional (dq, dk, dv) tensors to write into.
+    """
     squeeze = q.dim() == 3
     q4, k4, v4 = _as4(q, "q"), _as4(k, "k"), _as4(v, "v")
     o4, do4 = _as4(o, "o"), _as4(dout, "dout")
@@ -114,9 +120,15 @@ def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None
     if lse.shape != (B, H, S) or lse.dtype != torch.float32 or lse.device != q4.device:
         raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "lse must be float32 (B,H,S) on q's device")
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    dq = torch.empty_like(q4, memory_format=torch.contiguous_format)
-    dk = torch.empty_like(k4, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v4, memory_format=torch.contiguous_format)
+    if out is None:
+        dq = torch.empty_like(q4, memory_format=torch.contiguous_format)
+        dk = torch.empty_like(k4, memory_format=torch.contiguous_format)
+        dv = torch.empty_like(v4, memory_format=torch.contiguous_format)
+    else:
+        dq, dk, dv = (_as4(t, "out") for t in out)
+        for t in (dq, dk, dv):
+            if t.shape != q4.shape or t.dtype != q4.dtype or t.device != q4.device:
+                raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "out grads do not match q")
     kk = _keep(key_keep, B, S, q4.device)
     a = _abi.AttnBwdArgs(dtype=_dtype_code(q4), batch=B, seq=S, heads=H, head_dim=D, scale=scale,
                          q=_ptr(q4), k=_ptr(k4), v=_ptr(v4), o=_ptr(o4), dout=_ptr(do4),
@@ -129,7 +141,12 @@ def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q4.device)
     a.workspace = workspace.data_ptr()
     a.workspace_bytes = workspace.numel() * workspace.element_size()
-    check(lib().fa_attn_bwd(ctypes.byref(a), _stream(q4)))
+    if phases is None:
+        check(lib().fa_attn_bwd(ctypes.byref(a), _stream(q4)))
+    else:
+        for ph, st in phases:
+            sp = _stream(q4) if st is None else st.cuda_stream
+            check(lib().fa_attn_bwd_phase(ctypes.byref(a), int(ph), sp))
     if squeeze:
         return dq[0], dk[0], dv[0]
     return dq, dk, dv

@@ -126,6 +126,22 @@ size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
  * Replaces AttnBwd::bwd (lib.rs:216-263). */
 fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
 
+/* The backward in its three launches, for callers that time them or run the
+ * two independent gradient kernels on separate streams:
+ *   FA_BWD_PREPASS  rowsum(dO * O) and LSE*log2(e) into the workspace
+ *   FA_BWD_DKDV     dK and dV (needs the pre-pass)
+ *   FA_BWD_DQ       dQ        (needs the pre-pass)
+ * FA_BWD_ALL runs all three, as fa_attn_bwd.  The caller orders the pre-pass
+ * before the other two (same stream, or an event).  No reference
+ * counterpart: AttnBwd::bwd (lib.rs:216-263) is one call. */
+typedef enum fa_bwd_phase {
+    FA_BWD_ALL = 0,
+    FA_BWD_PREPASS = 1,
+    FA_BWD_DKDV = 2,
+    FA_BWD_DQ = 3
+} fa_bwd_phase;
+fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *args, int32_t phase, void *stream);
+
 /* ------------------------------------------------------------------------- */
 /* QK prologue: RMSNorm -> axial RoPE -> joint buffer                        */
 /* ------------------------------------------------------------------------- */

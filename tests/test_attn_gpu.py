@@ -228,3 +228,35 @@ def test_custom_op_surface_and_autograd():
     torch.cuda.synchronize()
     assert torch.equal(out, res)
     assert torch.equal(qa.grad, dq) and torch.equal(ka.grad, dk) and torch.equal(va.grad, dv)
+
+
+def test_backward_phases_match_single_call():
+    """fa_attn_bwd_phase: pre-pass, dK/dV and dQ issued separately (one
+    stream, then dK/dV and dQ on two streams) give the one-call bits."""
+    from foundry_attn import _abi
+    torch.manual_seed(3)
+    q, k, v, do = (torch.randn(2, 700, 3, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
+    keep = torch.ones(2, 700, dtype=torch.uint8, device="cuda")
+    keep[0, 100:300] = 0
+    o, lse = attn_fwd(q, k, v, key_keep=keep)
+    ref = attn_bwd(q, k, v, o, do, lse, key_keep=keep)
+    seq = attn_bwd(q, k, v, o, do, lse, key_keep=keep,
+                   phases=[(_abi.FA_BWD_PREPASS, None), (_abi.FA_BWD_DKDV, None),
+                           (_abi.FA_BWD_DQ, None)])
+    cur = torch.cuda.current_stream()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()  # default priority
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    out = tuple(torch.empty_like(q) for _ in range(3))
+    attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=ws, out=out,
+             phases=[(_abi.FA_BWD_PREPASS, None)])
+    s1.wait_stream(cur)
+    s2.wait_stream(cur)
+    attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=ws, out=out,
+             phases=[(_abi.FA_BWD_DKDV, s1)])
+    attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=ws, out=out,
+             phases=[(_abi.FA_BWD_DQ, s2)])
+    cur.wait_stream(s1)
+    cur.wait_stream(s2)
+    torch.cuda.synchronize()
+    for a, b, c in zip(ref, seq, out):
+        assert torch.equal(a, b) and torch.equal(a, c)
