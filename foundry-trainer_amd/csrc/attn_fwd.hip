@@ -26,6 +26,8 @@
 //     (b, h) query tiles and share K/V in their own L2.
 #include <math.h>
 
+#include <type_traits>
+
 #include "fa_device.hpp"
 #include "fa_kernels.hpp"
 #include "fa_lds.hpp"
@@ -41,27 +43,37 @@ constexpr int kThreads = 256;
 // O / l rescale (64 + 1 multiplies per lane) runs in a handful of blocks.
 constexpr float kRescaleLog2 = 8.f;
 
+// LDS: K0 | K1 | V0 | V1, each a row-major 64-row tile.  K runs one block
+// ahead of V: iteration j reads K_{j+1} (for the next scores) and V_j.
 template <int D>
 struct FwdTile {
     using T = LdsTile<D, kBN>;
-    static constexpr int K_OFF = 0;                  // K tile, row-major
-    static constexpr int V_OFF = T::BYTES;           // V tile, row-major
-    static constexpr int STAGE = 2 * T::BYTES;
-    static constexpr int SMEM = 2 * STAGE;           // double buffered
+    static constexpr int K_OFF = 0;
+    static constexpr int V_OFF = 2 * T::BYTES;
+    static constexpr int SMEM = 4 * T::BYTES;
     static constexpr int WI = T::WAVE_INSTS / 4;     // wave-instructions per wave per tile
 };
 
+// Per-lane state of one query tile after a range of key blocks: the O^T
+// accumulators and this lane's half of the row sum, both relative to the exp2
+// reference m_sc = m_run * scale_log2 (0 while m_run = -inf).
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
+struct FwdState {
+    f32x16 o[D / 32];
+    float m_run, m_sc, l_run;
+};
+
+// Key blocks [kb0, kb1) of query tile t (t = (b*H + h)*nq + qt).
+template <int D>
+__device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0, int kb1, char *smem,
+                                         FwdState<D> &st) {
     using F = FwdTile<D>;
     using T = typename F::T;
-    extern __shared__ __align__(16) char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nq = (S + kBM - 1) / kBM;
-    const int work = xcd_remap(blockIdx.x, gridDim.x);
-    const int qt = work % nq, bh = work / nq;
+    const int qt = t % nq, bh = t / nq;
     const int h = bh % H, b = bh / H;
 
     const bf16 *qbase = static_cast<const bf16 *>(p.q) + b * p.q_sb + h * p.q_sh;
@@ -77,26 +89,26 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParam
     const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
     const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
     const uint32_t kstep = (uint32_t)(kBN * p.k_ss * 2), vstep = (uint32_t)(kBN * p.v_ss * 2);
-    auto issue = [&](int kb, int buf) {
-        char *st = smem + buf * F::STAGE;
+    auto issue_k = [&](int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(krs, st + F::K_OFF + (i * 4 + wave) * 1024, kvo, kb * kstep + i * ki_step);
+            buffer_to_lds_16(krs, smem + F::K_OFF + buf * T::BYTES + (i * 4 + wave) * 1024, kvo,
+                             kb * kstep + i * ki_step);
+    };
+    auto issue_v = [&](int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(vrs, st + F::V_OFF + (i * 4 + wave) * 1024, vvo, kb * vstep + i * vi_step);
+            buffer_to_lds_16(vrs, smem + F::V_OFF + buf * T::BYTES + (i * 4 + wave) * 1024, vvo,
+                             kb * vstep + i * vi_step);
     };
 
     // loop-invariant LDS operand offsets
     uint32_t koff[D / 16];
 #pragma unroll
     for (int kd = 0; kd < D / 16; ++kd) koff[kd] = row_frag_off<D>(n, kd, g);
-    uint32_t voff[D / 32][2];
+    uint32_t voff[D / 32];  // rows +8 come from col_frag_hi8
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-        voff[dt][0] = col_frag_off<D>(0, 0, dt, lane);
-        voff[dt][1] = col_frag_off<D>(0, 1, dt, lane);
-    }
+    for (int dt = 0; dt < D / 32; ++dt) voff[dt] = col_frag_off<D>(0, 0, dt, lane);
 
     // Q^T fragments (B operand): lane holds Q[qi][kd*16 + g*8 .. +8].
     bf16x8 qf[D / 16];
@@ -114,47 +126,58 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParam
     const float c = p.scale_log2;
     const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
 
-    const int nkb = (S + kBN - 1) / kBN;
-    issue(0, 0);
-    for (int kb = 0; kb < nkb; ++kb) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // tile kb landed for every wave; tile kb-1 fully consumed
-        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
-        const char *ks_t = smem + (kb & 1) * F::STAGE + F::K_OFF;
-        const char *vs_t = smem + (kb & 1) * F::STAGE + F::V_OFF;
+    // S^T = K Q^T for a 64-key tile: MFMAs kd_lo .. kd_hi-1 of the 2 x D/16.
+    auto qk_part = [&](const char *kt, f32x16 &s0, f32x16 &s1, int kd_lo, int kd_hi) {
+#pragma unroll
+        for (int kd = kd_lo; kd < kd_hi; ++kd) {
+            const bf16x8 a0 = lds_read_row_frag(kt, koff[kd]);
+            const bf16x8 a1 = lds_read_row_frag(kt, koff[kd] + 32 * T::ROWB);
+            s0 = mfma_32x32x16(a0, qf[kd], s0);
+            s1 = mfma_32x32x16(a1, qf[kd], s1);
+        }
+    };
 
-        // key-keep bits of this block (uniform over the workgroup)
+    // One key block, software-pipelined: the scores of block kb (cur, computed
+    // one iteration earlier) go through the softmax and P V while the MFMAs of
+    // block kb+1's scores (nxt) are interleaved with that VALU work.  PAR is
+    // kb % 2, so every LDS stage offset is an immediate.
+    auto block = [&](auto par, int kb, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1) {
+        constexpr int P = decltype(par)::value;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // K_{kb+1}, V_kb landed; K_kb and V_{kb-1} fully consumed
+        if (kb + 2 < kb1) issue_k(kb + 2, P);
+        if (kb + 1 < kb1) issue_v(kb + 1, P ^ 1);
+        const char *kn = smem + F::K_OFF + (P ^ 1) * T::BYTES;  // K_{kb+1}
+        const char *vt = smem + F::V_OFF + P * T::BYTES;        // V_kb
+
+        // key-keep bits of block kb (uniform over the workgroup)
         uint64_t km = ~0ull;
         if (keep || (kb + 1) * kBN > S) {
             const int key = kb * kBN + lane;
             km = __ballot(key < S && (!keep || keep[key]));
         }
-
-        // S^T = K Q^T : two 32-key tiles
-        f32x16 s0, s1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
-#pragma unroll
-        for (int kd = 0; kd < D / 16; ++kd) {
-            const bf16x8 a0 = lds_read_row_frag(ks_t, koff[kd]);
-            const bf16x8 a1 = lds_read_row_frag(ks_t, koff[kd] + 32 * T::ROWB);
-            s0 = mfma_32x32x16(a0, qf[kd], s0);
-            s1 = mfma_32x32x16(a1, qf[kd], s1);
-        }
+        for (int r = 0; r < 16; ++r) n0[r] = n1[r] = 0.f;
+        // The last block computes scores of a stale K tile that are never
+        // used: keeping the MFMAs unconditional keeps them interleavable.
+        qk_part(kn, n0, n1, 0, 2);
         if (km != ~0ull) {
+            // acc_row(r, lane) = (r/4)*8 + 4*g + r%4: one lane-dependent shift,
+            // then constant bit positions
+            const uint32_t k0 = (uint32_t)(km >> (4 * g)), k1 = (uint32_t)(km >> (32 + 4 * g));
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int kk = acc_row(r, lane);
-                if (!((km >> kk) & 1)) s0[r] = -INFINITY;
-                if (!((km >> (kk + 32)) & 1)) s1[r] = -INFINITY;
+                const int kk = (r >> 2) * 8 + (r & 3);
+                if (!((k0 >> kk) & 1)) c0[r] = -INFINITY;
+                if (!((k1 >> kk) & 1)) c1[r] = -INFINITY;
             }
         }
 
         // online softmax, exp2 domain, lazily rescaled
-        float mx = fmaxf(s0[0], s1[0]);
+        float mx = fmaxf(c0[0], c1[0]);
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-        mx = fmaxf(mx, xor32(mx));
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(c0[r], c1[r]));
+        mx = max_xor32(mx);
         const float m_new = fmaxf(m_run, mx);
         if (__any((m_new - m_run) * c > kRescaleLog2)) {
             const float m_sc_new = m_new == -INFINITY ? 0.f : m_new * c;
@@ -167,10 +190,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParam
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
         }
-        bf16x8 pf[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const f32x16 &sv = (ks >> 1) ? s1 : s0;
+            const f32x16 &sv = (ks >> 1) ? c1 : c0;
             u32x4 w;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -181,22 +203,52 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParam
                 // row sum of the bf16 P actually multiplied into O
                 l_run = __builtin_amdgcn_fdot2_f32_bf16(u32_as_bf16x2(word), ones, l_run, false);
             }
-            pf[ks] = as_bf16x8(w);
-        }
-
-        // O^T += V^T P^T  (V^T fragments by transpose reads of the row-major V tile)
+            const bf16x8 pf = as_bf16x8(w);
+            // next block's scores, a slice per k-step
+            qk_part(kn, n0, n1, 2 + ks * (D / 16 - 2) / 4, 2 + (ks + 1) * (D / 16 - 2) / 4);
+            // O^T += V^T P^T  (V^T fragments by transpose reads of the row-major V tile)
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8 a = lds_read_col_frag(vs_t, voff[dt][0] + ks * 16 * T::ROWB,
-                                                   voff[dt][1] + ks * 16 * T::ROWB);
-                o[dt] = mfma_32x32x16(a, pf[ks], o[dt]);
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const bf16x8 a = lds_read_col_frag(vt, voff[dt] + ks * 16 * T::ROWB,
+                                                   col_frag_hi8<D>(voff, dt) + ks * 16 * T::ROWB);
+                o[dt] = mfma_32x32x16(a, pf, o[dt]);
             }
-    }
+        }
+    };
 
-    // finalize: O = O / l, LSE = m*scale + ln(l)   (P and l share the reference m_run)
-    const float l_tot = l_run + xor32(l_run);
+    // prologue: K_kb0 -> scores of block kb0; K_kb0+1 and V_kb0 in flight
+    f32x16 sa0, sa1, sb0, sb1;
+    issue_k(kb0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kb0 + 1 < kb1) issue_k(kb0 + 1, 1);
+    issue_v(kb0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sa0[r] = sa1[r] = 0.f;
+    qk_part(smem + F::K_OFF, sa0, sa1, 0, D / 16);
+    for (int kb = kb0; kb < kb1; kb += 2) {
+        block(std::integral_constant<int, 0>{}, kb, sa0, sa1, sb0, sb1);
+        if (kb + 1 < kb1) block(std::integral_constant<int, 1>{}, kb + 1, sb0, sb1, sa0, sa1);
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) st.o[dt] = o[dt];
+    st.m_run = m_run;
+    st.m_sc = m_sc;
+    st.l_run = l_run;
+
+}
+
+// O = O / l and LSE = (m_sc + log2 l) * ln 2 for query tile t.
+template <int D>
+__device__ __forceinline__ void fwd_store(const AttnFwdParams &p, int t, const FwdState<D> &st) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, g = lane >> 5;
+    const int S = p.S, H = p.H;
+    const int nq = (S + kBM - 1) / kBM;
+    const int qt = t % nq, bh = t / nq;
+    const int h = bh % H, b = bh / H;
+    const int qi = qt * kBM + wave * 32 + n;
+    const float l_tot = sum_xor32(st.l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (qi < S) {
         bf16 *orow = static_cast<bf16 *>(p.o) + b * p.o_sb + h * p.o_sh + qi * p.o_ss;
@@ -206,14 +258,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParam
             for (int grp = 0; grp < 4; ++grp) {
                 const int d = dt * 32 + grp * 8 + g * 4;
                 u32x2 w;
-                w[0] = pack_bf16x2(o[dt][grp * 4 + 0] * inv, o[dt][grp * 4 + 1] * inv);
-                w[1] = pack_bf16x2(o[dt][grp * 4 + 2] * inv, o[dt][grp * 4 + 3] * inv);
+                w[0] = pack_bf16x2(st.o[dt][grp * 4 + 0] * inv, st.o[dt][grp * 4 + 1] * inv);
+                w[1] = pack_bf16x2(st.o[dt][grp * 4 + 2] * inv, st.o[dt][grp * 4 + 3] * inv);
                 *reinterpret_cast<u32x2 *>(orow + d) = w;
             }
         if (g == 0)
             p.lse[((int64_t)b * H + h) * S + qi] =
-                l_tot > 0.f ? m_run * p.scale + log2_fast(l_tot) * 0.6931471805599453f : -INFINITY;
+                l_tot > 0.f ? (st.m_sc + log2_fast(l_tot)) * 0.6931471805599453f : -INFINITY;
     }
+}
+
+// One workgroup per 128-query tile.
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
+    extern __shared__ __align__(16) char smem[];
+    const int nkb = (p.S + kBN - 1) / kBN;
+    const int t = xcd_remap(blockIdx.x, gridDim.x);
+    FwdState<D> st;
+    fwd_tile<D>(p, t, 0, nkb, smem, st);
+    fwd_store<D>(p, t, st);
 }
 
 // ---------------------------------------------------------------------------

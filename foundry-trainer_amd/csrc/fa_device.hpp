@@ -73,6 +73,19 @@ __device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(
 // Swap values between lane l and lane l^32.
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
+// max / sum of a lane's value and its lane ^ 32 partner in one VALU exchange
+// (v_permlane32_swap: the returned pair is (x[l], x[l+32]) on lanes < 32 and
+// (x[l-32], x[l]) on lanes >= 32, so both halves combine the same operands in
+// the same order and get bit-identical results).
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Map a linear block id to a logical work id so that consecutive logical ids
 // land on the same XCD.  Workgroups are dispatched round-robin over the 8
 // XCDs (bid % 8); tiles of one (b, h) then share that XCD's L2 for K and V.
@@ -80,33 +93,6 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     const int q = nblocks >> 3, r = nblocks & 7;
     const int x = bid & 7, i = bid >> 3;
     return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
-}
-
-// ---- row-major tile with XOR-swizzled 16-byte chunks ----------------------
-// A tile of `rows` x DCH 16-byte chunks (DCH = D/8 for bf16).  Chunk c of row
-// r is stored at chunk position c ^ (r % DCH): 8 consecutive rows read at the
-// same logical chunk hit 8 distinct bank groups.
-template <int DCH>
-__device__ __forceinline__ int swz_off(int row, int chunk) {
-    return (row * DCH + (chunk ^ (row & (DCH - 1)))) * 16;
-}
-
-// ---- transposed tile ("key-major -> feature-major") -----------------------
-// T[f][key] for a 64-key tile, 128 bytes per feature row (8 chunks of 8 keys).
-// Within each 16-key group the keys are stored in MFMA-operand order so that
-// lane half g reads its 8 keys {4g..4g+3, 8+4g..8+4g+3} as one 16-byte chunk;
-// the chunk index is XOR-swizzled with (f % 8).  Returns the byte offset of
-// the 4-byte word holding keys (key, key+1), key even.
-__device__ __forceinline__ int tr64_pair_off(int f, int key) {
-    const int grp = key >> 4, kk = key & 15;
-    const int g = (kk >> 2) & 1, t = ((kk >> 3) << 2) | (kk & 3);
-    const int chunk = (grp * 2 + g) ^ (f & 7);
-    return f * 128 + chunk * 16 + t * 2;
-}
-// Byte offset of the 16-byte chunk lane-half g reads for MFMA k-step ks
-// (keys ks*16 .. ks*16+15) of feature row f.
-__device__ __forceinline__ int tr64_read_off(int f, int ks, int g) {
-    return f * 128 + (((ks * 2 + g) ^ (f & 7)) * 16);
 }
 
 }  // namespace fa

@@ -2,7 +2,7 @@
 // and the operand reads that consume them.
 //
 // Tile layout: R rows x D bf16 features, row-major, 2*D bytes per row, the
-// 16-byte chunks of row r stored at chunk position (c ^ (r % (D/8))).
+// 16-byte chunk c of row r stored at chunk position c ^ chunk_swz<D>(r).
 //
 // Loads: `buffer_load_dwordx4 ... lds` writes lane l's 16 bytes to
 // LDS[M0 + 16*l], so a wave-instruction fills 1 KiB of the tile; each lane
@@ -56,6 +56,25 @@ __device__ __forceinline__ void set_half(bf16x8 &v, int half, u32x2 w) {
     v = as_bf16x8(u);
 }
 
+// XOR key of row r's chunks.  Two read shapes must both hit distinct banks:
+//   row fragments: 16 consecutive rows at one logical chunk -> the key must
+//     be a bijection of r % 16 (of r % 8 within any 8 aligned rows);
+//   transpose reads: 4 aligned rows x 2 (or 4) adjacent chunks -> the keys of
+//     the 4 rows must differ in chunk bits 1..2 (and 2..3).
+// The plain key r % 16 fails the second (rows 4i..4i+3 only permute chunks
+// inside one aligned group).  With r = (r3 r2 r1 r0):
+//   key = (r1^r3) << 3 | r0 << 2 | r1 << 1 | (r2^r1)
+// is linear and invertible over GF(2) (r0 = k2, r1 = k1, r2 = k0^k1,
+// r3 = k3^k1), and over the 4 rows of a transpose read (r2, r3 fixed) bits
+// 1..2 take (r1, r0) and bits 2..3 take (r0, r1^r3): all distinct.  It depends
+// on r % 16 only.  D = 64 tiles have 8 chunks per row and use bits 0..2.
+template <int D>
+__device__ __forceinline__ int chunk_swz(int row) {
+    const int r0 = row & 1, r1 = (row >> 1) & 1, r2 = (row >> 2) & 1, r3 = (row >> 3) & 1;
+    const int k = (r2 ^ r1) | (r1 << 1) | (r0 << 2);
+    return D >= 128 ? (k | ((r1 ^ r3) << 3)) : k;
+}
+
 // Tile geometry for a D-feature bf16 tile of `ROWS` rows.
 template <int D, int ROWS>
 struct LdsTile {
@@ -72,13 +91,13 @@ __device__ __forceinline__ uint32_t tile_src_off(int inst, int lane, int64_t row
     constexpr int DCH = D / 8;
     const int c = inst * 64 + lane;              // physical chunk index in the tile
     const int row = c / DCH, phys = c % DCH;
-    const int logical = phys ^ (row & (DCH - 1));
+    const int logical = phys ^ chunk_swz<D>(row);
     return (uint32_t)((row * row_stride_elems + logical * 8) * 2);
 }
 
 // Wave-instruction `inst` of a tile covers rows inst*(1024/ROWB) ..; for a
 // 64-row tile the 4 instructions of one wave are 16 rows apart, where the
-// XOR swizzle repeats, so they share one per-lane offset and differ only by
+// chunk swizzle repeats, so they share one per-lane offset and differ only by
 // the uniform row step (added to the scalar offset).
 template <int D>
 __device__ __forceinline__ uint32_t tile_inst_row_step(int64_t row_stride_elems) {
@@ -93,8 +112,7 @@ struct RowFragAddr {
 };
 template <int D>
 __device__ __forceinline__ RowFragAddr row_frag_addr(int row, int g) {
-    constexpr int DCH = D / 8;
-    return {(uint32_t)(row * 2 * D), (uint32_t)(g ^ (row & (DCH - 1)))};
+    return {(uint32_t)(row * 2 * D), (uint32_t)(g ^ chunk_swz<D>(row))};
 }
 __device__ __forceinline__ uint32_t row_frag_at(RowFragAddr a, int kd) {
     return a.base + (((uint32_t)(kd * 2) ^ a.key) << 4);
@@ -108,13 +126,12 @@ struct ColFragAddr {
 };
 template <int D>
 __device__ __forceinline__ ColFragAddr col_frag_addr(int half, int lane) {
-    constexpr int DCH = D / 8;
     const int j = lane & 15, G = lane >> 4;
     const int g = G >> 1, dhalf = G & 1;
     const int row = half * 8 + g * 4 + (j >> 2);
     const int f = dhalf * 16 + 4 * (j & 3);  // feature within the 32-feature tile
     const int x = f >> 3;                    // chunk within the tile, < 4
-    return {(uint32_t)(row * 2 * D + (f & 7) * 2), (uint32_t)(x ^ (row & (DCH - 1)))};
+    return {(uint32_t)(row * 2 * D + (f & 7) * 2), (uint32_t)(x ^ chunk_swz<D>(row))};
 }
 __device__ __forceinline__ uint32_t col_frag_at(ColFragAddr a, int ft) {
     return a.base + (((uint32_t)(ft * 4) ^ a.key) << 4);
@@ -123,8 +140,7 @@ __device__ __forceinline__ uint32_t col_frag_at(ColFragAddr a, int ft) {
 // Row fragment: row `row`, features kd*16 + g*8 .. +8.
 template <int D>
 __device__ __forceinline__ uint32_t row_frag_off(int row, int kd, int g) {
-    constexpr int DCH = D / 8;
-    return (uint32_t)(row * 2 * D + (((kd * 2 + g) ^ (row & (DCH - 1))) << 4));
+    return (uint32_t)(row * 2 * D + (((kd * 2 + g) ^ chunk_swz<D>(row)) << 4));
 }
 
 __device__ __forceinline__ bf16x8 lds_read_row_frag(const char *smem, uint32_t off) {
@@ -136,12 +152,21 @@ __device__ __forceinline__ bf16x8 lds_read_row_frag(const char *smem, uint32_t o
 // `ft` (32 features).  lane -> group G = lane/16, j = lane%16, g = lane/32.
 template <int D>
 __device__ __forceinline__ uint32_t col_frag_off(int ks, int half, int ft, int lane) {
-    constexpr int DCH = D / 8;
     const int j = lane & 15, G = lane >> 4;
     const int g = G >> 1, dhalf = G & 1;
     const int row = ks * 16 + half * 8 + g * 4 + (j >> 2);
     const int f = ft * 32 + dhalf * 16 + 4 * (j & 3);
-    return (uint32_t)(row * 2 * D + (((f >> 3) ^ (row & (DCH - 1))) << 4) + (f & 7) * 2);
+    return (uint32_t)(row * 2 * D + (((f >> 3) ^ chunk_swz<D>(row)) << 4) + (f & 7) * 2);
+}
+
+// Column-fragment offset of the rows +8 half from the rows +0 offsets of all
+// feature tiles: chunk_swz(r + 8) = chunk_swz(r) ^ 8 flips chunk bit 3, which
+// is feature tile bit 1 (D = 128) — so it is tile dt ^ 2 of the +0 half moved
+// down 8 rows, an immediate.  For D = 64 (8 chunks) bit 3 is not used and the
+// +8 half is the same tile.
+template <int D>
+__device__ __forceinline__ uint32_t col_frag_hi8(const uint32_t *off0, int dt) {
+    return (D >= 128 ? off0[dt ^ 2] : off0[dt]) + 8 * 2 * D;
 }
 
 __device__ __forceinline__ i16x4 lds_read_tr16(const char *smem, uint32_t off) {
