@@ -115,7 +115,6 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
     const bf16 *dobase = static_cast<const bf16 *>(p.dout) + b * p.do_sb + h * p.do_sh;
     const int64_t row0 = ((int64_t)b * H + h) * S;
     const int kj = kt * kKT + wave * 32 + n;  // this lane's key
-    const bool key_kept = kj < S && (!p.keep || p.keep[(int64_t)b * S + kj]);
 
     // K and V rows of this lane's key (B operands): features kd*16 + g*8 .. +8
     bf16x8 kf[D / 16], vf[D / 16];
@@ -193,7 +192,7 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = grp * 4 + e;
-                    pv[e] = key_kept ? exp2_fast(sa[r] * c - l4[e]) : 0.f;
+                    pv[e] = exp2_fast(sa[r] * c - l4[e]);
                     dsv[e] = pv[e] * (dp[r] - d4[e]);
                 }
                 u32x2 pw, dw;
@@ -217,17 +216,21 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
         }
     }
 
-    // accumulators: element r of lane = (key kt*128 + wave*32 + acc_row(r), d = dt*32 + n)
+    // accumulators: element r of lane = (key kt*128 + wave*32 + acc_row(r), d = dt*32 + n).
+    // A lane's P / dS values feed only its own key's rows of dV / dK (the A
+    // operand row), so an excluded key is handled here: its rows are zero
+    // (selected, not multiplied: its unmasked P may have overflowed).
     bf16 *dkb = static_cast<bf16 *>(p.dk) + b * p.dk_sb + h * p.dk_sh;
     bf16 *dvb = static_cast<bf16 *>(p.dv) + b * p.dv_sb + h * p.dv_sh;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int key = kt * kKT + wave * 32 + acc_row(r, lane);
         if (key < S) {
+            const bool kept = !p.keep || p.keep[(int64_t)b * S + key];
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
-                dkb[key * p.dk_ss + dt * 32 + n] = f32_to_bf16(dk[dt][r] * p.scale);
-                dvb[key * p.dv_ss + dt * 32 + n] = f32_to_bf16(dv[dt][r]);
+                dkb[key * p.dk_ss + dt * 32 + n] = f32_to_bf16(kept ? dk[dt][r] * p.scale : 0.f);
+                dvb[key * p.dv_ss + dt * 32 + n] = f32_to_bf16(kept ? dv[dt][r] : 0.f);
             }
         }
     }
@@ -338,6 +341,14 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work, char 
                 sa = mfma_32x32x16(lds_read_row_frag(ks_t, o), qf[kd], sa);
                 dp = mfma_32x32x16(lds_read_row_frag(vs_t, o), of[kd], dp);
             }
+            if (km != ~0ull) {
+                // acc_row(r, lane) = (r/4)*8 + 4*g + r%4: one lane shift, then
+                // constant bit positions
+                const uint32_t kb32 = (uint32_t)(km >> (t * 32 + 4 * g));
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (!((kb32 >> ((r >> 2) * 8 + (r & 3))) & 1)) sa[r] = -INFINITY;
+            }
             bf16x8 df[2];
 #pragma unroll
             for (int h4 = 0; h4 < 4; ++h4) {
@@ -348,9 +359,7 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work, char 
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         const int r = h4 * 4 + 2 * e + u;
-                        const int kk = t * 32 + acc_row(r, lane);
-                        float pv = exp2_fast(sa[r] * c - lse2);
-                        pv = ((km >> kk) & 1) ? pv : 0.f;
+                        const float pv = exp2_fast(sa[r] * c - lse2);
                         d2[u] = pv * (dp[r] - dlt);
                     }
                     w[e] = pack_bf16x2(d2[0], d2[1]);

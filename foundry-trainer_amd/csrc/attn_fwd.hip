@@ -43,15 +43,12 @@ constexpr int kThreads = 256;
 // O / l rescale (64 + 1 multiplies per lane) runs in a handful of blocks.
 constexpr float kRescaleLog2 = 8.f;
 
-// LDS: K0 | K1 | V0 | V1, each a row-major 64-row tile.  K runs one block
+// LDS: K0, K1, V0, V1, each a row-major 64-row tile.  K runs one block
 // ahead of V: iteration j reads K_{j+1} (for the next scores) and V_j.
 template <int D>
 struct FwdTile {
     using T = LdsTile<D, kBN>;
-    static constexpr int K_OFF = 0;
-    static constexpr int V_OFF = 2 * T::BYTES;
-    static constexpr int SMEM = 4 * T::BYTES;
-    static constexpr int WI = T::WAVE_INSTS / 4;     // wave-instructions per wave per tile
+    static constexpr int WI = T::WAVE_INSTS / 4;  // wave-instructions per wave per tile
 };
 
 // Per-lane state of one query tile after a range of key blocks: the O^T
@@ -65,8 +62,7 @@ struct FwdState {
 
 // Key blocks [kb0, kb1) of query tile t (t = (b*H + h)*nq + qt).
 template <int D>
-__device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0, int kb1, char *smem,
-                                         FwdState<D> &st) {
+__device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0, int kb1, FwdState<D> &st) {
     using F = FwdTile<D>;
     using T = typename F::T;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -89,17 +85,20 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
     const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
     const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
     const uint32_t kstep = (uint32_t)(kBN * p.k_ss * 2), vstep = (uint32_t)(kBN * p.v_ss * 2);
-    auto issue_k = [&](int kb, int buf) {
+    // The four stage buffers are distinct LDS objects: the compiler can then
+    // tell a read of one stage from the DMA still filling another and emits no
+    // wait for the prefetch (one shared buffer makes it drain the prefetch
+    // before every transpose read).
+    __shared__ __align__(16) char ks0[T::BYTES], ks1[T::BYTES], vs0[T::BYTES], vs1[T::BYTES];
+    auto issue_k = [&](int kb, char *dst) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(krs, smem + F::K_OFF + buf * T::BYTES + (i * 4 + wave) * 1024, kvo,
-                             kb * kstep + i * ki_step);
+            buffer_to_lds_16(krs, dst + (i * 4 + wave) * 1024, kvo, kb * kstep + i * ki_step);
     };
-    auto issue_v = [&](int kb, int buf) {
+    auto issue_v = [&](int kb, char *dst) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(vrs, smem + F::V_OFF + buf * T::BYTES + (i * 4 + wave) * 1024, vvo,
-                             kb * vstep + i * vi_step);
+            buffer_to_lds_16(vrs, dst + (i * 4 + wave) * 1024, vvo, kb * vstep + i * vi_step);
     };
 
     // loop-invariant LDS operand offsets
@@ -145,10 +144,10 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         constexpr int P = decltype(par)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // K_{kb+1}, V_kb landed; K_kb and V_{kb-1} fully consumed
-        if (kb + 2 < kb1) issue_k(kb + 2, P);
-        if (kb + 1 < kb1) issue_v(kb + 1, P ^ 1);
-        const char *kn = smem + F::K_OFF + (P ^ 1) * T::BYTES;  // K_{kb+1}
-        const char *vt = smem + F::V_OFF + P * T::BYTES;        // V_kb
+        if (kb + 2 < kb1) issue_k(kb + 2, P ? ks1 : ks0);
+        if (kb + 1 < kb1) issue_v(kb + 1, P ? vs0 : vs1);
+        const char *kn = P ? ks0 : ks1;  // K_{kb+1}
+        const char *vt = P ? vs1 : vs0;  // V_kb
 
         // key-keep bits of block kb (uniform over the workgroup)
         uint64_t km = ~0ull;
@@ -218,14 +217,14 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
 
     // prologue: K_kb0 -> scores of block kb0; K_kb0+1 and V_kb0 in flight
     f32x16 sa0, sa1, sb0, sb1;
-    issue_k(kb0, 0);
+    issue_k(kb0, ks0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (kb0 + 1 < kb1) issue_k(kb0 + 1, 1);
-    issue_v(kb0, 0);
+    if (kb0 + 1 < kb1) issue_k(kb0 + 1, ks1);
+    issue_v(kb0, vs0);
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa0[r] = sa1[r] = 0.f;
-    qk_part(smem + F::K_OFF, sa0, sa1, 0, D / 16);
+    qk_part(ks0, sa0, sa1, 0, D / 16);
     for (int kb = kb0; kb < kb1; kb += 2) {
         block(std::integral_constant<int, 0>{}, kb, sa0, sa1, sb0, sb1);
         if (kb + 1 < kb1) block(std::integral_constant<int, 1>{}, kb + 1, sb0, sb1, sa0, sa1);
@@ -271,11 +270,10 @@ __device__ __forceinline__ void fwd_store(const AttnFwdParams &p, int t, const F
 // One workgroup per 128-query tile.
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
-    extern __shared__ __align__(16) char smem[];
     const int nkb = (p.S + kBN - 1) / kBN;
     const int t = xcd_remap(blockIdx.x, gridDim.x);
     FwdState<D> st;
-    fwd_tile<D>(p, t, 0, nkb, smem, st);
+    fwd_tile<D>(p, t, 0, nkb, st);
     fwd_store<D>(p, t, st);
 }
 
@@ -383,9 +381,9 @@ hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s) {
     const int nq = (p.S + kBM - 1) / kBM;
     const dim3 grid(p.B * p.H * nq), block(kThreads);
     if (D == 128)
-        hipLaunchKernelGGL(attn_fwd_bf16_kernel<128>, grid, block, FwdTile<128>::SMEM, s, p);
+        hipLaunchKernelGGL(attn_fwd_bf16_kernel<128>, grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL(attn_fwd_bf16_kernel<64>, grid, block, FwdTile<64>::SMEM, s, p);
+        hipLaunchKernelGGL(attn_fwd_bf16_kernel<64>, grid, block, 0, s, p);
     return hipGetLastError();
 }
 
@@ -399,13 +397,6 @@ hipError_t launch_attn_fwd_f32(const AttnFwdParams &p, int D, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t prepare_fwd_kernels() {
-    hipError_t e = hipFuncSetAttribute((const void *)attn_fwd_bf16_kernel<128>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       FwdTile<128>::SMEM);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)attn_fwd_bf16_kernel<64>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, FwdTile<64>::SMEM);
-}
+hipError_t prepare_fwd_kernels() { return hipSuccess; }  // static LDS only
 
 }  // namespace fa
