@@ -238,29 +238,26 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
 
 // ---------------------------------------------------------------------------
 // 3. dQ (bf16): a workgroup owns 128 queries (4 waves x 32) and streams K/V in
-//    64-key stages straight into LDS, double-buffered.  S^T = K Q^T and
+//    32-key units straight into LDS, four buffers deep.  S^T = K Q^T and
 //    dP^T = V dO^T put the wave's queries on the lanes; dQ^T = K^T dS^T takes
-//    K^T from the row-major K tile by transpose reads.
+//    K^T from the row-major K tile by transpose reads.  Software pipeline per
+//    unit u: the MFMAs of unit u+1's S^T / dP^T are interleaved with unit u's
+//    dS^T VALU work and dQ^T MFMAs, unit u+2 is in flight and unit u+3 is
+//    issued into the buffer unit u-1 just released.
 // ---------------------------------------------------------------------------
 constexpr int kQT = 128;  // queries per workgroup
-constexpr int kKB = 64;   // keys per LDS stage
+constexpr int kKU = 32;   // keys per unit
 
 template <int D>
 struct DqTile {
-    using T = LdsTile<D, kKB>;
-    static constexpr int K_OFF = 0;
-    static constexpr int V_OFF = T::BYTES;
-    static constexpr int STAGE = 2 * T::BYTES;
-    static constexpr int SMEM = 2 * STAGE;
-    static constexpr int WI = T::WAVE_INSTS / 4;
+    using T = LdsTile<D, kKU>;
+    static constexpr int WI = T::WAVE_INSTS / 4;  // wave-instructions per wave per tile
 };
 
-constexpr int kFusedSmem128 =
-    DkvTile<128>::SMEM > DqTile<128>::SMEM ? DkvTile<128>::SMEM : DqTile<128>::SMEM;
-constexpr int kFusedSmem64 = DkvTile<64>::SMEM > DqTile<64>::SMEM ? DkvTile<64>::SMEM : DqTile<64>::SMEM;
-
-template <int D>
-__device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work, char *smem) {
+// KEEP: a key mask is given (p.keep != nullptr).  The unmasked instance has
+// no per-unit loads besides the tile DMA.
+template <int D, bool KEEP>
+__device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     using F = DqTile<D>;
     using T = typename F::T;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -274,27 +271,38 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work, char 
     const bf16 *kbase = static_cast<const bf16 *>(p.k) + b * p.k_sb + h * p.k_sh;
     const bf16 *vbase = static_cast<const bf16 *>(p.v) + b * p.v_sb + h * p.v_sh;
     const bf16 *dobase = static_cast<const bf16 *>(p.dout) + b * p.do_sb + h * p.do_sh;
-    const uint8_t *keep = p.keep ? p.keep + (int64_t)b * S : nullptr;
+    const uint8_t *keep = KEEP ? p.keep + (int64_t)b * S : nullptr;
     const int qi = qt * kQT + wave * 32 + n;
+
+    // distinct LDS objects per buffer (see attn_fwd.hip: lets the compiler
+    // keep the prefetch DMA in flight across reads of the other buffers)
+    __shared__ __align__(16) char k0[T::BYTES], k1[T::BYTES], k2[T::BYTES], k3[T::BYTES];
+    __shared__ __align__(16) char v0[T::BYTES], v1[T::BYTES], v2[T::BYTES], v3[T::BYTES];
+    auto kb_ = [&](int i) -> char * { return i == 0 ? k0 : i == 1 ? k1 : i == 2 ? k2 : k3; };
+    auto vb_ = [&](int i) -> char * { return i == 0 ? v0 : i == 1 ? v1 : i == 2 ? v2 : v3; };
 
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(((S - 1) * p.k_ss + D) * 2));
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(((S - 1) * p.v_ss + D) * 2));
     const uint32_t kvo = tile_src_off<D>(wave, lane, p.k_ss);
     const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
     const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
-    const uint32_t kstep = (uint32_t)(kKB * p.k_ss * 2), vstep = (uint32_t)(kKB * p.v_ss * 2);
-    auto issue = [&](int kb, int buf) {
-        char *st = smem + buf * F::STAGE;
+    const uint32_t kstep = (uint32_t)(kKU * p.k_ss * 2), vstep = (uint32_t)(kKU * p.v_ss * 2);
+    auto issue = [&](int u, char *kd, char *vd) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(krs, st + F::K_OFF + (i * 4 + wave) * 1024, kvo, kb * kstep + i * ki_step);
+            buffer_to_lds_16(krs, kd + (i * 4 + wave) * 1024, kvo, u * kstep + i * ki_step);
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(vrs, st + F::V_OFF + (i * 4 + wave) * 1024, vvo, kb * vstep + i * vi_step);
+            buffer_to_lds_16(vrs, vd + (i * 4 + wave) * 1024, vvo, u * vstep + i * vi_step);
     };
 
-    const RowFragAddr ra = row_frag_addr<D>(n, g);
-    const ColFragAddr ca0 = col_frag_addr<D>(0, lane), ca1 = col_frag_addr<D>(1, lane);
+    // loop-invariant LDS operand offsets
+    uint32_t roff[D / 16];
+#pragma unroll
+    for (int kd = 0; kd < D / 16; ++kd) roff[kd] = row_frag_off<D>(n, kd, g);
+    uint32_t coff[D / 32];  // rows +8 come from col_frag_hi8
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) coff[dt] = col_frag_off<D>(0, 0, dt, lane);
 
     bf16x8 qf[D / 16], of[D / 16];
 #pragma unroll
@@ -315,68 +323,100 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work, char 
         for (int r = 0; r < 16; ++r) dq[dt][r] = 0.f;
     const float c = p.scale_log2;
 
-    const int nkb = (S + kKB - 1) / kKB;
-    issue(0, 0);
-    for (int kb = 0; kb < nkb; ++kb) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
-        const char *ks_t = smem + (kb & 1) * F::STAGE + F::K_OFF;
-        const char *vs_t = smem + (kb & 1) * F::STAGE + F::V_OFF;
-        uint64_t km = ~0ull;
-        if (keep || (kb + 1) * kKB > S) {
-            const int key = kb * kKB + lane;
-            km = __ballot(key < S && (!keep || keep[key]));
+    // S^T = K Q^T and dP^T = V dO^T of one unit, MFMAs kd_lo .. kd_hi-1
+    auto sdp = [&](const char *kt, const char *vt, f32x16 &sa, f32x16 &dp, int kd_lo, int kd_hi) {
+#pragma unroll
+        for (int kd = kd_lo; kd < kd_hi; ++kd) {
+            sa = mfma_32x32x16(lds_read_row_frag(kt, roff[kd]), qf[kd], sa);
+            dp = mfma_32x32x16(lds_read_row_frag(vt, roff[kd]), of[kd], dp);
         }
-        // one 32-key tile at a time: S^T = K Q^T, dP^T = V dO^T, dS^T, then
-        // dQ^T += K^T dS^T over the tile's two 16-key steps
+    };
+
+    // Units run in groups of four (padding units lie past S: they read zeros
+    // and are fully masked).  Every unit issues its prefetch and its next
+    // keep-byte load unconditionally, so each unit sees the same loads in
+    // flight and the only waits are the explicit ones at the barriers.
+    const int nku = (S + kKU - 1) / kKU;
+    const int nku4 = (nku + 3) & ~3;
+    // keep byte of this lane's key in unit u (clamped address; KEEP only)
+    auto keep_byte = [&](int u) -> uint32_t { return KEEP ? keep[min(u * kKU + n, S - 1)] : 1u; };
+    uint32_t kbyte = keep_byte(0);
+    auto unit = [&](auto par, int u, f32x16 &sc, f32x16 &dc, f32x16 &sn, f32x16 &dn) {
+        constexpr int P = decltype(par)::value;  // u % 4
+        // unit u+1 landed (unit u+2, 2*WI loads per wave, may still be in
+        // flight, as may the keep byte issued after it); unit u-1 consumed
+        barrier_keep_dma<2 * F::WI>();
+        // key-keep bits of unit u, lanes 0..31 (uniform over the workgroup).
+        // The byte was loaded one unit ago and has landed under the barrier's
+        // wait; the empty asm keeps its use here (hoisted into the previous
+        // unit, its wait would also drain the prefetch issued after it).
+        if constexpr (KEEP) asm volatile("" : "+v"(kbyte));
+        const int key = u * kKU + n;
+        const uint64_t km = __ballot(key < S && kbyte != 0);
+        kbyte = keep_byte(u + 1);
+        issue(u + 3, kb_((P + 3) & 3), vb_((P + 3) & 3));
+        const char *kc = kb_(P), *kn = kb_((P + 1) & 3), *vn = vb_((P + 1) & 3);
+
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            f32x16 sa, dp;
+        for (int r = 0; r < 16; ++r) sn[r] = dn[r] = 0.f;
+        // next unit's scores (a zero or stale tile after the last unit, never
+        // used) interleave with this unit's work
+        sdp(kn, vn, sn, dn, 0, 2);
+        if (km != ~0ull) {
+            // acc_row(r, lane) = (r/4)*8 + 4*g + r%4: one lane shift, then
+            // constant bit positions
+            const uint32_t kb32 = (uint32_t)(km >> (4 * g));
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sa[r] = dp[r] = 0.f;
+            for (int r = 0; r < 16; ++r)
+                if (!((kb32 >> ((r >> 2) * 8 + (r & 3))) & 1)) sc[r] = -INFINITY;
+        }
 #pragma unroll
-            for (int kd = 0; kd < D / 16; ++kd) {
-                const uint32_t o = row_frag_at(ra, kd) + t * 32 * T::ROWB;
-                sa = mfma_32x32x16(lds_read_row_frag(ks_t, o), qf[kd], sa);
-                dp = mfma_32x32x16(lds_read_row_frag(vs_t, o), of[kd], dp);
-            }
-            if (km != ~0ull) {
-                // acc_row(r, lane) = (r/4)*8 + 4*g + r%4: one lane shift, then
-                // constant bit positions
-                const uint32_t kb32 = (uint32_t)(km >> (t * 32 + 4 * g));
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 df;
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (!((kb32 >> ((r >> 2) * 8 + (r & 3))) & 1)) sa[r] = -INFINITY;
-            }
-            bf16x8 df[2];
-#pragma unroll
-            for (int h4 = 0; h4 < 4; ++h4) {
+            for (int hh = 0; hh < 2; ++hh) {
                 u32x2 w;
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     float d2[2];
 #pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const int r = h4 * 4 + 2 * e + u;
-                        const float pv = exp2_fast(sa[r] * c - lse2);
-                        d2[u] = pv * (dp[r] - dlt);
+                    for (int v = 0; v < 2; ++v) {
+                        const int r = (ks * 2 + hh) * 4 + 2 * e + v;
+                        const float pv = exp2_fast(sc[r] * c - lse2);
+                        d2[v] = pv * (dc[r] - dlt);
                     }
                     w[e] = pack_bf16x2(d2[0], d2[1]);
                 }
-                set_half(df[h4 >> 1], h4 & 1, w);
+                set_half(df, hh, w);
             }
+            sdp(kn, vn, sn, dn, 2 + ks * (D / 16 - 2) / 2, 2 + (ks + 1) * (D / 16 - 2) / 2);
+            // dQ^T += K^T dS^T over this 16-key step
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const uint32_t kso = (t * 2 + ks) * 16 * T::ROWB;
-                    dq[dt] = mfma_32x32x16(
-                        lds_read_col_frag(ks_t, col_frag_at(ca0, dt) + kso, col_frag_at(ca1, dt) + kso),
-                        df[ks], dq[dt]);
-                }
+                dq[dt] = mfma_32x32x16(lds_read_col_frag(kc, coff[dt] + ks * 16 * T::ROWB,
+                                                         col_frag_hi8<D>(coff, dt) + ks * 16 * T::ROWB),
+                                       df, dq[dt]);
         }
+    };
+
+    // prologue: units 0..2 issued, unit 0's scores computed
+    issue(0, k0, v0);
+    issue(1, k1, v1);
+    issue(2, k2, v2);
+    barrier_keep_dma<0>();
+    f32x16 sa0, da0, sa1, da1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sa0[r] = da0[r] = 0.f;
+    sdp(k0, v0, sa0, da0, 0, D / 16);
+    for (int u = 0; u < nku4; u += 4) {
+        unit(std::integral_constant<int, 0>{}, u, sa0, da0, sa1, da1);
+        unit(std::integral_constant<int, 1>{}, u + 1, sa1, da1, sa0, da0);
+        unit(std::integral_constant<int, 2>{}, u + 2, sa0, da0, sa1, da1);
+        unit(std::integral_constant<int, 3>{}, u + 3, sa1, da1, sa0, da0);
     }
+    // the last prefetches are still writing LDS: they must land before the
+    // workgroup can end
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (qi < S) {
         bf16 *row = static_cast<bf16 *>(p.dq) + b * p.dq_sb + h * p.dq_sh + qi * p.dq_ss;
@@ -399,23 +439,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParam
     dkdv_block<D>(p, xcd_remap(blockIdx.x, gridDim.x), smem);
 }
 
-template <int D>
+template <int D, bool KEEP>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
-    extern __shared__ __align__(16) char smem[];
-    dq_block<D>(p, xcd_remap(blockIdx.x, gridDim.x), smem);
-}
-
-// dK/dV and dQ in one launch: the first n_kv workgroups take dK/dV key tiles,
-// the rest dQ query tiles, so the shorter dQ tiles fill the last partial
-// wave of dK/dV workgroups instead of leaving CUs idle between two launches.
-template <int D>
-__global__ __launch_bounds__(256, 2) void attn_bwd_fused_bf16_kernel(AttnBwdParams p, int n_kv) {
-    extern __shared__ __align__(16) char smem[];
-    const int bid = blockIdx.x;
-    if (bid < n_kv)
-        dkdv_block<D>(p, xcd_remap(bid, n_kv), smem);
-    else
-        dq_block<D>(p, xcd_remap(bid - n_kv, (int)gridDim.x - n_kv), smem);
+    dq_block<D, KEEP>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
 // ---------------------------------------------------------------------------
@@ -599,26 +625,23 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStr
     const dim3 block(256);
     const int n_kv = p.B * p.H * ((p.S + kKT - 1) / kKT);
     const int n_q = p.B * p.H * ((p.S + kQT - 1) / kQT);
-    if (phase == 0) {
-        const dim3 grid(n_kv + n_q);
-        if (D == 128)
-            hipLaunchKernelGGL(attn_bwd_fused_bf16_kernel<128>, grid, block, kFusedSmem128, s, p, n_kv);
-        else
-            hipLaunchKernelGGL(attn_bwd_fused_bf16_kernel<64>, grid, block, kFusedSmem64, s, p, n_kv);
-        return hipGetLastError();
-    }
-    if (phase == 2) {
+    if (phase == 0 || phase == 2) {
         if (D == 128)
             hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, dim3(n_kv), block, DkvTile<128>::SMEM, s, p);
         else
             hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, dim3(n_kv), block, DkvTile<64>::SMEM, s, p);
-        e = hipGetLastError();
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if (phase == 3) {
-        if (D == 128)
-            hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<128>, dim3(n_q), block, DqTile<128>::SMEM, s, p);
+    if (phase == 0 || phase == 3) {
+        const dim3 grid(n_q);
+        if (D == 128 && p.keep)
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, true>), grid, block, 0, s, p);
+        else if (D == 128)
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, false>), grid, block, 0, s, p);
+        else if (p.keep)
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, true>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL(attn_bwd_dq_bf16_kernel<64>, dim3(n_q), block, DqTile<64>::SMEM, s, p);
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, false>), grid, block, 0, s, p);
         e = hipGetLastError();
     }
     return e;
@@ -649,29 +672,11 @@ hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStre
 }
 
 hipError_t prepare_bwd_kernels() {
-    {
-        hipError_t e = hipFuncSetAttribute((const void *)attn_bwd_fused_bf16_kernel<128>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kFusedSmem128);
-        if (e != hipSuccess) return e;
-        e = hipFuncSetAttribute((const void *)attn_bwd_fused_bf16_kernel<64>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kFusedSmem64);
-        if (e != hipSuccess) return e;
-    }
-    hipError_t e;
-    if ((e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<128>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 DkvTile<128>::SMEM)) != hipSuccess)
-        return e;
-    if ((e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<64>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 DkvTile<64>::SMEM)) != hipSuccess)
-        return e;
-    if ((e = hipFuncSetAttribute((const void *)attn_bwd_dq_bf16_kernel<128>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 DqTile<128>::SMEM)) != hipSuccess)
-        return e;
-    return hipFuncSetAttribute((const void *)attn_bwd_dq_bf16_kernel<64>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, DqTile<64>::SMEM);
+    hipError_t e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<128>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, DkvTile<128>::SMEM);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<64>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, DkvTile<64>::SMEM);
 }
 
 }  // namespace fa

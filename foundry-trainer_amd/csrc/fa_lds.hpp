@@ -48,6 +48,26 @@ __device__ __forceinline__ void buffer_to_lds_4(__amdgpu_buffer_rsrc_t rsrc, cha
                                              voff, soff, 0, 0);
 }
 
+// Workgroup barrier that keeps buffer->LDS loads in flight.  __syncthreads()
+// drains every outstanding one (its workgroup release fence counts them as
+// pending LDS writes), which would cap a prefetch at one stage.  Here each
+// wave first waits until at most VM of its vector-memory loads are
+// outstanding (the DMA the next reads need has landed) and for its own LDS
+// reads, then meets the others; the "memory" clobbers keep the compiler from
+// moving LDS accesses across the barrier.
+template <int VM>
+__device__ __forceinline__ void barrier_keep_dma() {
+    static_assert(VM == 0 || VM == 2 || VM == 4, "vmcnt literal");
+    if constexpr (VM == 4)
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+    else if constexpr (VM == 2)
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Replace elements 4*half .. 4*half+3 of an MFMA operand with two packed words.
 __device__ __forceinline__ void set_half(bf16x8 &v, int half, u32x2 w) {
     u32x4 u = as_u32x4(v);
