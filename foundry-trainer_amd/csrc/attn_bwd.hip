@@ -94,15 +94,15 @@ struct DkvTile {
     static constexpr int LSE_OFF = 2 * T::BYTES;        // 64 f32
     static constexpr int DELTA_OFF = LSE_OFF + kQB * 4;  // 64 f32
     static constexpr int STAGE = DELTA_OFF + kQB * 4;
-    static constexpr int SMEM = 2 * STAGE;
     static constexpr int WI = T::WAVE_INSTS / 4;
 };
 
 template <int D>
-__device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, char *smem) {
+__device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
     using F = DkvTile<D>;
     using T = typename F::T;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nk = (S + kKT - 1) / kKT;
@@ -134,8 +134,11 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
     const uint32_t ovo = tile_src_off<D>(wave, lane, p.do_ss);
     const uint32_t qi_step = tile_inst_row_step<D>(p.q_ss), oi_step = tile_inst_row_step<D>(p.do_ss);
     const uint32_t qstep = (uint32_t)(kQB * p.q_ss * 2), ostep = (uint32_t)(kQB * p.do_ss * 2);
+    // one LDS object per stage: the compiler then keeps the prefetch DMA in
+    // flight across the transpose reads of the other stage
+    __shared__ __align__(16) char stage0[F::STAGE], stage1[F::STAGE];
     auto issue = [&](int qb, int buf) {
-        char *st = smem + buf * F::STAGE;
+        char *st = buf ? stage1 : stage0;
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
             buffer_to_lds_16(qrs, st + F::Q_OFF + (i * 4 + wave) * 1024, qvo, qb * qstep + i * qi_step);
@@ -150,7 +153,7 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
 
     // loop-invariant LDS operand offsets
     const RowFragAddr ra = row_frag_addr<D>(n, g);
-    const ColFragAddr ca0 = col_frag_addr<D>(0, lane), ca1 = col_frag_addr<D>(1, lane);
+    const ColFragAddr ca0 = col_frag_addr<D>(0, lane);
 
     f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
@@ -161,11 +164,12 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
 
     const int nqb = (S + kQB - 1) / kQB;
     issue(0, 0);
-    for (int qb = 0; qb < nqb; ++qb) {
+    auto stage = [&](auto par, int qb) {
+        constexpr int P = decltype(par)::value;  // qb % 2
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (qb + 1 < nqb) issue(qb + 1, (qb + 1) & 1);
-        const char *st = smem + (qb & 1) * F::STAGE;
+        if (qb + 1 < nqb) issue(qb + 1, P ^ 1);
+        const char *st = P ? stage1 : stage0;
         const char *qs_t = st + F::Q_OFF, *os_t = st + F::DO_OFF;
         const float *lse_s = reinterpret_cast<const float *>(st + F::LSE_OFF);
         const float *dlt_s = reinterpret_cast<const float *>(st + F::DELTA_OFF);
@@ -209,11 +213,15 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work, cha
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
                     const uint32_t o0 = col_frag_at(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
-                    const uint32_t o1 = col_frag_at(ca1, dt) + (sub * 2 + ks) * 16 * T::ROWB;
+                    const uint32_t o1 = col_frag_at_hi8<D>(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
                     dv[dt] = mfma_32x32x16(pf[ks], lds_read_col_frag(os_t, o0, o1), dv[dt]);
                     dk[dt] = mfma_32x32x16(df[ks], lds_read_col_frag(qs_t, o0, o1), dk[dt]);
                 }
         }
+    };
+    for (int qb = 0; qb < nqb; qb += 2) {
+        stage(std::integral_constant<int, 0>{}, qb);
+        if (qb + 1 < nqb) stage(std::integral_constant<int, 1>{}, qb + 1);
     }
 
     // accumulators: element r of lane = (key kt*128 + wave*32 + acc_row(r), d = dt*32 + n).
@@ -260,7 +268,8 @@ template <int D, bool KEEP>
 __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     using F = DqTile<D>;
     using T = typename F::T;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nq = (S + kQT - 1) / kQT;
@@ -435,8 +444,7 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
-    extern __shared__ __align__(16) char smem[];
-    dkdv_block<D>(p, xcd_remap(blockIdx.x, gridDim.x), smem);
+    dkdv_block<D>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
 template <int D, bool KEEP>
@@ -627,9 +635,9 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStr
     const int n_q = p.B * p.H * ((p.S + kQT - 1) / kQT);
     if (phase == 0 || phase == 2) {
         if (D == 128)
-            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, dim3(n_kv), block, DkvTile<128>::SMEM, s, p);
+            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, dim3(n_kv), block, 0, s, p);
         else
-            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, dim3(n_kv), block, DkvTile<64>::SMEM, s, p);
+            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, dim3(n_kv), block, 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (phase == 0 || phase == 3) {
@@ -671,12 +679,6 @@ hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStre
     return e;
 }
 
-hipError_t prepare_bwd_kernels() {
-    hipError_t e = hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<128>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, DkvTile<128>::SMEM);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)attn_bwd_dkdv_bf16_kernel<64>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, DkvTile<64>::SMEM);
-}
+hipError_t prepare_bwd_kernels() { return hipSuccess; }  // static LDS only
 
 }  // namespace fa

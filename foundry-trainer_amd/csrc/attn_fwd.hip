@@ -65,7 +65,8 @@ template <int D>
 __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0, int kb1, FwdState<D> &st) {
     using F = FwdTile<D>;
     using T = typename F::T;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nq = (S + kBM - 1) / kBM;
@@ -240,7 +241,8 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
 // O = O / l and LSE = (m_sc + log2 l) * ln 2 for query tile t.
 template <int D>
 __device__ __forceinline__ void fwd_store(const AttnFwdParams &p, int t, const FwdState<D> &st) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nq = (S + kBM - 1) / kBM;

@@ -55,18 +55,27 @@ __device__ __forceinline__ void buffer_to_lds_4(__amdgpu_buffer_rsrc_t rsrc, cha
 // outstanding (the DMA the next reads need has landed) and for its own LDS
 // reads, then meets the others; the "memory" clobbers keep the compiler from
 // moving LDS accesses across the barrier.
+#define FA_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ") lgkmcnt(0)" ::: "memory")
 template <int VM>
 __device__ __forceinline__ void barrier_keep_dma() {
-    static_assert(VM == 0 || VM == 2 || VM == 4, "vmcnt literal");
-    if constexpr (VM == 4)
-        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
-    else if constexpr (VM == 2)
-        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    static_assert(VM >= 0 && VM <= 12, "vmcnt literal");
+    if constexpr (VM == 0) FA_WAIT_VM(0);
+    else if constexpr (VM == 1) FA_WAIT_VM(1);
+    else if constexpr (VM == 2) FA_WAIT_VM(2);
+    else if constexpr (VM == 3) FA_WAIT_VM(3);
+    else if constexpr (VM == 4) FA_WAIT_VM(4);
+    else if constexpr (VM == 5) FA_WAIT_VM(5);
+    else if constexpr (VM == 6) FA_WAIT_VM(6);
+    else if constexpr (VM == 7) FA_WAIT_VM(7);
+    else if constexpr (VM == 8) FA_WAIT_VM(8);
+    else if constexpr (VM == 9) FA_WAIT_VM(9);
+    else if constexpr (VM == 10) FA_WAIT_VM(10);
+    else if constexpr (VM == 11) FA_WAIT_VM(11);
+    else FA_WAIT_VM(12);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
+#undef FA_WAIT_VM
 
 // Replace elements 4*half .. 4*half+3 of an MFMA operand with two packed words.
 __device__ __forceinline__ void set_half(bf16x8 &v, int half, u32x2 w) {
@@ -155,6 +164,13 @@ __device__ __forceinline__ ColFragAddr col_frag_addr(int half, int lane) {
 }
 __device__ __forceinline__ uint32_t col_frag_at(ColFragAddr a, int ft) {
     return a.base + (((uint32_t)(ft * 4) ^ a.key) << 4);
+}
+// The rows +8 half (col_frag_addr(1, lane)) from the rows +0 half: for D = 128
+// chunk_swz(r + 8) = chunk_swz(r) ^ 8 swaps feature tiles dt and dt ^ 2; for
+// D = 64 the key does not depend on row bit 3.
+template <int D>
+__device__ __forceinline__ uint32_t col_frag_at_hi8(ColFragAddr a0, int ft) {
+    return col_frag_at(a0, D >= 128 ? ft ^ 2 : ft) + 8 * 2 * D;
 }
 
 // Row fragment: row `row`, features kd*16 + g*8 .. +8.
