@@ -33,20 +33,29 @@ sys.path.insert(0, os.path.join(ROOT, "foundry-trainer_amd"))
 METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block steps/s"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-# HBM bytes per launch of a kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE
-# counter runs scaled by a copy kernel of known size (recorded in
-# profiles/; None until measured for that kernel and workload)
-TRAFFIC = {}
+# HBM bytes per launch of a kernel: rocprofv3 FETCH_SIZE and WRITE_SIZE runs
+# of this script (--calib-copy-mib 256), scaled by what the same counters read
+# for that 256 MiB copy (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, KiB).  Kept in
+# profiles/attn_c2_pmc.md; None for a kernel or workload not measured.
+TRAFFIC = {
+    ("c2", "attn_fwd"): int((2.0 * 53939.1 + 28911.8) * 1024),
+    ("c2", "attn_bwd_prepass"): int((2.0 * 29408.6 + 5760.2) * 1024),
+    ("c2", "attn_bwd_dkdv"): int((2.0 * 65962.7 + 56160.0) * 1024),
+    ("c2", "attn_bwd_dq"): int((2.0 * 70812.6 + 28386.0) * 1024),
+}
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c5"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 = skip)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB: the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to HBM bytes")
     return ap.parse_args()
 
 
@@ -119,6 +128,12 @@ def main():
 
     cfg = CONFIGS[args.config]
     torch.cuda.set_device(0)
+    if args.calib_copy_mib > 0:
+        src = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v, do, keep = make_inputs(cfg, torch, fa)
     lse = torch.empty((cfg.batch, cfg.heads, cfg.seq), dtype=torch.float32, device="cuda")
     o = torch.empty_like(q)
