@@ -30,7 +30,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "foundry-trainer_amd"))
 
-METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block steps/s"
+METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block steps/s"  # block: rec["block"]
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per launch of a kernel: rocprofv3 FETCH_SIZE and WRITE_SIZE runs
@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c5"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 = skip)")
+    ap.add_argument("--block-steps", type=int, default=10,
+                    help="timed c4 LoRA block steps (0 = skip the block measurement)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to HBM bytes")
@@ -79,6 +81,47 @@ def make_inputs(cfg, torch, fa):
         keep = torch.from_numpy(cfg.key_keep()).to("cuda")
         do = do * keep[:, :, None, None].to(bf)
     return q, k, v, do, keep
+
+
+def block_bench(torch, steps: int, warmup: int):
+    """c4: one double-stream LoRA block training step (forward, backward to
+    the LoRA factors, AdamW) per step, img 4096 + txt 512 tokens, dim 3072,
+    24 x 128 heads, MLP 4x tanh-GELU, LoRA r16 on q/k/v/out of both streams;
+    synthetic N(0,1) inputs, conditioning and dY; random-init weights."""
+    from foundry_attn import block as fb
+    from foundry_attn.configs import C4
+    rows = int(round(C4.img_tokens ** 0.5))
+    blk = fb.random_block(C4.hidden, C4.heads, C4.txt_tokens, rows, C4.img_tokens // rows, C4.mlp_ratio,
+                          C4.lora_rank, C4.lora_alpha)
+    g = torch.Generator(device="cuda").manual_seed(20261028)
+    blk.set_conditioning(torch.randn(C4.hidden, device="cuda", generator=g).to(torch.bfloat16))
+    x = {"img": torch.randn(C4.img_tokens, C4.hidden, device="cuda", generator=g).to(torch.bfloat16),
+         "txt": torch.randn(C4.txt_tokens, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)}
+    dy = {k: torch.randn(v.shape, device="cuda", generator=g).to(torch.bfloat16) for k, v in x.items()}
+    for _ in range(warmup):
+        blk.train_step(x, dy)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        blk.train_step(x, dy)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    gpu = e0.elapsed_time(e1) * 1e-3 / steps
+    N, C, F, S, H, D, r = (C4.img_tokens + C4.txt_tokens, C4.hidden, C4.mlp_ratio * C4.hidden,
+                           C4.img_tokens + C4.txt_tokens, C4.heads, C4.head_dim, C4.lora_rank)
+    gemm_fwd = 2 * N * C * 3 * C + 2 * N * C * C + 2 * 2 * N * C * F
+    gemm_bwd = 2 * 2 * N * C * F + 2 * N * C * C  # dX of the MLP and out projections only
+    attn = 14 * H * S * S * D
+    lora = 4 * (2 * N * r * (C + C)) * 3  # fwd + 2 bwd GEMM pairs per adapter, 4 adapters per stream
+    flops = gemm_fwd + gemm_bwd + attn + lora
+    return {"workload": "c4: double-stream LoRA block step (fwd + bwd + AdamW), img 4096 + txt 512 tokens, "
+                        "dim 3072, 24x128 heads, MLP 4x tanh-GELU, LoRA r16 on q/k/v/out of both streams",
+            "steps": steps, "warmup": warmup, "steps_per_s": round(1.0 / wall, 2),
+            "ms_per_step": round(wall * 1e3, 3), "gpu_ms_per_step": round(gpu * 1e3, 3),
+            "tflops": round(flops / wall / 1e12, 1), "step_tflop": round(flops / 1e12, 3)}
 
 
 def cpu_baseline(cfg, budget_s: float):
@@ -233,6 +276,8 @@ def main():
                      "traffic": TRAFFIC.get((cfg.name, dominant))},
         "kernels": kernels,
     }
+    if args.block_steps > 0:
+        rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
     if args.cpu_seconds > 0:
         rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     else:

@@ -1,0 +1,294 @@
+// Memory-bound kernels of foundry-spike's double-stream LoRA block (the
+// pieces around the attention and the frozen linears):
+//   LayerNorm-modulation   y = (1 + scale) * LN(x) + shift    (lib.rs:60-71)
+//   its backward           dx = dres + rstd*(dn - mean(dn) - n*mean(dn*n)),
+//                          dn = dy * (1 + scale)
+//   gated residual         y = x + g * b, g broadcast over rows
+//                          (throughput.rs:552-572)
+//   tanh-GELU and its derivative (the c4 block's MLP activation; the
+//                          reference block uses SwiGLU, lib.rs:293-297)
+//   SiLU                   of the conditioning vector (throughput.rs:297-324)
+//   AdamW step             lib.rs:477-510, operation for operation
+// All are HBM-bound: rows move with 16-byte vector accesses, statistics are
+// f32, results are rounded once to the storage type.
+#include <math.h>
+
+#include "fa_device.hpp"
+#include "fa_kernels.hpp"
+
+namespace fa {
+namespace {
+
+// 8 consecutive elements <-> f32 (bf16: one 16-byte access, f32: two)
+__device__ __forceinline__ void load8(const bf16 *p, float v[8]) {
+    const bf16x8 a = as_bf16x8(ld_global_16(p));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (float)a[j];
+}
+__device__ __forceinline__ void load8(const float *p, float v[8]) {
+    const f32x4 a = __builtin_bit_cast(f32x4, ld_global_16(p));
+    const f32x4 b = __builtin_bit_cast(f32x4, ld_global_16(p + 4));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = a[j];
+        v[4 + j] = b[j];
+    }
+}
+__device__ __forceinline__ void store8(bf16 *p, const float v[8]) {
+    bf16x8 a;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = f32_to_bf16(v[j]);
+    *reinterpret_cast<bf16x8 *>(p) = a;
+}
+__device__ __forceinline__ void store8(float *p, const float v[8]) {
+    *reinterpret_cast<f32x4 *>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4 *>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+__device__ __forceinline__ float wave_sum(float s) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    return s;
+}
+
+// One wave per row; lane l holds elements k*512 + 8*l .. +8 for k < MAXCH.
+template <typename T, int MAXCH>
+__global__ __launch_bounds__(256) void ln_mod_fwd_kernel(LnModParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.N) return;
+    const int C = p.C;
+    const T *x = static_cast<const T *>(p.x) + row * p.ldx;
+    float v[MAXCH][8];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXCH; ++k) {
+        const int e = k * 512 + lane * 8;
+        if (e < C) {
+            load8(x + e, v[k]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += v[k][j];
+        }
+    }
+    const float mean = wave_sum(s) / (float)C;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXCH; ++k) {
+        const int e = k * 512 + lane * 8;
+        if (e < C) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float d = v[k][j] - mean;
+                q += d * d;
+            }
+        }
+    }
+    const float var = wave_sum(q) / (float)C;
+    const float den = sqrtf(var + p.eps);
+    const T *shift = static_cast<const T *>(p.shift), *scale = static_cast<const T *>(p.scale);
+    T *y = static_cast<T *>(p.y) + row * p.ldy;
+#pragma unroll
+    for (int k = 0; k < MAXCH; ++k) {
+        const int e = k * 512 + lane * 8;
+        if (e < C) {
+            float sh[8], sc[8], o[8];
+            load8(shift + e, sh);
+            load8(scale + e, sc);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = (v[k][j] - mean) / den * (sc[j] + 1.f) + sh[j];
+            store8(y + e, o);
+        }
+    }
+    if (lane == 0 && p.mean) {
+        p.mean[row] = mean;
+        p.rstd[row] = 1.f / den;
+    }
+}
+
+template <typename T, int MAXCH>
+__global__ __launch_bounds__(256) void ln_mod_bwd_kernel(LnModParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.N) return;
+    const int C = p.C;
+    const T *x = static_cast<const T *>(p.x) + row * p.ldx;
+    const T *dy = static_cast<const T *>(p.dy) + row * p.lddy;
+    const T *scale = static_cast<const T *>(p.scale);
+    const float mean = p.mean[row], rstd = p.rstd[row];
+    float n[MAXCH][8], dn[MAXCH][8];
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXCH; ++k) {
+        const int e = k * 512 + lane * 8;
+        if (e < C) {
+            float xv[8], gv[8], sc[8];
+            load8(x + e, xv);
+            load8(dy + e, gv);
+            load8(scale + e, sc);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                n[k][j] = (xv[j] - mean) * rstd;
+                dn[k][j] = gv[j] * (sc[j] + 1.f);
+                a += dn[k][j];
+                b += dn[k][j] * n[k][j];
+            }
+        }
+    }
+    const float ma = wave_sum(a) / (float)C, mb = wave_sum(b) / (float)C;
+    const T *dres = static_cast<const T *>(p.dres);
+    T *dx = static_cast<T *>(p.dx) + row * p.lddx;
+#pragma unroll
+    for (int k = 0; k < MAXCH; ++k) {
+        const int e = k * 512 + lane * 8;
+        if (e < C) {
+            float o[8], r[8];
+            if (dres) {
+                load8(dres + row * p.ldres + e, r);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) r[j] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = r[j] + rstd * (dn[k][j] - ma - n[k][j] * mb);
+            store8(dx + e, o);
+        }
+    }
+}
+
+// Elementwise over an [N, C] view, 8 elements per thread (C % 8 == 0).
+// op 0: y = x + g * b (x may be null: y = g * b);  1: y = gelu(b);
+// op 2: y = x * gelu'(b) (x = upstream gradient);  3: y = silu(b)
+// gelu(u) = u/2 * (1 + tanh(k0 * (u + k1 u^3))), tanh(z) = 1 - 2/(1 + e^{2z})
+constexpr float kGeluK0 = 0.7978845608028654f;  // sqrt(2/pi)
+constexpr float kGeluK1 = 0.044715f;
+
+__device__ __forceinline__ float tanh_via_exp(float z) {
+    return 1.f - 2.f / (1.f + exp2_fast(2.f * kLog2e * z));
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void elementwise_kernel(EltParams p) {
+    const int64_t per_row = p.C / 8;
+    const int64_t total = (int64_t)p.N * per_row;
+    const T *g = static_cast<const T *>(p.g);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t row = i / per_row;
+        const int e = (int)(i - row * per_row) * 8;
+        float bv[8], o[8];
+        load8(static_cast<const T *>(p.b) + row * p.ldb + e, bv);
+        if constexpr (OP == 0) {
+            float gv[8], xv[8];
+            load8(g + e, gv);
+            if (p.x) {
+                load8(static_cast<const T *>(p.x) + row * p.ldx + e, xv);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xv[j] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = xv[j] + gv[j] * bv[j];
+        } else if constexpr (OP == 1) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float u = bv[j];
+                o[j] = 0.5f * u * (1.f + tanh_via_exp(kGeluK0 * (u + kGeluK1 * u * u * u)));
+            }
+        } else if constexpr (OP == 2) {
+            float xv[8];
+            load8(static_cast<const T *>(p.x) + row * p.ldx + e, xv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float u = bv[j];
+                const float t = tanh_via_exp(kGeluK0 * (u + kGeluK1 * u * u * u));
+                const float d = 0.5f * (1.f + t) + 0.5f * u * (1.f - t * t) * kGeluK0 * (1.f + 3.f * kGeluK1 * u * u);
+                o[j] = xv[j] * d;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = bv[j] / (1.f + exp2_fast(-kLog2e * bv[j]));
+        }
+        store8(static_cast<T *>(p.y) + row * p.ldy + e, o);
+    }
+}
+
+// AdamW, weight decay 0, in the reference's operation order:
+//   m' = m*b1 + g*(1-b1);  v' = v*b2 + (g*g)*(1-b2)
+//   p' = p - ((m' * ibc1) / (sqrt(v' * ibc2) + eps)) * lr
+// each product / sum rounded separately (contraction off for the
+// expressions written here), IEEE sqrt and division, p' rounded to T.
+template <typename T>
+__global__ __launch_bounds__(256) void adamw_kernel(AdamwParams p) {
+#pragma clang fp contract(off)
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < p.n; i += (int64_t)gridDim.x * 256) {
+        const float g = p.grad[i];
+        const float m = p.m[i] * p.b1 + g * p.one_m_b1;
+        const float gg = g * g;
+        const float v = p.v[i] * p.b2 + gg * p.one_m_b2;
+        const float mhat = m * p.ibc1;
+        const float den = sqrtf(v * p.ibc2) + p.eps;
+        const float delta = (mhat / den) * p.lr;
+        T *w = static_cast<T *>(p.param);
+        w[i] = (T)((float)w[i] - delta);
+        p.m[i] = m;
+        p.v[i] = v;
+    }
+}
+
+inline int elt_grid(int64_t n8) {
+    const int64_t blocks = (n8 + 255) / 256;
+    return (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
+}
+
+}  // namespace
+
+template <typename T>
+static hipError_t ln_fwd_t(const LnModParams &p, hipStream_t s) {
+    const dim3 grid((unsigned)((p.N + 3) / 4)), block(256);
+    if (p.C <= 1024)
+        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 2>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 8>), grid, block, 0, s, p);
+    return hipGetLastError();
+}
+template <typename T>
+static hipError_t ln_bwd_t(const LnModParams &p, hipStream_t s) {
+    const dim3 grid((unsigned)((p.N + 3) / 4)), block(256);
+    if (p.C <= 1024)
+        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 2>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 8>), grid, block, 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_mod_fwd(const LnModParams &p, int dtype, hipStream_t s) {
+    return dtype == 0 ? ln_fwd_t<bf16>(p, s) : ln_fwd_t<float>(p, s);
+}
+hipError_t launch_ln_mod_bwd(const LnModParams &p, int dtype, hipStream_t s) {
+    return dtype == 0 ? ln_bwd_t<bf16>(p, s) : ln_bwd_t<float>(p, s);
+}
+
+template <typename T>
+static hipError_t elt_t(const EltParams &p, int op, hipStream_t s) {
+    const dim3 grid(elt_grid((int64_t)p.N * (p.C / 8))), block(256);
+    switch (op) {
+        case 0: hipLaunchKernelGGL((elementwise_kernel<T, 0>), grid, block, 0, s, p); break;
+        case 1: hipLaunchKernelGGL((elementwise_kernel<T, 1>), grid, block, 0, s, p); break;
+        case 2: hipLaunchKernelGGL((elementwise_kernel<T, 2>), grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL((elementwise_kernel<T, 3>), grid, block, 0, s, p); break;
+    }
+    return hipGetLastError();
+}
+hipError_t launch_elementwise(const EltParams &p, int op, int dtype, hipStream_t s) {
+    return dtype == 0 ? elt_t<bf16>(p, op, s) : elt_t<float>(p, op, s);
+}
+
+hipError_t launch_adamw(const AdamwParams &p, int dtype, hipStream_t s) {
+    const dim3 grid(elt_grid(p.n)), block(256);
+    if (dtype == 0)
+        hipLaunchKernelGGL((adamw_kernel<bf16>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((adamw_kernel<float>), grid, block, 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace fa

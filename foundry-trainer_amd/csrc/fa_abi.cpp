@@ -11,6 +11,7 @@
 #include <mutex>
 
 #include "../../include/foundry_attn.h"
+#include "../../include/foundry_block.h"
 #include "fa_kernels.hpp"
 
 namespace {
@@ -439,6 +440,160 @@ fa_status fa_lora_bwd(const fa_lora_bwd_args *a, void *stream) {
     p.work = static_cast<float *>(a->workspace);
     const hipError_t e = fa::launch_lora_bwd(p, a->fwd.dtype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lora backward launch");
+    return ok();
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Block ops (include/foundry_block.h)
+// ---------------------------------------------------------------------------
+namespace {
+
+size_t dtype_bytes(int32_t dt) { return dt == FA_DTYPE_BF16 ? 2 : 4; }
+
+fa_status check_row_view(const char *name, const void *p, int64_t ld, int32_t cols, int32_t dtype) {
+    if (!p) return fail(FA_ERR_INVALID_ARG, "%s is NULL", name);
+    if (!aligned(p, 16)) return fail(FA_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
+    if (ld < cols || (ld * (int64_t)dtype_bytes(dtype)) % 16)
+        return fail(FA_ERR_INVALID_ARG, "%s: ld %lld must be >= cols %d and keep rows 16-byte aligned", name,
+                    (long long)ld, cols);
+    return FA_OK;
+}
+fa_status check_vec(const char *name, const void *p) {
+    if (!p || !aligned(p, 16)) return fail(FA_ERR_INVALID_ARG, "%s is NULL or not 16-byte aligned", name);
+    return FA_OK;
+}
+fa_status check_rows_shape(int32_t dtype, int32_t rows, int32_t cols, int32_t max_cols) {
+    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32) return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (rows < 1 || cols < 8 || cols % 8 || cols > max_cols)
+        return fail(FA_ERR_INVALID_ARG, "rows %d / cols %d: need rows >= 1, 8 <= cols <= %d, cols %% 8 == 0", rows,
+                    cols, max_cols);
+    return FA_OK;
+}
+
+fa_status rows_op(const fa_rows_args *a, int op, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_rows_shape(a->dtype, a->rows, a->cols, 1 << 30));
+    FA_TRY(check_row_view("b", a->b, a->ldb, a->cols, a->dtype));
+    FA_TRY(check_row_view("y", a->y, a->ldy, a->cols, a->dtype));
+    if (op == 0) FA_TRY(check_vec("g", a->g));
+    if (op == 2 || (op == 0 && a->x)) FA_TRY(check_row_view("x", a->x, a->ldx, a->cols, a->dtype));
+    FA_TRY(init_current());
+    fa::EltParams p{};
+    p.x = (op == 0 || op == 2) ? a->x : nullptr;
+    p.ldx = a->ldx;
+    p.g = a->g;
+    p.b = a->b;
+    p.ldb = a->ldb;
+    p.y = a->y;
+    p.ldy = a->ldy;
+    p.N = a->rows;
+    p.C = a->cols;
+    const hipError_t e = fa::launch_elementwise(p, op, a->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "elementwise launch");
+    return ok();
+}
+
+fa_status check_ln(const fa_ln_mod_args *a) {
+    FA_TRY(check_rows_shape(a->dtype, a->rows, a->cols, 4096));
+    if (!(a->eps > 0.f) || !isfinite(a->eps)) return fail(FA_ERR_INVALID_ARG, "eps must be finite and > 0");
+    FA_TRY(check_row_view("x", a->x, a->ldx, a->cols, a->dtype));
+    FA_TRY(check_vec("shift", a->shift));
+    FA_TRY(check_vec("scale", a->scale));
+    return FA_OK;
+}
+
+fa::LnModParams ln_params(const fa_ln_mod_args *a) {
+    fa::LnModParams p{};
+    p.x = a->x;
+    p.ldx = a->ldx;
+    p.shift = a->shift;
+    p.scale = a->scale;
+    p.y = a->y;
+    p.ldy = a->ldy;
+    p.mean = a->mean;
+    p.rstd = a->rstd;
+    p.N = a->rows;
+    p.C = a->cols;
+    p.eps = a->eps;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+fa_status fa_ln_mod_fwd(const fa_ln_mod_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_ln(a));
+    FA_TRY(check_row_view("y", a->y, a->ldy, a->cols, a->dtype));
+    if ((a->mean == nullptr) != (a->rstd == nullptr))
+        return fail(FA_ERR_INVALID_ARG, "mean and rstd must both be given or both NULL");
+    if (a->mean && (!aligned(a->mean, 4) || !aligned(a->rstd, 4)))
+        return fail(FA_ERR_INVALID_ARG, "mean/rstd misaligned");
+    FA_TRY(init_current());
+    const hipError_t e = fa::launch_ln_mod_fwd(ln_params(a), a->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "layer-norm-mod launch");
+    return ok();
+}
+
+fa_status fa_ln_mod_bwd(const fa_ln_mod_bwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_ln(&a->fwd));
+    if (!a->fwd.mean || !a->fwd.rstd || !aligned(a->fwd.mean, 4) || !aligned(a->fwd.rstd, 4))
+        return fail(FA_ERR_INVALID_ARG, "mean and rstd (from the forward) are required");
+    FA_TRY(check_row_view("dy", a->dy, a->lddy, a->fwd.cols, a->fwd.dtype));
+    FA_TRY(check_row_view("dx", a->dx, a->lddx, a->fwd.cols, a->fwd.dtype));
+    if (a->dres) FA_TRY(check_row_view("dres", a->dres, a->ldres, a->fwd.cols, a->fwd.dtype));
+    FA_TRY(init_current());
+    fa::LnModParams p = ln_params(&a->fwd);
+    p.dy = a->dy;
+    p.lddy = a->lddy;
+    p.dres = a->dres;
+    p.ldres = a->ldres;
+    p.dx = a->dx;
+    p.lddx = a->lddx;
+    const hipError_t e = fa::launch_ln_mod_bwd(p, a->fwd.dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "layer-norm-mod backward launch");
+    return ok();
+}
+
+fa_status fa_gated_residual(const fa_rows_args *a, void *stream) { return rows_op(a, 0, stream); }
+fa_status fa_gelu_fwd(const fa_rows_args *a, void *stream) { return rows_op(a, 1, stream); }
+fa_status fa_gelu_bwd(const fa_rows_args *a, void *stream) { return rows_op(a, 2, stream); }
+fa_status fa_silu(const fa_rows_args *a, void *stream) { return rows_op(a, 3, stream); }
+
+fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)
+        return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", a->dtype);
+    if (a->n < 1) return fail(FA_ERR_INVALID_ARG, "n must be >= 1");
+    if (a->step < 1) return fail(FA_ERR_INVALID_ARG, "step must be >= 1");
+    if (!a->param || !a->grad || !a->m || !a->v || !aligned(a->param, dtype_bytes(a->dtype)) ||
+        !aligned(a->grad, 4) || !aligned(a->m, 4) || !aligned(a->v, 4))
+        return fail(FA_ERR_INVALID_ARG, "param/grad/m/v is NULL or misaligned");
+    if (!(a->lr >= 0.0) || !(a->beta1 >= 0.0 && a->beta1 < 1.0) || !(a->beta2 >= 0.0 && a->beta2 < 1.0) ||
+        !(a->eps > 0.0))
+        return fail(FA_ERR_INVALID_ARG, "need lr >= 0, 0 <= beta < 1, eps > 0");
+    FA_TRY(init_current());
+    fa::AdamwParams p{};
+    p.param = a->param;
+    p.grad = a->grad;
+    p.m = a->m;
+    p.v = a->v;
+    p.n = a->n;
+    const double b1 = a->beta1, b2 = a->beta2;
+    p.lr = (float)a->lr;
+    p.b1 = (float)b1;
+    p.b2 = (float)b2;
+    p.one_m_b1 = (float)(1.0 - b1);
+    p.one_m_b2 = (float)(1.0 - b2);
+    p.eps = (float)a->eps;
+    p.ibc1 = (float)(1.0 / (1.0 - pow(b1, a->step)));
+    p.ibc2 = (float)(1.0 / (1.0 - pow(b2, a->step)));
+    const hipError_t e = fa::launch_adamw(p, a->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "adamw launch");
     return ok();
 }
 

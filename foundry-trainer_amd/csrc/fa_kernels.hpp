@@ -89,4 +89,47 @@ struct LoraParams {
 hipError_t launch_lora_fwd(const LoraParams &p, int dtype, hipStream_t s);
 hipError_t launch_lora_bwd(const LoraParams &p, int dtype, hipStream_t s);
 
+// LayerNorm-modulation over [N, C] rows (C % 8 == 0, C <= 4096).
+struct LnModParams {
+    const void *x;
+    int64_t ldx;
+    const void *shift, *scale;  // [C]
+    void *y;
+    int64_t ldy;
+    float *mean, *rstd;  // [N]: written by fwd (optional), read by bwd
+    const void *dy;      // bwd
+    int64_t lddy;
+    const void *dres;  // bwd: residual gradient added to dx (optional)
+    int64_t ldres;
+    void *dx;
+    int64_t lddx;
+    int N, C;
+    float eps;
+};
+hipError_t launch_ln_mod_fwd(const LnModParams &p, int dtype, hipStream_t s);
+hipError_t launch_ln_mod_bwd(const LnModParams &p, int dtype, hipStream_t s);
+
+// Elementwise ops over an [N, C] view (C % 8 == 0): 0 gated residual
+// y = x + g*b, 1 y = gelu(b), 2 y = x * gelu'(b), 3 y = silu(b).
+struct EltParams {
+    const void *x;
+    int64_t ldx;
+    const void *g;  // [C]
+    const void *b;
+    int64_t ldb;
+    void *y;
+    int64_t ldy;
+    int N, C;
+};
+hipError_t launch_elementwise(const EltParams &p, int op, int dtype, hipStream_t s);
+
+struct AdamwParams {
+    void *param;        // dtype of the op
+    const float *grad;  // f32
+    float *m, *v;       // f32 moments
+    int64_t n;
+    float lr, b1, b2, one_m_b1, one_m_b2, eps, ibc1, ibc2;
+};
+hipError_t launch_adamw(const AdamwParams &p, int dtype, hipStream_t s);
+
 }  // namespace fa

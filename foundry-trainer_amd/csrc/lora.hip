@@ -12,10 +12,15 @@
 //           dx += du A): one thread per output column and row phase, Wt rows
 //           staged in LDS.  HBM-bound: one read and one write of Y.
 //   colsum  out[j][c] = s * sum_n U[n][j] X[n][c]      (dB^T = s u^T dy and
-//           dA = du^T x): each workgroup owns 64 columns and sweeps all rows
-//           in a fixed order — deterministic, no atomics.
+//           dA = du^T x).  bf16: a skinny MFMA GEMM, X^T (by transpose reads
+//           of 64-token x 128-column tiles streamed into LDS) times U^T (bf16,
+//           tokens contiguous), split over tokens; the splits are summed in a
+//           fixed order by a second kernel — deterministic, no atomics.  f32
+//           (the parity path): each workgroup owns 64 columns and sweeps all
+//           rows in a fixed order.
 #include "fa_device.hpp"
 #include "fa_kernels.hpp"
+#include "fa_lds.hpp"
 
 namespace fa {
 namespace {
@@ -128,6 +133,96 @@ __global__ __launch_bounds__(256) void lora_colsum_kernel(const float *__restric
                 s * (((part[0][cl][j] + part[1][cl][j]) + part[2][cl][j]) + part[3][cl][j]);
 }
 
+// ---- colsum, bf16 (MFMA) ------------------------------------------------
+// U^T in the MFMA operand order: ut[j][n'] for j < 32, n' < npad (multiple of
+// 64), bf16.  Within each 16-token group the tokens are stored as
+// {0..3, 8..11, 4..7, 12..15}: lane half g of the B operand then reads its 8
+// values {4g..4g+3, 8+4g..8+4g+3} — the k order of the transpose-read A
+// operand — as one 16-byte chunk.  Rows j >= R and tokens >= N are zero.
+__global__ void lora_ut_kernel(const float *__restrict__ U, int64_t ldu, bf16 *ut, int N, int R, int npad) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)32 * npad) return;
+    const int j = (int)(e / npad), p = (int)(e % npad);
+    const int grp = p >> 4, q = p & 15;
+    const int n = grp * 16 + ((q & 4) ? 8 : 0) + ((q & 8) ? 4 : 0) + (q & 3);
+    ut[e] = f32_to_bf16(j < R && n < N ? U[(int64_t)n * ldu + j] : 0.f);
+}
+
+constexpr int kCsCols = 128;  // columns per workgroup (4 waves x 32)
+constexpr int kCsRows = 64;   // tokens per LDS stage
+
+// Workgroup (column tile ct, token split sp): part[sp][c][j] = sum over the
+// split's tokens of X[n][c] U[n][j], for the tile's 128 columns and j < 32.
+__global__ __launch_bounds__(256) void lora_colsum_mfma_kernel(const bf16 *__restrict__ X, int64_t ldx,
+                                                               const bf16 *__restrict__ ut, int npad,
+                                                               float *part, int N, int C, int chunk) {
+    using T = LdsTile<128, kCsRows>;
+    constexpr int WI = T::WAVE_INSTS / 4;
+    __shared__ __align__(16) char st0[T::BYTES], st1[T::BYTES];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int c0 = blockIdx.x * kCsCols;
+    const int t_begin = blockIdx.y * chunk, t_end = min(t_begin + chunk, npad);
+    // rows >= N (and, in the last row, columns >= C) read as zero
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X + c0, (uint32_t)(((int64_t)(N - 1) * ldx + (C - c0)) * 2));
+    const uint32_t xvo = tile_src_off<128>(wave, lane, ldx);
+    const uint32_t row_step = tile_inst_row_step<128>(ldx);
+    const uint32_t stage_step = (uint32_t)(kCsRows * ldx * 2);
+    auto issue = [&](int t0, char *dst) {
+#pragma unroll
+        for (int i = 0; i < WI; ++i)
+            buffer_to_lds_16(xrs, dst + (i * 4 + wave) * 1024, xvo, (uint32_t)(t0 / kCsRows) * stage_step + i * row_step);
+    };
+    uint32_t coff[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) coff[dt] = col_frag_off<128>(0, 0, dt, lane);
+    const bf16 *ub = ut + (int64_t)n * npad + g * 8;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    auto stage = [&](const char *tile, int t0) {
+#pragma unroll
+        for (int ks = 0; ks < kCsRows / 16; ++ks) {
+            const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
+                                               col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
+            const bf16x8 b = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
+            acc = mfma_32x32x16(a, b, acc);
+        }
+    };
+    issue(t_begin, st0);
+    for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
+        barrier_keep_dma<0>();
+        if (t0 + kCsRows < t_end) issue(t0 + kCsRows, st1);
+        stage(st0, t0);
+        if (t0 + kCsRows < t_end) {
+            barrier_keep_dma<0>();
+            if (t0 + 2 * kCsRows < t_end) issue(t0 + 2 * kCsRows, st0);
+            stage(st1, t0 + kCsRows);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // acc element r: column c0 + wave*32 + acc_row(r, lane), j = n
+    float *pp = part + (int64_t)blockIdx.y * C * 32;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int c = c0 + wave * 32 + acc_row(r, lane);
+        if (c < C) pp[(int64_t)c * 32 + n] = acc[r];
+    }
+}
+
+// out[j * os_j + c * os_c] = s * sum_sp part[sp][c][j] (fixed order), j < R.
+__global__ void lora_colsum_reduce_kernel(const float *__restrict__ part, float *out, int64_t os_j,
+                                          int64_t os_c, int C, int R, int splits, float s) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)C * 32) return;
+    const int c = (int)(e >> 5), j = (int)(e & 31);
+    if (j >= R) return;
+    float acc = 0.f;
+    for (int sp = 0; sp < splits; ++sp) acc += part[(int64_t)sp * C * 32 + e];
+    out[j * os_j + (int64_t)c * os_c] = s * acc;
+}
+
 // Small transpose [R][C] -> [C][R] (dtype).
 template <typename T>
 __global__ void lora_transpose_kernel(const T *__restrict__ src, T *dst, int R, int C) {
@@ -152,6 +247,32 @@ hipError_t expand(const float *U, int64_t ldu, const T *Wt, T *Y, int64_t ldy, i
     const dim3 grid((C + 63) / 64, (N + rpb - 1) / rpb), block(256);
     hipLaunchKernelGGL(lora_expand_kernel<T>, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s,
                        rpb);
+    return hipGetLastError();
+}
+
+// Token splits of the bf16 colsum: enough workgroups to fill the GPU, each
+// split a multiple of 64 tokens.
+inline int colsum_splits(int N, int C) {
+    const int tiles = (C + kCsCols - 1) / kCsCols;
+    const int stages = (N + kCsRows - 1) / kCsRows;
+    int sp = (512 + tiles - 1) / tiles;
+    if (sp > stages) sp = stages;
+    return sp < 1 ? 1 : sp;
+}
+inline int colsum_npad(int N) { return (N + kCsRows - 1) / kCsRows * kCsRows; }
+
+// bf16: U (f32 [N, R]) -> ut (bf16, operand order) -> split partials -> out.
+hipError_t colsum_bf16(const float *U, int64_t ldu, const bf16 *X, int64_t ldx, float *out, int64_t os_j,
+                       int64_t os_c, int N, int C, int R, float s, bf16 *ut, float *part, hipStream_t st) {
+    const int npad = colsum_npad(N), splits = colsum_splits(N, C);
+    const int stages = npad / kCsRows;
+    const int chunk = (stages + splits - 1) / splits * kCsRows;
+    hipLaunchKernelGGL(lora_ut_kernel, dim3((unsigned)((32 * (int64_t)npad + 255) / 256)), dim3(256), 0, st, U,
+                       ldu, ut, N, R, npad);
+    hipLaunchKernelGGL(lora_colsum_mfma_kernel, dim3((unsigned)((C + kCsCols - 1) / kCsCols), (unsigned)splits),
+                       dim3(256), 0, st, X, ldx, ut, npad, part, N, C, chunk);
+    hipLaunchKernelGGL(lora_colsum_reduce_kernel, dim3((unsigned)((C * 32 + 255) / 256)), dim3(256), 0, st, part,
+                       out, os_j, os_c, C, R, splits, s);
     return hipGetLastError();
 }
 
@@ -182,29 +303,42 @@ hipError_t lora_fwd_t(const LoraParams &p, hipStream_t st) {
                      p.r, p.scale, st);
 }
 
-// Workspace layout (bytes, each 256-aligned): du f32 [N, r] | B^T [r, M] | A^T [K, r]
+inline size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Workspace layout (bytes, each 256-aligned): du f32 [N, r] | B^T [r, M] |
+// A^T [K, r] | bf16 colsum only: ut bf16 [32, npad] | partials f32
+// [splits(N, C) * C * 32], the larger of C = K and C = M
 template <typename T>
 hipError_t lora_bwd_t(const LoraParams &p, hipStream_t st) {
     char *ws = reinterpret_cast<char *>(p.work);
     float *du = reinterpret_cast<float *>(ws);
-    const size_t du_b = ((size_t)p.N * p.r * 4 + 255) & ~size_t(255);
+    const size_t du_b = al256((size_t)p.N * p.r * 4);
     T *bt = reinterpret_cast<T *>(ws + du_b);
-    const size_t bt_b = ((size_t)p.r * p.M * sizeof(T) + 255) & ~size_t(255);
+    const size_t bt_b = al256((size_t)p.r * p.M * sizeof(T));
     T *at = reinterpret_cast<T *>(ws + du_b + bt_b);
+    const size_t at_b = al256((size_t)p.K * p.r * sizeof(T));
+    bf16 *ut = reinterpret_cast<bf16 *>(ws + du_b + bt_b + at_b);
+    float *part = reinterpret_cast<float *>(ws + du_b + bt_b + at_b + al256((size_t)32 * colsum_npad(p.N) * 2));
     hipError_t e;
     // dB[o][j] = s * sum_n dy[n][o] u[n][j]
-    if ((e = colsum<T>(p.u, p.r, static_cast<const T *>(p.dy), p.lddy, p.db, 1, p.r, p.N, p.M, p.r,
-                       p.scale, st)) != hipSuccess)
-        return e;
+    if constexpr (sizeof(T) == 2)
+        e = colsum_bf16(p.u, p.r, static_cast<const bf16 *>(p.dy), p.lddy, p.db, 1, p.r, p.N, p.M, p.r, p.scale,
+                        ut, part, st);
+    else
+        e = colsum<T>(p.u, p.r, static_cast<const T *>(p.dy), p.lddy, p.db, 1, p.r, p.N, p.M, p.r, p.scale, st);
+    if (e != hipSuccess) return e;
     // du = s * dy B  (B^T as the [r, M] row operand)
     if ((e = transpose<T>(static_cast<const T *>(p.b), bt, p.M, p.r, st)) != hipSuccess) return e;
     if ((e = rowdot<T>(static_cast<const T *>(p.dy), p.lddy, bt, du, p.r, p.N, p.M, p.r, p.scale,
                        st)) != hipSuccess)
         return e;
     // dA[j][k] = sum_n du[n][j] x[n][k]
-    if ((e = colsum<T>(du, p.r, static_cast<const T *>(p.x), p.ldx, p.da, p.K, 1, p.N, p.K, p.r,
-                       1.f, st)) != hipSuccess)
-        return e;
+    if constexpr (sizeof(T) == 2)
+        e = colsum_bf16(du, p.r, static_cast<const bf16 *>(p.x), p.ldx, p.da, p.K, 1, p.N, p.K, p.r, 1.f, ut,
+                        part, st);
+    else
+        e = colsum<T>(du, p.r, static_cast<const T *>(p.x), p.ldx, p.da, p.K, 1, p.N, p.K, p.r, 1.f, st);
+    if (e != hipSuccess) return e;
     if (p.dx) {
         // dx += du A  (A^T [K, r] as Wt)
         if ((e = transpose<T>(static_cast<const T *>(p.a), at, p.r, p.K, st)) != hipSuccess) return e;
@@ -218,10 +352,11 @@ hipError_t lora_bwd_t(const LoraParams &p, hipStream_t st) {
 }  // namespace
 
 size_t lora_bwd_workspace_bytes(int N, int K, int M, int r, int elt) {
-    const size_t du_b = ((size_t)N * r * 4 + 255) & ~size_t(255);
-    const size_t bt_b = ((size_t)r * M * elt + 255) & ~size_t(255);
-    const size_t at_b = ((size_t)K * r * elt + 255) & ~size_t(255);
-    return du_b + bt_b + at_b;
+    const size_t base = al256((size_t)N * r * 4) + al256((size_t)r * M * elt) + al256((size_t)K * r * elt);
+    if (elt != 2) return base;
+    // the two colsum calls (C = M for dB, C = K for dA) share the partials
+    const size_t pk = (size_t)colsum_splits(N, K) * K, pm = (size_t)colsum_splits(N, M) * M;
+    return base + al256((size_t)32 * colsum_npad(N) * 2) + al256((pk > pm ? pk : pm) * 32 * 4);
 }
 
 hipError_t launch_lora_fwd(const LoraParams &p, int dtype, hipStream_t s) {

@@ -24,6 +24,9 @@ EXPORTED = [
     "fa_attn_fwd", "fa_attn_bwd_workspace_size", "fa_attn_bwd", "fa_attn_bwd_phase",
     "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
+    # include/foundry_block.h
+    "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
+    "fa_adamw_step",
 ]
 
 
@@ -99,6 +102,38 @@ class LoraBwdArgs(ctypes.Structure):
     ]
 
 
+class LnModArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+        ("eps", ctypes.c_float), ("x", ctypes.c_void_p), ("ldx", ctypes.c_int64),
+        ("shift", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64), ("mean", ctypes.c_void_p), ("rstd", ctypes.c_void_p),
+    ]
+
+
+class LnModBwdArgs(ctypes.Structure):
+    _fields_ = [("fwd", LnModArgs), ("dy", ctypes.c_void_p), ("lddy", ctypes.c_int64),
+                ("dres", ctypes.c_void_p), ("ldres", ctypes.c_int64), ("dx", ctypes.c_void_p),
+                ("lddx", ctypes.c_int64)]
+
+
+class RowsArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+        ("x", ctypes.c_void_p), ("ldx", ctypes.c_int64), ("g", ctypes.c_void_p),
+        ("b", ctypes.c_void_p), ("ldb", ctypes.c_int64), ("y", ctypes.c_void_p), ("ldy", ctypes.c_int64),
+    ]
+
+
+class AdamwArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("n", ctypes.c_int64), ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p), ("m", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("lr", ctypes.c_double), ("beta1", ctypes.c_double), ("beta2", ctypes.c_double),
+        ("eps", ctypes.c_double), ("step", ctypes.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -130,6 +165,12 @@ def lib() -> ctypes.CDLL:
     L.fa_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnBwdArgs)]
     L.fa_lora_bwd_workspace_size.restype = ctypes.c_size_t
     L.fa_lora_bwd_workspace_size.argtypes = [ctypes.POINTER(LoraBwdArgs)]
+    for name, st in (("fa_ln_mod_fwd", LnModArgs), ("fa_ln_mod_bwd", LnModBwdArgs),
+                     ("fa_gated_residual", RowsArgs), ("fa_gelu_fwd", RowsArgs),
+                     ("fa_gelu_bwd", RowsArgs), ("fa_silu", RowsArgs), ("fa_adamw_step", AdamwArgs)):
+        fn = getattr(L, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
     L.fa_rope_tables_host.restype = ctypes.c_int
     L.fa_rope_tables_host.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_float, ctypes.c_int32,

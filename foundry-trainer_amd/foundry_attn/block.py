@@ -1,0 +1,342 @@
+"""foundry-spike's double-stream LoRA block on the MI355X path (config c4).
+
+Mirrors ``double_block`` (crates/foundry-spike/src/bin/throughput.rs:480-574)
+and one training step of it (Session::step, throughput.rs:784-803: forward,
+backward, adamw_step on the LoRA factors), with the c4 choices:
+  - both streams' q, k, v and out projections carry LoRA (the reference's
+    klein run trains the image stream only, throughput.rs:424-428);
+  - the MLP is tanh-GELU with hidden 4 * dim (the reference block uses
+    SwiGLU, lib.rs:293-297);
+  - the upstream gradient is a given dY per stream (the seed trick,
+    attn_backward.rs:220-222) instead of the MSE loss;
+  - the frozen linears have no bias.
+
+Compute path: the memory-bound ops (layer_norm_mod and its backward, gated
+residuals, GELU, the fused QK-RMSNorm + RoPE prologue, the LoRA adapters,
+AdamW) and the joint attention run as libfoundry_attn.so kernels; the frozen
+base linears are plain library GEMMs (torch.mm -> hipBLASLt), bf16 in, f32
+accumulation, bf16 out.
+
+The backward forms exactly the gradients Candle's autograd needs for the
+LoRA factors: nothing flows into the first layer_norm_mod (its output feeds
+only frozen weights and the adapters), so no dX is formed for the frozen qkv
+projection.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+from typing import Dict, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import _abi
+from ._abi import FoundryAttnError, check, lib
+from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_fwd, qk_prologue,
+                  qk_prologue_bwd, rope_tables)
+
+
+# ---------------------------------------------------------------------------
+# block ops (include/foundry_block.h)
+# ---------------------------------------------------------------------------
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be 2-D with contiguous rows")
+    return t
+
+
+def _vec(t: torch.Tensor, C: int, like: torch.Tensor, name: str) -> torch.Tensor:
+    if t.shape != (C,) or not t.is_contiguous() or t.dtype != like.dtype or t.device != like.device:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be a contiguous [{C}] {like.dtype}")
+    return t
+
+
+def _like(out: Optional[torch.Tensor], ref: torch.Tensor, name: str = "out") -> torch.Tensor:
+    if out is None:
+        return torch.empty_like(ref, memory_format=torch.contiguous_format)
+    _rows(out, name)
+    if out.shape != ref.shape or out.dtype != ref.dtype or out.device != ref.device:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must match {tuple(ref.shape)} {ref.dtype}")
+    return out
+
+
+def ln_mod_fwd(x, shift, scale, eps: float = 1e-6, out=None, stats: bool = False):
+    """layer_norm_mod (lib.rs:60-71) over the rows of x [N, C]:
+    y = (1 + scale) * LN(x) + shift.  With stats=True also returns the f32
+    row mean and rstd the backward needs: (y, mean, rstd)."""
+    x = _rows(x, "x")
+    N, C = x.shape
+    y = _like(out, x)
+    mean = rstd = None
+    if stats:
+        mean = torch.empty(N, dtype=torch.float32, device=x.device)
+        rstd = torch.empty(N, dtype=torch.float32, device=x.device)
+    a = _abi.LnModArgs(dtype=_dtype_code(x), rows=N, cols=C, eps=float(eps), x=_ptr(x), ldx=x.stride(0),
+                       shift=_ptr(_vec(shift, C, x, "shift")), scale=_ptr(_vec(scale, C, x, "scale")),
+                       y=_ptr(y), ldy=y.stride(0), mean=_ptr(mean), rstd=_ptr(rstd))
+    check(lib().fa_ln_mod_fwd(ctypes.byref(a), _stream(x)))
+    return (y, mean, rstd) if stats else y
+
+
+def ln_mod_bwd(x, dy, scale, mean, rstd, eps: float = 1e-6, dres=None, out=None):
+    """dx = dres + d/dx layer_norm_mod(x)^T dy (shift / scale frozen)."""
+    x, dy = _rows(x, "x"), _rows(dy, "dy")
+    N, C = x.shape
+    dx = _like(out, x)
+    if dres is not None:
+        _rows(dres, "dres")
+    fwd = _abi.LnModArgs(dtype=_dtype_code(x), rows=N, cols=C, eps=float(eps), x=_ptr(x), ldx=x.stride(0),
+                         shift=_ptr(_vec(scale, C, x, "scale")), scale=_ptr(_vec(scale, C, x, "scale")),
+                         mean=_ptr(mean), rstd=_ptr(rstd))
+    a = _abi.LnModBwdArgs(fwd=fwd, dy=_ptr(dy), lddy=dy.stride(0), dres=_ptr(dres),
+                          ldres=0 if dres is None else dres.stride(0), dx=_ptr(dx), lddx=dx.stride(0))
+    check(lib().fa_ln_mod_bwd(ctypes.byref(a), _stream(x)))
+    return dx
+
+
+def _rows_op(fn, x, g, b, out):
+    b = _rows(b, "b")
+    N, C = b.shape
+    y = _like(out, b)
+    if x is not None:
+        _rows(x, "x")
+    a = _abi.RowsArgs(dtype=_dtype_code(b), rows=N, cols=C, x=_ptr(x), ldx=0 if x is None else x.stride(0),
+                      g=_ptr(g), b=_ptr(b), ldb=b.stride(0), y=_ptr(y), ldy=y.stride(0))
+    check(getattr(lib(), fn)(ctypes.byref(a), _stream(b)))
+    return y
+
+
+def gated_residual(x, g, b, out=None):
+    """y = x + g * b (g [C] broadcast over rows); x None gives g * b."""
+    return _rows_op("fa_gated_residual", x, _vec(g, b.shape[1], b, "g"), b, out)
+
+
+def gelu(b, out=None):
+    """tanh-GELU, elementwise."""
+    return _rows_op("fa_gelu_fwd", None, None, b, out)
+
+
+def gelu_bwd(dy, b, out=None):
+    """dy * gelu'(b); out may be dy itself."""
+    return _rows_op("fa_gelu_bwd", dy, None, b, out)
+
+
+def silu(b, out=None):
+    return _rows_op("fa_silu", None, None, b, out)
+
+
+def adamw_step(param, grad, m, v, step: int, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8):
+    """adamw_step (lib.rs:477-510) in place on param (bf16/f32) with f32 grad,
+    m, v of the same number of elements."""
+    n = param.numel()
+    for name, t in (("grad", grad), ("m", m), ("v", v)):
+        if t.numel() != n or t.dtype != torch.float32 or not t.is_contiguous() or t.device != param.device:
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be contiguous float32 like param")
+    if not param.is_contiguous():
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "param must be contiguous")
+    a = _abi.AdamwArgs(dtype=_dtype_code(param), n=n, param=_ptr(param), grad=_ptr(grad), m=_ptr(m),
+                       v=_ptr(v), lr=float(lr), beta1=float(betas[0]), beta2=float(betas[1]), eps=float(eps),
+                       step=int(step))
+    check(lib().fa_adamw_step(ctypes.byref(a), _stream(param)))
+
+
+# ---------------------------------------------------------------------------
+# the block
+# ---------------------------------------------------------------------------
+LORA_TARGETS = ("q", "k", "v", "out")
+STREAMS = ("txt", "img")  # joint order: txt first (throughput.rs:545-547)
+
+
+@dataclass
+class StreamWeights:
+    """Frozen weights of one stream (torch tensors, compute dtype) and its
+    LoRA factors with their AdamW moments."""
+    w_qkv: torch.Tensor   # [3C, C]: to_q, to_k, to_v stacked
+    w_out: torch.Tensor   # [C, C]
+    w1: torch.Tensor      # [F, C]
+    w2: torch.Tensor      # [C, F]
+    q_norm: torch.Tensor  # [D]
+    k_norm: torch.Tensor  # [D]
+    w_mod: torch.Tensor   # [6C, C]: shift1, scale1, gate1, shift2, scale2, gate2
+    lora_a: Dict[str, torch.Tensor] = field(default_factory=dict)  # [r, in]
+    lora_b: Dict[str, torch.Tensor] = field(default_factory=dict)  # [out, r]
+    m: Dict[str, torch.Tensor] = field(default_factory=dict)
+    v: Dict[str, torch.Tensor] = field(default_factory=dict)
+    mod: Tuple[torch.Tensor, ...] = ()
+
+
+class DoubleBlockLoRA:
+    """One double-stream block with LoRA on q/k/v/out of both streams.
+
+    heads * head_dim = dim; img tokens lie on an (img_rows, img_cols) grid,
+    txt tokens get positions (l, 0, 0), img tokens (0, r, c)
+    (throughput.rs:724-748).
+    """
+
+    def __init__(self, weights: Dict[str, StreamWeights], heads: int, head_dim: int, txt_tokens: int,
+                 img_rows: int, img_cols: int, axes: Sequence[int] = (16, 56, 56), theta: float = 1e4,
+                 lora_scale: float = 1.0, eps: float = 1e-6):
+        self.w = weights
+        self.H, self.D = heads, head_dim
+        self.C = heads * head_dim
+        self.T, self.I = txt_tokens, img_rows * img_cols
+        self.S = self.T + self.I
+        self.axes = tuple(int(a) for a in axes)
+        self.lora_scale = float(lora_scale)
+        self.eps = float(eps)
+        self.attn_scale = 1.0 / math.sqrt(head_dim)
+        ref = weights["img"].w_qkv
+        self.dtype, self.device = ref.dtype, ref.device
+        pos = np.zeros((self.S, 3), np.float32)
+        pos[:self.T, 0] = np.arange(self.T)
+        rr, cc = np.meshgrid(np.arange(img_rows), np.arange(img_cols), indexing="ij")
+        pos[self.T:, 1] = rr.ravel()
+        pos[self.T:, 2] = cc.ravel()
+        cos, sin = rope_tables(pos, self.axes, theta, dtype=self.dtype, device=self.device)
+        self.rope = {"txt": (cos[:self.T].contiguous(), sin[:self.T].contiguous()),
+                     "img": (cos[self.T:].contiguous(), sin[self.T:].contiguous())}
+        self.offset = {"txt": 0, "img": self.T}
+        self.rows = {"txt": self.T, "img": self.I}
+        self.step_count = 0
+        self._buf = None
+
+    # -- conditioning: computed once per run (throughput.rs:936-938) -------
+    def set_conditioning(self, c: torch.Tensor) -> None:
+        """Modulation parts chunk6(silu(c) W_mod^T) per stream."""
+        sc = silu(c.reshape(1, -1))
+        for name in STREAMS:
+            w = self.w[name]
+            m = torch.mm(sc, w.w_mod.t()).reshape(-1)
+            w.mod = tuple(t.contiguous() for t in m.split(self.C))
+
+    def _buffers(self):
+        if self._buf is None:
+            C, S, H, D = self.C, self.S, self.H, self.D
+            F = self.w["img"].w1.shape[0]
+            kw = dict(dtype=self.dtype, device=self.device)
+            b = {"qkv": torch.empty((S, 3 * C), **kw), "dqkv": torch.empty((S, 3 * C), **kw),
+                 "q": torch.empty((1, S, H, D), **kw), "k": torch.empty((1, S, H, D), **kw),
+                 "o": torch.empty((1, S, H, D), **kw), "do": torch.empty((1, S, H, D), **kw),
+                 "dq": torch.empty((1, S, H, D), **kw), "dk": torch.empty((1, S, H, D), **kw),
+                 "lse": torch.empty((1, H, S), dtype=torch.float32, device=self.device),
+                 "ws": torch.empty(2 * ((H * S * 4 + 255) // 256) * 256, dtype=torch.uint8, device=self.device)}
+            for name in STREAMS:
+                n = self.rows[name]
+                for key, width in (("h", C), ("out", C), ("x1", C), ("h2", C), ("y", C), ("t1", C),
+                                   ("t2", C), ("dx1", C), ("pre", F), ("act", F), ("dact", F), ("mlp", C)):
+                    b[f"{key}.{name}"] = torch.empty((n, width), **kw)
+            self._buf = b
+        return self._buf
+
+    def forward_backward(self, x: Dict[str, torch.Tensor], dy: Dict[str, torch.Tensor]):
+        """Block outputs y[stream] and the f32 LoRA gradients
+        grads[(stream, target)] = (dA, dB) for upstream gradients dy."""
+        B = self._buffers()
+        C, S, H, D = self.C, self.S, self.H, self.D
+        s = self.lora_scale
+        qkv, dqkv = B["qkv"], B["dqkv"]
+        saved = {}
+        # q / k / v: layer_norm_mod -> frozen fused qkv + three adapters -> prologue
+        for name in STREAMS:
+            w, off, n = self.w[name], self.offset[name], self.rows[name]
+            sh1, sc1 = w.mod[0], w.mod[1]
+            h = ln_mod_fwd(x[name], sh1, sc1, self.eps, out=B[f"h.{name}"])
+            rows = qkv[off:off + n]
+            torch.mm(h, w.w_qkv.t(), out=rows)
+            for j, t in enumerate(("q", "k", "v")):
+                saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
+            cos, sin = self.rope[name]
+            qk_prologue(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, self.eps,
+                        out=B["q"], seq_offset=off)
+            qk_prologue(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, self.eps,
+                        out=B["k"], seq_offset=off)
+        v = qkv[:, 2 * C:].view(1, S, H, D)
+        attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=B["o"], lse=B["lse"])
+        y = {}
+        # out projection, gated residuals, MLP, and the backward down to dO
+        for name in STREAMS:
+            w, off, n = self.w[name], self.offset[name], self.rows[name]
+            sh2, sc2, g1, g2 = w.mod[3], w.mod[4], w.mod[2], w.mod[5]
+            a = B["o"][0, off:off + n].reshape(n, C)
+            out = torch.mm(a, w.w_out.t(), out=B[f"out.{name}"])
+            u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s)
+            x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
+            h2, mean2, rstd2 = ln_mod_fwd(x1, sh2, sc2, self.eps, out=B[f"h2.{name}"], stats=True)
+            pre = torch.mm(h2, w.w1.t(), out=B[f"pre.{name}"])
+            act = gelu(pre, out=B[f"act.{name}"])
+            mlp = torch.mm(act, w.w2.t(), out=B[f"mlp.{name}"])
+            y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
+            # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
+            dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
+            dact = torch.mm(dmlp, w.w2, out=B[f"dact.{name}"])
+            gelu_bwd(dact, pre, out=dact)
+            dh2 = torch.mm(dact, w.w1, out=B[f"t2.{name}"])
+            dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
+            dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
+            do_rows = B["do"][0, off:off + n].reshape(n, C)
+            torch.mm(dout, w.w_out, out=do_rows)
+            saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
+                                                    dx=do_rows)
+        dv = dqkv[:, 2 * C:].view(1, S, H, D)
+        attn_bwd(B["q"], B["k"], v, B["o"], B["do"], B["lse"], self.attn_scale, None, workspace=B["ws"],
+                 out=(B["dq"], B["dk"], dv))
+        grads = {}
+        for name in STREAMS:
+            w, off, n = self.w[name], self.offset[name], self.rows[name]
+            rows, drows = qkv[off:off + n], dqkv[off:off + n]
+            cos, sin = self.rope[name]
+            qk_prologue_bwd(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, B["dq"],
+                            seq_offset=off, eps=self.eps, dx=drows[:, :C].view(1, n, H, D))
+            qk_prologue_bwd(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, B["dk"],
+                            seq_offset=off, eps=self.eps, dx=drows[:, C:2 * C].view(1, n, H, D))
+            h = B[f"h.{name}"]
+            for j, t in enumerate(("q", "k", "v")):
+                grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
+                                            drows[:, j * C:(j + 1) * C], s)
+            grads[(name, "out")] = saved[(name, "out", "grad")]
+        return y, grads
+
+    def apply_adamw(self, grads, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8) -> None:
+        self.step_count += 1
+        for (name, t), (da, db) in grads.items():
+            w = self.w[name]
+            adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
+            adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
+
+    def train_step(self, x, dy, lr: float = 1e-3):
+        """One LoRA block step: forward, backward, AdamW (the unit of the
+        'LoRA block steps/s' metric)."""
+        y, grads = self.forward_backward(x, dy)
+        self.apply_adamw(grads, lr)
+        return y, grads
+
+
+def random_block(dim: int, heads: int, txt_tokens: int, img_rows: int, img_cols: int, mlp_ratio: int = 4,
+                 rank: int = 16, alpha: float = 16.0, dtype=torch.bfloat16, device="cuda", seed: int = 20261028,
+                 axes=(16, 56, 56), theta: float = 1e4) -> DoubleBlockLoRA:
+    """c4-style random init: base W ~ N(0, 0.02) frozen, LoRA A ~ N(0, 1/r)
+    (PEFT "gaussian"), B ~ N(0, 1e-3), QK-norm scales 1 + N(0, 0.02),
+    modulation W ~ N(0, 0.02)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    C, F = dim, mlp_ratio * dim
+    D = dim // heads
+
+    def rn(*shape, std):
+        return (torch.randn(*shape, generator=g) * std).to(dtype=dtype, device=device)
+
+    ws = {}
+    for name in STREAMS:
+        w = StreamWeights(w_qkv=rn(3 * C, C, std=0.02), w_out=rn(C, C, std=0.02), w1=rn(F, C, std=0.02),
+                          w2=rn(C, F, std=0.02), q_norm=(1 + rn(D, std=0.02).float()).to(dtype),
+                          k_norm=(1 + rn(D, std=0.02).float()).to(dtype), w_mod=rn(6 * C, C, std=0.02))
+        for t in LORA_TARGETS:
+            w.lora_a[t] = rn(rank, C, std=1.0 / rank)
+            w.lora_b[t] = rn(C, rank, std=1e-3)
+            for part, shape in (("a", (rank, C)), ("b", (C, rank))):
+                w.m[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
+                w.v[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
+        ws[name] = w
+    return DoubleBlockLoRA(ws, heads, D, txt_tokens, img_rows, img_cols, axes=axes, theta=theta,
+                           lora_scale=alpha / rank)

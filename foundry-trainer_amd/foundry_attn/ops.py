@@ -272,15 +272,21 @@ def qk_prologue(x, weight, cos, sin, axes: Sequence[int], eps: float = 1e-6,
 
 
 def qk_prologue_bwd(x, weight, cos, sin, axes: Sequence[int], dy, seq_offset: int = 0,
-                    eps: float = 1e-6):
-    """Gradient wrt x of qk_prologue, given dy wrt the joint buffer."""
+                    eps: float = 1e-6, dx: Optional[torch.Tensor] = None):
+    """Gradient wrt x of qk_prologue, given dy wrt the joint buffer; written to
+    `dx` (a view shaped like x, any row strides) when given."""
     squeeze = x.dim() == 3
     x4, dy4 = _as4(x, "x"), _as4(dy, "dy")
     B, T, H, D = x4.shape
     if dy4.shape[0] != B or dy4.shape[2:] != (H, D) or seq_offset + T > dy4.shape[1] \
             or dy4.dtype != x4.dtype or dy4.device != x4.device:
         raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "dy does not fit x at seq_offset")
-    dx = torch.empty(x4.shape, dtype=x4.dtype, device=x4.device)
+    if dx is None:
+        dx = torch.empty(x4.shape, dtype=x4.dtype, device=x4.device)
+    else:
+        dx = _as4(dx, "dx")
+        if dx.shape != x4.shape or dx.dtype != x4.dtype or dx.device != x4.device:
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "dx must match x")
     a = _abi.QkPrologueBwdArgs(fwd=_prologue_args(x4, weight, cos, sin, axes, eps, dy4, seq_offset),
                                dy=_ptr(dy4), dx=_ptr(dx), dx_stride=_strides(dx))
     check(lib().fa_qk_prologue_bwd(ctypes.byref(a), _stream(x4)))

@@ -1,0 +1,116 @@
+/*
+ * foundry_block.h — C ABI of the memory-bound ops of the double-stream LoRA
+ * block (libfoundry_attn.so, same library and conventions as foundry_attn.h).
+ *
+ * These replace the Candle op chains the reference's block runs between its
+ * linears and its attention (crates/foundry-spike/src/bin/throughput.rs:
+ * 480-574, the fixture-sized lib.rs:301-392):
+ *   layer_norm_mod   lib.rs:60-71        fa_ln_mod_fwd / fa_ln_mod_bwd
+ *   gated residual   throughput.rs:552-572   fa_gated_residual
+ *   MLP activation   (c4 block: tanh-GELU; the reference block's SwiGLU,
+ *                    lib.rs:293-297, has no tanh-GELU counterpart)
+ *                                        fa_gelu_fwd / fa_gelu_bwd
+ *   modulation input silu(temb)  throughput.rs:297-324     fa_silu
+ *   adamw_step       lib.rs:477-510      fa_adamw_step
+ *
+ * Row views: `rows` x `cols` elements, row r starting at base + r * ld
+ * elements; cols % 8 == 0, ld >= cols, and base and ld keep every row
+ * 16-byte aligned (ld % 8 == 0 for bf16, % 4 for f32).  Per-column vectors
+ * ([cols]: shift, scale, gate) are contiguous and 16-byte aligned.
+ * Arithmetic is f32; results are rounded once to the storage dtype.
+ */
+#ifndef FOUNDRY_BLOCK_H
+#define FOUNDRY_BLOCK_H
+
+#include "foundry_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fa_ln_mod_args {
+    int32_t dtype;        /* fa_dtype of x, shift, scale, y (and dy, dres, dx)   */
+    int32_t rows, cols;   /* N >= 1; 8 <= C <= 4096                              */
+    float eps;            /* > 0 (the reference's NORM_EPS is 1e-6)              */
+    const void *x;        /* [N, C]                                              */
+    int64_t ldx;
+    const void *shift;    /* [C] */
+    const void *scale;    /* [C]: y = (1 + scale) * LN(x) + shift                */
+    void *y;              /* [N, C] output (fwd)                                 */
+    int64_t ldy;
+    float *mean, *rstd;   /* [N] f32: written by fwd when non-NULL (rstd =
+                             1/sqrt(var + eps)); required by bwd                 */
+} fa_ln_mod_args;
+
+/* y = (1 + scale) * (x - mean) / sqrt(var + eps) + shift per row, mean and
+ * (biased) variance in f32.  Replaces layer_norm_mod (lib.rs:60-71). */
+fa_status fa_ln_mod_fwd(const fa_ln_mod_args *args, void *stream);
+
+typedef struct fa_ln_mod_bwd_args {
+    fa_ln_mod_args fwd;   /* x, scale, mean, rstd as in the forward; y unused    */
+    const void *dy;       /* [N, C] gradient of y                                */
+    int64_t lddy;
+    const void *dres;     /* [N, C] or NULL: added to dx (the residual path)     */
+    int64_t ldres;
+    void *dx;             /* [N, C] output                                       */
+    int64_t lddx;
+} fa_ln_mod_bwd_args;
+
+/* dx = dres + rstd * (dn - mean(dn) - n * mean(dn * n)), n = (x - mean) * rstd,
+ * dn = dy * (1 + scale): the gradient Candle's autograd forms through
+ * layer_norm_mod (shift and scale are frozen, so no gradient for them). */
+fa_status fa_ln_mod_bwd(const fa_ln_mod_bwd_args *args, void *stream);
+
+typedef struct fa_rows_args {
+    int32_t dtype;        /* fa_dtype of every view                              */
+    int32_t rows, cols;
+    const void *x;        /* [N, C] (see each op)                                */
+    int64_t ldx;
+    const void *g;        /* [C] gate (fa_gated_residual only)                   */
+    const void *b;        /* [N, C] input                                        */
+    int64_t ldb;
+    void *y;              /* [N, C] output; may alias x or b element for element */
+    int64_t ldy;
+} fa_rows_args;
+
+/* y = x + g * b with g broadcast over rows; x may be NULL (y = g * b, the
+ * gradient of the gated branch).  Replaces the broadcast_mul + add of
+ * throughput.rs:552-572. */
+fa_status fa_gated_residual(const fa_rows_args *args, void *stream);
+
+/* y = b/2 * (1 + tanh(sqrt(2/pi) * (b + 0.044715 b^3))) (x unused).  The c4
+ * block's MLP activation; no reference counterpart (the reference block uses
+ * SwiGLU, lib.rs:293-297). */
+fa_status fa_gelu_fwd(const fa_rows_args *args, void *stream);
+
+/* y = x * gelu'(b): x is the gradient of gelu(b). */
+fa_status fa_gelu_bwd(const fa_rows_args *args, void *stream);
+
+/* y = b / (1 + exp(-b)) (x unused): the SiLU of the conditioning vector that
+ * feeds the frozen modulation linear (throughput.rs:297-324). */
+fa_status fa_silu(const fa_rows_args *args, void *stream);
+
+typedef struct fa_adamw_args {
+    int32_t dtype;        /* fa_dtype of param                                   */
+    int64_t n;            /* elements, >= 1                                      */
+    void *param;          /* [n], updated in place                               */
+    const float *grad;    /* [n] f32                                             */
+    float *m, *v;         /* [n] f32 moments, updated in place (zero at step 1)  */
+    double lr, beta1, beta2, eps; /* f64, as the reference's AdamW fields; each is
+                             rounded to f32 where the reference's f32 affine
+                             uses it, 1 - beta and the bias corrections are
+                             formed in f64                                       */
+    int32_t step;         /* >= 1: bias corrections 1 - beta^step (in double)   */
+} fa_adamw_args;
+
+/* One AdamW step, weight decay 0, in adamw_step's operation order
+ * (lib.rs:477-510): m' = m*b1 + g*(1-b1); v' = v*b2 + g^2*(1-b2);
+ * p' = p - ((m'/bc1) / (sqrt(v'/bc2) + eps)) * lr, every f32 product or sum
+ * rounded separately. */
+fa_status fa_adamw_step(const fa_adamw_args *args, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FOUNDRY_BLOCK_H */

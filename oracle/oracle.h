@@ -74,6 +74,18 @@ void og_gemm_tn(int M, int N, int K, const float *A, long lda, const float *B, l
                 float *C, long ldc, int nthreads);
 void og_transpose(int R, int C, const float *src, long lds, float *dst, long ldd, int nthreads);
 
+/* Double-stream block ops (block_oracle.c): rows are [N][C] contiguous. */
+void oracle_ln_mod_fwd(const float *x, long N, int C, const float *shift, const float *scale, float eps,
+                       int bf16, float *y, float *mean, float *rstd);
+void oracle_ln_mod_bwd(const float *x, const float *dy, long N, int C, const float *scale, const float *mean,
+                       const float *rstd, const float *dres, int bf16, float *dx);
+void oracle_gated_residual(const float *x, const float *g, const float *b, long N, int C, int bf16, float *y);
+void oracle_gelu_fwd(const float *b, long n, int bf16, float *y);
+void oracle_gelu_bwd(const float *dy, const float *b, long n, int bf16, float *y);
+void oracle_silu(const float *b, long n, int bf16, float *y);
+void oracle_adamw_step(float *param, const float *grad, float *m, float *v, long n, double lr, double beta1,
+                       double beta2, double eps, int step, int bf16);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,17 @@ def lib():
             ctypes.c_float, ctypes.c_int, ctypes.c_int]
         L.oracle_linear_lora_bwd.argtypes = [_f32p] * 8 + [ctypes.c_int] * 4 + [
             ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        L.oracle_ln_mod_fwd.argtypes = [_f32p, ctypes.c_long, ctypes.c_int, _f32p, _f32p, ctypes.c_float,
+                                        ctypes.c_int, _f32p, _f32p, _f32p]
+        L.oracle_ln_mod_bwd.argtypes = [_f32p, _f32p, ctypes.c_long, ctypes.c_int, _f32p, _f32p, _f32p,
+                                        _f32p, ctypes.c_int, _f32p]
+        L.oracle_gated_residual.argtypes = [_f32p, _f32p, _f32p, ctypes.c_long, ctypes.c_int, ctypes.c_int,
+                                            _f32p]
+        L.oracle_gelu_fwd.argtypes = [_f32p, ctypes.c_long, ctypes.c_int, _f32p]
+        L.oracle_gelu_bwd.argtypes = [_f32p, _f32p, ctypes.c_long, ctypes.c_int, _f32p]
+        L.oracle_silu.argtypes = [_f32p, ctypes.c_long, ctypes.c_int, _f32p]
+        L.oracle_adamw_step.argtypes = [_f32p] * 4 + [ctypes.c_long] + [ctypes.c_double] * 4 + [
+            ctypes.c_int, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -215,3 +226,65 @@ def linear_lora_bwd(x, W, A, Bm, dy, scale=1.0, bf16=False, want_dx=True, nthrea
                                  in_f, out_f, r, float(scale), int(bf16),
                                  nthreads or default_threads())
     return dx, dA, dB
+
+
+# ----- double-stream block ops (block_oracle.c) -------------------------------
+
+def ln_mod_fwd(x, shift, scale, eps=1e-6, bf16=False):
+    """layer_norm_mod (lib.rs:60-71) over the rows of x [N, C]; returns
+    y, mean [N], rstd [N]."""
+    x = _c(x)
+    N, C = x.shape
+    y = np.empty_like(x)
+    mean = np.empty(N, np.float32)
+    rstd = np.empty(N, np.float32)
+    lib().oracle_ln_mod_fwd(_p(x), N, C, _p(_c(shift)), _p(_c(scale)), eps, int(bf16), _p(y), _p(mean),
+                            _p(rstd))
+    return y, mean, rstd
+
+
+def ln_mod_bwd(x, dy, scale, mean, rstd, dres=None, bf16=False):
+    x, dy = _c(x), _c(dy)
+    N, C = x.shape
+    dx = np.empty_like(x)
+    lib().oracle_ln_mod_bwd(_p(x), _p(dy), N, C, _p(_c(scale)), _p(_c(mean)), _p(_c(rstd)),
+                            None if dres is None else _p(_c(dres)), int(bf16), _p(dx))
+    return dx
+
+
+def gated_residual(x, g, b, bf16=False):
+    b = _c(b)
+    N, C = b.shape
+    y = np.empty_like(b)
+    lib().oracle_gated_residual(None if x is None else _p(_c(x)), _p(_c(g)), _p(b), N, C, int(bf16), _p(y))
+    return y
+
+
+def gelu_fwd(b, bf16=False):
+    b = _c(b)
+    y = np.empty_like(b)
+    lib().oracle_gelu_fwd(_p(b), b.size, int(bf16), _p(y))
+    return y
+
+
+def gelu_bwd(dy, b, bf16=False):
+    b, dy = _c(b), _c(dy)
+    y = np.empty_like(b)
+    lib().oracle_gelu_bwd(_p(dy), _p(b), b.size, int(bf16), _p(y))
+    return y
+
+
+def silu(b, bf16=False):
+    b = _c(b)
+    y = np.empty_like(b)
+    lib().oracle_silu(_p(b), b.size, int(bf16), _p(y))
+    return y
+
+
+def adamw_step(param, grad, m, v, step, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, bf16=False):
+    """adamw_step (lib.rs:477-510); returns the updated (param, m, v)."""
+    p, g = _c(param).copy(), _c(grad)
+    m, v = _c(m).copy(), _c(v).copy()
+    lib().oracle_adamw_step(_p(p), _p(g), _p(m), _p(v), p.size, lr, beta1, beta2, eps, int(step), int(bf16))
+    return p, m, v
+

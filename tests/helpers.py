@@ -37,6 +37,13 @@ def load_golden(tag: str) -> dict:
             load_file(os.path.join(GOLDEN, f"attn_fixture_{tag}.safetensors")).items()}
 
 
+def load_block_golden(tag: str) -> dict:
+    """The reference fixture's block subset (block_fixture_{tag}) as float32 numpy."""
+    from safetensors.torch import load_file
+    return {k: v.float().numpy() for k, v in
+            load_file(os.path.join(GOLDEN, f"block_fixture_{tag}.safetensors")).items()}
+
+
 def bf16_round(a):
     import oracle
     return oracle.bf16_round(a)

@@ -13,12 +13,15 @@ from foundry_attn import _abi
 from foundry_attn._abi import lib
 
 HEADER = os.path.join(ROOT, "include", "foundry_attn.h")
+BLOCK_HEADER = os.path.join(ROOT, "include", "foundry_block.h")
 
 
 def header_functions():
-    src = open(HEADER).read()
-    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", src)))
+    names = set()
+    for h in (HEADER, BLOCK_HEADER):
+        src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", src))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
@@ -45,8 +48,10 @@ def test_struct_layouts_match_header(tmp_path):
     structs = {"fa_strides": _abi.Strides, "fa_attn_fwd_args": _abi.AttnFwdArgs,
                "fa_attn_bwd_args": _abi.AttnBwdArgs, "fa_qk_prologue_args": _abi.QkPrologueArgs,
                "fa_qk_prologue_bwd_args": _abi.QkPrologueBwdArgs, "fa_lora_args": _abi.LoraArgs,
-               "fa_lora_bwd_args": _abi.LoraBwdArgs}
-    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+               "fa_lora_bwd_args": _abi.LoraBwdArgs, "fa_ln_mod_args": _abi.LnModArgs,
+               "fa_ln_mod_bwd_args": _abi.LnModBwdArgs, "fa_rows_args": _abi.RowsArgs,
+               "fa_adamw_args": _abi.AdamwArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{BLOCK_HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:
@@ -166,3 +171,58 @@ def test_rope_tables_host_matches_oracle(bf16):
     oc, os_ = oracle.rope_tables(pos, [16, 56, 56], 1e4, bf16=bf16)
     np.testing.assert_array_equal(cos, oc)
     np.testing.assert_array_equal(sin, os_)
+
+
+# ----- block ops (include/foundry_block.h) ----------------------------------
+
+_FAKE = 1 << 20  # aligned non-null placeholder; validation fails before any use
+
+
+def _status_name(st):
+    return _abi.STATUS_NAMES[st]
+
+
+def test_block_ops_validate_before_device_work():
+    L = lib()
+    ok_dev = _abi.FA_OK if gpu_available() else _abi.FA_ERR_NO_DEVICE
+    ln = _abi.LnModArgs(dtype=0, rows=4, cols=3072, eps=1e-6, x=_FAKE, ldx=3072, shift=_FAKE, scale=_FAKE,
+                        y=_FAKE, ldy=3072)
+    if not gpu_available():
+        assert L.fa_ln_mod_fwd(ctypes.byref(ln), None) == ok_dev
+    for field, val in (("cols", 3070), ("cols", 8192), ("eps", 0.0), ("ldx", 3071), ("rows", 0),
+                       ("dtype", 7), ("x", 0), ("shift", _FAKE + 4)):
+        bad = _abi.LnModArgs.from_buffer_copy(ln)
+        setattr(bad, field, val)
+        assert L.fa_ln_mod_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+    # mean without rstd
+    bad = _abi.LnModArgs.from_buffer_copy(ln)
+    bad.mean = _FAKE
+    assert L.fa_ln_mod_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    # the backward needs the forward's statistics
+    bw = _abi.LnModBwdArgs(fwd=ln, dy=_FAKE, lddy=3072, dx=_FAKE, lddx=3072)
+    assert L.fa_ln_mod_bwd(ctypes.byref(bw), None) == _abi.FA_ERR_INVALID_ARG
+    assert b"mean and rstd" in L.fa_last_error()
+
+    rows = _abi.RowsArgs(dtype=0, rows=4, cols=64, x=0, ldx=64, g=_FAKE, b=_FAKE, ldb=64, y=_FAKE, ldy=64)
+    if not gpu_available():
+        for fn in ("fa_gated_residual", "fa_gelu_fwd", "fa_silu"):
+            assert getattr(L, fn)(ctypes.byref(rows), None) == ok_dev, fn
+    # gelu_bwd needs the upstream gradient x
+    assert L.fa_gelu_bwd(ctypes.byref(rows), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.RowsArgs.from_buffer_copy(rows)
+    bad.g = 0
+    assert L.fa_gated_residual(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.RowsArgs.from_buffer_copy(rows)
+    bad.ldb = 60
+    assert L.fa_gelu_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+
+    ad = _abi.AdamwArgs(dtype=0, n=1000, param=_FAKE, grad=_FAKE, m=_FAKE, v=_FAKE, lr=1e-3, beta1=0.9,
+                        beta2=0.999, eps=1e-8, step=1)
+    if not gpu_available():
+        assert L.fa_adamw_step(ctypes.byref(ad), None) == ok_dev
+    for field, val in (("step", 0), ("beta1", 1.0), ("beta2", -0.1), ("eps", 0.0), ("n", 0), ("grad", 0),
+                       ("m", _FAKE + 2)):
+        bad = _abi.AdamwArgs.from_buffer_copy(ad)
+        setattr(bad, field, val)
+        assert L.fa_adamw_step(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+

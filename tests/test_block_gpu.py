@@ -1,0 +1,182 @@
+"""GPU parity of the double-stream LoRA block (config c4's unit) against the
+CPU oracle.  Every block op goes through libfoundry_attn.so; the frozen base
+linears are library GEMMs.  Gates: the ops at bf16 max-abs / rel-L2 from the
+attention gates (2e-2 / 1e-2), f32 rel-L2 1e-4 (ln-mod backward 1e-3); the
+whole block step (outputs, LoRA gradients, updated LoRA factors) at the
+reference's own block thresholds, rel-L2 <= 2e-2 in bf16
+(tools/fixtures/PROVENANCE.md:49-53), 1e-3 in f32."""
+import numpy as np
+import pytest
+import torch
+
+import block_ref  # noqa: E402  (oracle/ on sys.path via conftest)
+import oracle
+from block_case import make_case, oracle_mods
+from foundry_attn import block as fb
+from helpers import max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device="cuda", dtype=dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("C", [256, 3072])
+def test_block_ops_match_oracle(dtype, C):
+    bf = dtype == torch.bfloat16
+    rng = np.random.default_rng(C)
+    rnd = (lambda a: oracle.bf16_round(a.astype(np.float32))) if bf else (lambda a: a.astype(np.float32))
+    N = 300
+    x, dy, dres, b = (rnd(rng.standard_normal((N, C))) for _ in range(4))
+    sh, sc, g = (rnd(0.1 * rng.standard_normal(C)) for _ in range(3))
+    tol = (2e-2, 1e-2) if bf else (None, 1e-4)
+
+    def chk(name, got, want, rel=None):
+        r = rel_l2(got, want)
+        print(f"  {name} C={C} {dtype}: rel_l2={r:.2e} max_abs={max_abs(got, want):.2e}", flush=True)
+        assert r <= (rel or tol[1]), (name, r)
+        if bf:
+            assert max_abs(got, want) <= tol[0] * max(1.0, float(np.abs(want).max())), name
+
+    y, mean, rstd = fb.ln_mod_fwd(dev(x, dtype), dev(sh, dtype), dev(sc, dtype), 1e-6, stats=True)
+    wy, wmean, wrstd = oracle.ln_mod_fwd(x, sh, sc, 1e-6, bf16=bf)
+    chk("ln_mod_fwd", host(y), wy)
+    np.testing.assert_allclose(host(mean), wmean, rtol=0, atol=1e-5)
+    np.testing.assert_allclose(host(rstd), wrstd, rtol=1e-5)
+    dx = fb.ln_mod_bwd(dev(x, dtype), dev(dy, dtype), dev(sc, dtype), mean, rstd, 1e-6, dres=dev(dres, dtype))
+    chk("ln_mod_bwd", host(dx), oracle.ln_mod_bwd(x, dy, sc, wmean, wrstd, dres=dres, bf16=bf),
+        None if bf else 1e-3)
+    chk("gated_residual", host(fb.gated_residual(dev(x, dtype), dev(g, dtype), dev(b, dtype))),
+        oracle.gated_residual(x, g, b, bf16=bf))
+    chk("gated_branch", host(fb.gated_residual(None, dev(g, dtype), dev(b, dtype))),
+        oracle.gated_residual(None, g, b, bf16=bf))
+    chk("gelu", host(fb.gelu(dev(b, dtype))), oracle.gelu_fwd(b, bf16=bf))
+    chk("gelu_bwd", host(fb.gelu_bwd(dev(dy, dtype), dev(b, dtype))), oracle.gelu_bwd(dy, b, bf16=bf))
+    chk("silu", host(fb.silu(dev(b, dtype))), oracle.silu(b, bf16=bf))
+    # in-place gelu_bwd (out aliases the upstream gradient), as the block uses it
+    t = dev(dy, dtype)
+    fb.gelu_bwd(t, dev(b, dtype), out=t)
+    chk("gelu_bwd_inplace", host(t), oracle.gelu_bwd(dy, b, bf16=bf))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_adamw_matches_oracle_over_steps(dtype):
+    bf = dtype == torch.bfloat16
+    rng = np.random.default_rng(1)
+    n = 70001
+    p = rng.standard_normal(n).astype(np.float32) * 0.05
+    if bf:
+        p = oracle.bf16_round(p)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    tp, tm, tv = dev(p, dtype), dev(m, torch.float32), dev(v, torch.float32)
+    for step in range(1, 6):
+        g = rng.standard_normal(n).astype(np.float32) * 10.0 ** rng.uniform(-6, 0)
+        fb.adamw_step(tp, dev(g, torch.float32), tm, tv, step)
+        p, m, v = oracle.adamw_step(p, g, m, v, step, bf16=bf)
+    torch.cuda.synchronize()
+    # same operation order: f32 moments agree to the last bits, the parameter
+    # to one bf16 ulp where a rounding tie flips
+    np.testing.assert_allclose(host(tm), m, rtol=1e-6, atol=1e-12)
+    np.testing.assert_allclose(host(tv), v, rtol=1e-6, atol=1e-20)
+    if bf:
+        assert np.mean(host(tp) != p) < 1e-3
+        assert max_abs(host(tp), p) <= 2 ** -8 * float(np.abs(p).max())
+    else:
+        np.testing.assert_allclose(host(tp), p, rtol=1e-6, atol=1e-9)
+
+
+def device_block(case, dtype):
+    ws = {}
+    for name in ("txt", "img"):
+        w = case["W"][name]
+        sw = fb.StreamWeights(w_qkv=dev(w["w_qkv"], dtype), w_out=dev(w["w_out"], dtype),
+                              w1=dev(w["w1"], dtype), w2=dev(w["w2"], dtype), q_norm=dev(w["q_norm"], dtype),
+                              k_norm=dev(w["k_norm"], dtype), w_mod=dev(w["w_mod"], dtype))
+        for t in fb.LORA_TARGETS:
+            sw.lora_a[t] = dev(w["lora_a"][t], dtype)
+            sw.lora_b[t] = dev(w["lora_b"][t], dtype)
+            for part, P in (("a", w["lora_a"][t]), ("b", w["lora_b"][t])):
+                sw.m[f"{t}.{part}"] = torch.zeros(P.shape, dtype=torch.float32, device="cuda")
+                sw.v[f"{t}.{part}"] = torch.zeros(P.shape, dtype=torch.float32, device="cuda")
+        ws[name] = sw
+    blk = fb.DoubleBlockLoRA(ws, case["H"], case["D"], case["T"], case["rows"], case["cols"], axes=case["axes"],
+                             lora_scale=case["scale"])
+    blk.set_conditioning(dev(case["c"], dtype))
+    return blk
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_block_step_matches_oracle(dtype):
+    bf = dtype == torch.bfloat16
+    case = oracle_mods(make_case(C=256, H=2, T=16, rows=4, cols=8, r=4, bf16=bf, seed=5))
+    blk = device_block(case, dtype)
+    for name in ("txt", "img"):  # the device modulation parts equal the oracle's
+        for i in range(6):
+            r = rel_l2(host(blk.w[name].mod[i]), case["W"][name]["mod"][i])
+            assert r <= (1e-2 if bf else 1e-5), (name, i, r)
+    x = {k: dev(v, dtype) for k, v in case["x"].items()}
+    dy = {k: dev(v, dtype) for k, v in case["dy"].items()}
+    y, grads = blk.train_step(x, dy)
+    torch.cuda.synchronize()
+    wy, wgrads, wupd = block_ref.block_step(case["x"], case["dy"], case["W"], case["H"], case["D"], case["cos"],
+                                            case["sin"], case["axes"], case["scale"], bf16=bf)
+    gate = 2e-2 if bf else 1e-3
+    for name in ("txt", "img"):
+        r = rel_l2(host(y[name]), wy[name])
+        print(f"  y.{name}: rel_l2={r:.2e}", flush=True)
+        assert r <= gate
+    for key, (wa, wb) in wgrads.items():
+        da, db = grads[key]
+        ra, rb = rel_l2(host(da), wa), rel_l2(host(db), wb)
+        print(f"  grad {key}: dA {ra:.2e} dB {rb:.2e}", flush=True)
+        assert ra <= gate and rb <= gate, key
+        a1, b1 = wupd[key]
+        w = blk.w[key[0]]
+        # one AdamW step moves each factor by ~lr * sign(g): compare the step
+        step_a = host(w.lora_a[key[1]]) - case["W"][key[0]]["lora_a"][key[1]]
+        step_b = host(w.lora_b[key[1]]) - case["W"][key[0]]["lora_b"][key[1]]
+        wa1 = a1 - case["W"][key[0]]["lora_a"][key[1]]
+        wb1 = b1 - case["W"][key[0]]["lora_b"][key[1]]
+        agree = np.mean(np.sign(step_a) == np.sign(wa1)), np.mean(np.sign(step_b) == np.sign(wb1))
+        print(f"  update {key}: sign agreement {agree[0]:.4f} {agree[1]:.4f}", flush=True)
+        assert min(agree) >= (0.97 if bf else 0.999), key
+
+
+def test_c4_block_step_properties():
+    """The full c4 block (4096 img + 512 txt tokens, dim 3072): one step gives
+    finite outputs, nonzero finite LoRA gradients that repeat bit for bit, and
+    an AdamW update of every factor."""
+    from foundry_attn.configs import C4
+    rows = int(C4.img_tokens ** 0.5)
+    blk = fb.random_block(C4.hidden, C4.heads, C4.txt_tokens, rows, C4.img_tokens // rows, C4.mlp_ratio,
+                          C4.lora_rank, C4.lora_alpha)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    blk.set_conditioning(torch.randn(C4.hidden, device="cuda", generator=g).to(torch.bfloat16))
+    x = {"img": torch.randn(C4.img_tokens, C4.hidden, device="cuda", generator=g).to(torch.bfloat16),
+         "txt": torch.randn(C4.txt_tokens, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)}
+    dy = {k: torch.randn(v.shape, device="cuda", generator=g).to(torch.bfloat16) for k, v in x.items()}
+    y1, g1 = blk.forward_backward(x, dy)
+    y1 = {k: v.clone() for k, v in y1.items()}
+    g1 = {k: (a.clone(), b.clone()) for k, (a, b) in g1.items()}
+    y2, g2 = blk.forward_backward(x, dy)
+    torch.cuda.synchronize()
+    for k in y1:
+        assert torch.isfinite(y1[k].float()).all() and torch.equal(y1[k], y2[k]), k
+    assert len(g1) == 8
+    for k, (da, db) in g1.items():
+        assert torch.isfinite(da).all() and torch.isfinite(db).all(), k
+        assert float(da.abs().max()) > 0 and float(db.abs().max()) > 0, k
+        assert torch.equal(da, g2[k][0]) and torch.equal(db, g2[k][1]), k
+    before = {k: (blk.w[k[0]].lora_a[k[1]].clone(), blk.w[k[0]].lora_b[k[1]].clone()) for k in g1}
+    blk.apply_adamw(g1)
+    torch.cuda.synchronize()
+    for k, (a0, b0) in before.items():
+        assert not torch.equal(a0, blk.w[k[0]].lora_a[k[1]]), k
+        assert not torch.equal(b0, blk.w[k[0]].lora_b[k[1]]), k
