@@ -27,6 +27,13 @@ __device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_bf16: A[m][k] lane = m + 16*(k/8) (8 consecutive k per
+// lane), B[k][n] lane = n + 16*(k/8); D element i of lane l is
+// D[4*(l/16) + i][l%16].
+__device__ __forceinline__ f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // v_mfma_f32_32x32x2_f32: A[m][k] lane = m + 32*k, B[k][n] lane = n + 32*k.
 __device__ __forceinline__ f32x16 mfma_32x32x2_f32(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);

@@ -97,6 +97,184 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(const float *__restric
     }
 }
 
+// ---- rowdot / expand, bf16 (MFMA) ---------------------------------------
+// rowdot: out[n][j] = s * sum_k X[n][k] W[j][k], R <= 16 * NT.  A workgroup
+// of 8 waves owns 16 rows; wave w takes k-steps (32 wide) w, w + 8, ..., four
+// at a time with all their loads issued before the MFMAs, and the 8 partial
+// tiles are summed in LDS in a fixed order (deterministic, no workspace).
+// Rows >= N and j >= R load from a clamped (valid) row and are zeroed.
+template <int NT>
+__global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restrict__ X, int64_t ldx,
+                                                            const bf16 *__restrict__ W, float *out, int64_t ldo,
+                                                            int N, int K, int R, float s) {
+    __shared__ float part[8][NT][4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m = lane & 15, q = lane >> 4;
+    const int row0 = blockIdx.x * 16;
+    const bool xin = row0 + m < N;
+    const bf16 *xp = X + (int64_t)min(row0 + m, N - 1) * ldx + q * 8;
+    const bf16 *wp[NT];
+    bool win[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        win[t] = t * 16 + m < R;
+        wp[t] = W + (int64_t)min(t * 16 + m, R - 1) * K + q * 8;
+    }
+    const u32x4 zero = {0, 0, 0, 0};
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nfull = K / 32;
+    int i = wave;
+    for (; i + 24 < nfull; i += 32) {
+        u32x4 a[4], w[4][NT];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            a[u] = ld_global_16(xp + (i + 8 * u) * 32);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) w[u][t] = ld_global_16(wp[t] + (i + 8 * u) * 32);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                acc[t] = mfma_16x16x32(as_bf16x8(xin ? a[u] : zero), as_bf16x8(win[t] ? w[u][t] : zero), acc[t]);
+    }
+    for (; i < nfull; i += 8) {
+        const u32x4 a = ld_global_16(xp + i * 32);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            acc[t] = mfma_16x16x32(as_bf16x8(xin ? a : zero),
+                                   as_bf16x8(win[t] ? ld_global_16(wp[t] + i * 32) : zero), acc[t]);
+    }
+    if (K % 32 && wave == (nfull & 7)) {
+        // K % 32 == 16: lanes q < 2 hold the last 16 columns, q >= 2 are past K
+        const bool kin = q < 2;
+        const u32x4 a = kin ? ld_global_16(xp + nfull * 32) : zero;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            acc[t] = mfma_16x16x32(as_bf16x8(xin ? a : zero),
+                                   as_bf16x8(win[t] && kin ? ld_global_16(wp[t] + nfull * 32) : zero), acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[wave][t][e][lane] = acc[t][e];
+    __syncthreads();
+    if (wave < NT) {
+        const int t = wave, col = t * 16 + m;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float v = part[0][t][e][lane];
+#pragma unroll
+            for (int w = 1; w < 8; ++w) v += part[w][t][e][lane];
+            const int row = row0 + 4 * q + e;
+            if (row < N && col < R) out[(int64_t)row * ldo + col] = v * s;
+        }
+    }
+}
+
+// expand: Y[n][c] += s * sum_j U[n][j] Wt[c][j], U f32 [N, R] rounded to bf16
+// for the MFMA, Wt [C, R] bf16 contiguous, R <= 32.  One wave per 32 rows x
+// 64 columns (two 32x32 output tiles, k = j).  VEC (16-byte loads of U and
+// Wt rows) needs R % 8 == 0 and 16-byte aligned U and Wt.
+template <bool VEC>
+__device__ __forceinline__ bf16x8 load8_guarded_f32_as_bf16(const float *p, int j0, int R) {
+    float v[8];
+    if (VEC && j0 + 8 <= R) {
+        const f32x4 a = __builtin_bit_cast(f32x4, ld_global_16(p));
+        const f32x4 b = __builtin_bit_cast(f32x4, ld_global_16(p + 4));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = a[e];
+            v[4 + e] = b[e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = j0 + e < R ? p[e] : 0.f;
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = f32_to_bf16(v[e]);
+    return o;
+}
+template <bool VEC>
+__device__ __forceinline__ bf16x8 load8_guarded_bf16(const bf16 *p, int j0, int R) {
+    if (VEC && j0 + 8 <= R) return as_bf16x8(ld_global_16(p));
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = j0 + e < R ? p[e] : (bf16)0.f;
+    return o;
+}
+
+template <bool VEC, bool Y16>
+__global__ __launch_bounds__(256) void lora_expand_mfma_kernel(const float *__restrict__ U, int64_t ldu,
+                                                               const bf16 *__restrict__ Wt, bf16 *Y, int64_t ldy,
+                                                               int N, int C, int R, float s) {
+    // per-wave 32 x 64 f32 result tile; rows padded to 68 floats (16-byte aligned)
+    __shared__ __attribute__((aligned(16))) float tile[4][32][68];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int row0 = blockIdx.y * 32;
+    const int col0 = (blockIdx.x * 4 + wave) * 64;
+    const bool active = col0 < C;  // wave-uniform
+    const int urow = min(row0 + n, N - 1);
+    f32x16 acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+    if (active) {
+        for (int j0 = 0; j0 < R; j0 += 16) {
+            const int ja = j0 + g * 8;
+            const bf16x8 a = ja < R ? load8_guarded_f32_as_bf16<VEC>(U + (int64_t)urow * ldu + ja, ja, R)
+                                    : as_bf16x8(u32x4{0, 0, 0, 0});
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int col = min(col0 + t * 32 + n, C - 1);
+                const bf16x8 b = ja < R ? load8_guarded_bf16<VEC>(Wt + (int64_t)col * R + ja, ja, R)
+                                        : as_bf16x8(u32x4{0, 0, 0, 0});
+                acc[t] = mfma_32x32x16(a, b, acc[t]);
+            }
+        }
+    }
+    // acc[t] element r: row acc_row(r, lane), column t*32 + n of the wave's tile
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tile[wave][acc_row(r, lane)][t * 32 + n] = acc[t][r];
+    __syncthreads();
+    if (!active) return;
+    // each lane updates four 8-column chunks: chunk c = lane + 64k covers tile
+    // row c / 8, columns 8 * (c % 8) .. + 7; C % 16 == 0 keeps a chunk whole
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int tr = (lane >> 3) + 8 * k, tc = 8 * (lane & 7);
+        const int row = row0 + tr, col = col0 + tc;
+        if (row >= N || col >= C) continue;
+        const f32x4 lo = *reinterpret_cast<const f32x4 *>(&tile[wave][tr][tc]);
+        const f32x4 hi = *reinterpret_cast<const f32x4 *>(&tile[wave][tr][tc + 4]);
+        bf16 *y = Y + (int64_t)row * ldy + col;
+        if constexpr (Y16) {
+            bf16x8 v = as_bf16x8(ld_global_16(y));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = f32_to_bf16((float)v[e] + s * lo[e]);
+                v[4 + e] = f32_to_bf16((float)v[4 + e] + s * hi[e]);
+            }
+            st_global_16(y, as_u32x4(v));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[e] = f32_to_bf16((float)y[e] + s * lo[e]);
+                y[4 + e] = f32_to_bf16((float)y[4 + e] + s * hi[e]);
+            }
+        }
+    }
+}
+
 // ---- colsum -------------------------------------------------------------
 // out[j][c] = s * sum_n U[n][j] * X[n][c]  (U f32 [N, R], X [N, C] ldx).
 // Written to out at (j * os_j + c * os_c) so the same kernel yields dA [R, K]
@@ -235,14 +413,32 @@ __global__ void lora_transpose_kernel(const T *__restrict__ src, T *dst, int R, 
 template <typename T>
 hipError_t rowdot(const T *X, int64_t ldx, const T *W, float *out, int64_t ldo, int N, int K,
                   int R, float s, hipStream_t st) {
-    const dim3 grid((N + 127) / 128), block(256);
-    hipLaunchKernelGGL(lora_rowdot_kernel<T>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+    if constexpr (sizeof(T) == 2) {
+        const dim3 grid((unsigned)((N + 15) / 16)), block(512);
+        if (R <= 16)
+            hipLaunchKernelGGL(lora_rowdot16_kernel<1>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+        else
+            hipLaunchKernelGGL(lora_rowdot16_kernel<2>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+    } else {
+        const dim3 grid((N + 127) / 128), block(256);
+        hipLaunchKernelGGL(lora_rowdot_kernel<T>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+    }
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t expand(const float *U, int64_t ldu, const T *Wt, T *Y, int64_t ldy, int N, int C,
                   int R, float s, hipStream_t st) {
+    if constexpr (sizeof(T) == 2) {
+        const dim3 grid((unsigned)((C + 255) / 256), (unsigned)((N + 31) / 32)), block(256);
+        const bool vec = R % 8 == 0 && ldu % 4 == 0 && reinterpret_cast<uintptr_t>(U) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(Wt) % 16 == 0;
+        const bool y16 = ldy % 8 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0;
+        auto kern = vec ? (y16 ? lora_expand_mfma_kernel<true, true> : lora_expand_mfma_kernel<true, false>)
+                        : (y16 ? lora_expand_mfma_kernel<false, true> : lora_expand_mfma_kernel<false, false>);
+        hipLaunchKernelGGL(kern, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s);
+        return hipGetLastError();
+    }
     const int rpb = 64;
     const dim3 grid((C + 63) / 64, (N + rpb - 1) / rpb), block(256);
     hipLaunchKernelGGL(lora_expand_kernel<T>, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s,

@@ -150,3 +150,36 @@ def test_lora_grads_fixture_replay():
                       dev(W("lora_b"), torch.float32), u, dev(dy, torch.float32), 2.0)
     assert rel_l2(host(dA), f["grad/double.img.to_v.lora_a"]) <= 1e-5
     assert rel_l2(host(dB), f["grad/double.img.to_v.lora_b"]) <= 1e-5
+
+
+@pytest.mark.parametrize("r", [4, 12, 32])
+def test_lora_bf16_ranks_ragged(r):
+    """bf16 adapters at ranks that are and are not multiples of 8, a token
+    count that is not a multiple of 32, and B held at a 2-byte offset (the
+    scalar-load path of the expand kernel)."""
+    rng = np.random.default_rng(100 + r)
+    N, K, M, s = 333, 192, 320, 0.5
+    rnd = oracle.bf16_round
+    x = rnd(rng.standard_normal((N, K)).astype(np.float32))
+    Wb = rnd(0.02 * rng.standard_normal((M, K)).astype(np.float32))
+    A = rnd(rng.standard_normal((r, K)).astype(np.float32) / r)
+    B = rnd(0.05 * rng.standard_normal((M, r)).astype(np.float32))
+    dy = rnd(rng.standard_normal((N, M)).astype(np.float32))
+    base = oracle.linear_lora(x, Wb, bf16=True)
+    want = oracle.linear_lora(x, Wb, None, A, B, scale=s, bf16=True)
+    Bbuf = torch.zeros(M * r + 1, dtype=torch.bfloat16, device="cuda")
+    Bv = Bbuf[1:].view(M, r)
+    Bv.copy_(dev(B, torch.bfloat16))
+    y = dev(base, torch.bfloat16)
+    u = lora_fwd(dev(x, torch.bfloat16), dev(A, torch.bfloat16), Bv, y, s)
+    got = host(y)
+    assert max_abs(got, want) <= BF16_MAX_ABS and rel_l2(got, want) <= BF16_REL_L2
+    np.testing.assert_allclose(host(u), x.astype(np.float64) @ A.T.astype(np.float64),
+                               rtol=1e-4, atol=1e-3)
+    dx = dev(np.zeros((N, K), np.float32), torch.bfloat16)
+    dA, dB = lora_bwd(dev(x, torch.bfloat16), dev(A, torch.bfloat16), Bv, u,
+                      dev(dy, torch.bfloat16), s, dx=dx)
+    _, wA, wB = oracle.linear_lora_bwd(x, Wb, A, B, dy, scale=s, bf16=False, want_dx=False)
+    want_dx = (s * (dy.astype(np.float64) @ B) @ A).astype(np.float32)
+    assert rel_l2(host(dA), wA) <= 1e-2 and rel_l2(host(dB), wB) <= 1e-2
+    assert rel_l2(host(dx), want_dx) <= 1e-2
