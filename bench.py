@@ -83,11 +83,33 @@ def make_inputs(cfg, torch, fa):
     return q, k, v, do, keep
 
 
+def _time_steps(torch, step, steps: int, warmup: int):
+    """Wall and GPU-event seconds per call of step() over `steps` timed calls."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def _lora_flops(N, r, fin, fout):
+    """x A^T, u B^T forward; dB, du, dA, dx backward: 6 skinny GEMMs of 2 N r (in or out)."""
+    return 6 * N * r * (fin + fout)
+
+
 def block_bench(torch, steps: int, warmup: int):
-    """c4: one double-stream LoRA block training step (forward, backward to
-    the LoRA factors, AdamW) per step, img 4096 + txt 512 tokens, dim 3072,
-    24 x 128 heads, MLP 4x tanh-GELU, LoRA r16 on q/k/v/out of both streams;
-    synthetic N(0,1) inputs, conditioning and dY; random-init weights."""
+    """c4: one double-stream LoRA block training step per step, as a block
+    inside a stack: forward, backward to the LoRA factors and to the block
+    input (dX through every frozen linear and both layer_norm_mods), AdamW.
+    img 4096 + txt 512 tokens, dim 3072, 24 x 128 heads, MLP 4x tanh-GELU,
+    LoRA r16 on q/k/v/out of both streams; synthetic N(0,1) inputs,
+    conditioning and dY; random-init weights."""
     from foundry_attn import block as fb
     from foundry_attn.configs import C4
     rows = int(round(C4.img_tokens ** 0.5))
@@ -98,27 +120,44 @@ def block_bench(torch, steps: int, warmup: int):
     x = {"img": torch.randn(C4.img_tokens, C4.hidden, device="cuda", generator=g).to(torch.bfloat16),
          "txt": torch.randn(C4.txt_tokens, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)}
     dy = {k: torch.randn(v.shape, device="cuda", generator=g).to(torch.bfloat16) for k, v in x.items()}
-    for _ in range(warmup):
-        blk.train_step(x, dy)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
-        blk.train_step(x, dy)
-    e1.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
-    gpu = e0.elapsed_time(e1) * 1e-3 / steps
-    N, C, F, S, H, D, r = (C4.img_tokens + C4.txt_tokens, C4.hidden, C4.mlp_ratio * C4.hidden,
-                           C4.img_tokens + C4.txt_tokens, C4.heads, C4.head_dim, C4.lora_rank)
-    gemm_fwd = 2 * N * C * 3 * C + 2 * N * C * C + 2 * 2 * N * C * F
-    gemm_bwd = 2 * 2 * N * C * F + 2 * N * C * C  # dX of the MLP and out projections only
-    attn = 14 * H * S * S * D
-    lora = 4 * (2 * N * r * (C + C)) * 3  # fwd + 2 bwd GEMM pairs per adapter, 4 adapters per stream
-    flops = gemm_fwd + gemm_bwd + attn + lora
-    return {"workload": "c4: double-stream LoRA block step (fwd + bwd + AdamW), img 4096 + txt 512 tokens, "
-                        "dim 3072, 24x128 heads, MLP 4x tanh-GELU, LoRA r16 on q/k/v/out of both streams",
+    wall, gpu = _time_steps(torch, lambda: blk.train_step(x, dy, want_dx=True), steps, warmup)
+    N, C, F, H, D, r = (C4.img_tokens + C4.txt_tokens, C4.hidden, C4.mlp_ratio * C4.hidden, C4.heads,
+                        C4.head_dim, C4.lora_rank)
+    gemm = 2 * (2 * N * C * 3 * C + 2 * N * C * C + 2 * 2 * N * C * F)  # forward + dX of every linear
+    attn = 14 * H * N * N * D
+    lora = 4 * _lora_flops(N, r, C, C)
+    flops = gemm + attn + lora
+    return {"workload": "c4: double-stream LoRA block step (fwd + bwd incl. block-input dX + AdamW), "
+                        "img 4096 + txt 512 tokens, dim 3072, 24x128 heads, MLP 4x tanh-GELU, LoRA r16 on "
+                        "q/k/v/out of both streams",
+            "steps": steps, "warmup": warmup, "steps_per_s": round(1.0 / wall, 2),
+            "ms_per_step": round(wall * 1e3, 3), "gpu_ms_per_step": round(gpu * 1e3, 3),
+            "tflops": round(flops / wall / 1e12, 1), "step_tflop": round(flops / 1e12, 3)}
+
+
+def single_block_bench(torch, steps: int, warmup: int):
+    """The single-stream klein block step (fused to_in 3072 -> 27648 with
+    LoRA, QK-RMSNorm + klein RoPE, joint attention over 4608 tokens, SwiGLU
+    3x, fused to_out 12288 -> 3072 with LoRA, one gate), backward including
+    the block-input dX, AdamW on the LoRA factors (r16)."""
+    from foundry_attn import block as fb
+    from foundry_attn.configs import C4
+    rows = int(round(C4.img_tokens ** 0.5))
+    blk = fb.random_single_block(C4.hidden, C4.heads, C4.txt_tokens, rows, C4.img_tokens // rows,
+                                 rank=C4.lora_rank, alpha=C4.lora_alpha)
+    g = torch.Generator(device="cuda").manual_seed(20261029)
+    blk.set_conditioning(torch.randn(C4.hidden, device="cuda", generator=g).to(torch.bfloat16))
+    N = C4.img_tokens + C4.txt_tokens
+    x = torch.randn(N, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(N, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    wall, gpu = _time_steps(torch, lambda: blk.train_step(x, dy, want_dx=True), steps, warmup)
+    C, M, H, D, r = C4.hidden, blk.M, C4.heads, C4.head_dim, C4.lora_rank
+    gemm = 2 * (2 * N * C * (3 * C + 2 * M) + 2 * N * (C + M) * C)
+    attn = 14 * H * N * N * D
+    lora = _lora_flops(N, r, C, 3 * C + 2 * M) + _lora_flops(N, r, C + M, C)
+    flops = gemm + attn + lora
+    return {"workload": "single-stream klein block step (fwd + bwd incl. block-input dX + AdamW), 4608 joint "
+                        "tokens, dim 3072, 24x128 heads, SwiGLU 3x, LoRA r16 on to_in and to_out",
             "steps": steps, "warmup": warmup, "steps_per_s": round(1.0 / wall, 2),
             "ms_per_step": round(wall * 1e3, 3), "gpu_ms_per_step": round(gpu * 1e3, 3),
             "tflops": round(flops / wall / 1e12, 1), "step_tflop": round(flops / 1e12, 3)}
@@ -278,6 +317,7 @@ def main():
     }
     if args.block_steps > 0:
         rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
+        rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.warmup // 4))
     if args.cpu_seconds > 0:
         rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     else:

@@ -211,6 +211,44 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EltParams p) {
     }
 }
 
+// SwiGLU over [N, C] views, 8 elements per thread.  Forward: y = T(T(silu(g))
+// * u).  Backward: du = T(dy * T(silu(g))), dg = T(T(dy * u) * silu'(g)) with
+// silu'(g) = s (1 + g (1 - s)), s = 1 / (1 + e^-g); T() = round to storage.
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+    return (float)(T)x;
+}
+
+template <typename T, bool BWD>
+__global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams p) {
+    const int64_t per_row = p.C / 8;
+    const int64_t total = (int64_t)p.N * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t row = i / per_row;
+        const int e = (int)(i - row * per_row) * 8;
+        float gv[8], uv[8], o[8];
+        load8(static_cast<const T *>(p.gate) + row * p.ldg + e, gv);
+        load8(static_cast<const T *>(p.up) + row * p.ldu + e, uv);
+        if constexpr (!BWD) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = round_to<T>(gv[j] / (1.f + exp2_fast(-kLog2e * gv[j]))) * uv[j];
+        } else {
+            float dv[8], du[8];
+            load8(static_cast<const T *>(p.dy) + row * p.lddy + e, dv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float g = gv[j];
+                const float sg = 1.f / (1.f + exp2_fast(-kLog2e * g));
+                const float silu = round_to<T>(g / (1.f + exp2_fast(-kLog2e * g)));
+                du[j] = dv[j] * silu;
+                o[j] = round_to<T>(dv[j] * uv[j]) * (sg * (1.f + g * (1.f - sg)));
+            }
+            store8(static_cast<T *>(p.dup) + row * p.lddup + e, du);
+        }
+        store8(static_cast<T *>(p.y) + row * p.ldy + e, o);
+    }
+}
+
 // AdamW, weight decay 0, in the reference's operation order:
 //   m' = m*b1 + g*(1-b1);  v' = v*b2 + (g*g)*(1-b2)
 //   p' = p - ((m' * ibc1) / (sqrt(v' * ibc2) + eps)) * lr
@@ -280,6 +318,19 @@ static hipError_t elt_t(const EltParams &p, int op, hipStream_t s) {
 }
 hipError_t launch_elementwise(const EltParams &p, int op, int dtype, hipStream_t s) {
     return dtype == 0 ? elt_t<bf16>(p, op, s) : elt_t<float>(p, op, s);
+}
+
+template <typename T>
+static hipError_t swiglu_t(const SwigluParams &p, bool bwd, hipStream_t s) {
+    const dim3 grid(elt_grid((int64_t)p.N * (p.C / 8))), block(256);
+    if (bwd)
+        hipLaunchKernelGGL((swiglu_kernel<T, true>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((swiglu_kernel<T, false>), grid, block, 0, s, p);
+    return hipGetLastError();
+}
+hipError_t launch_swiglu(const SwigluParams &p, bool bwd, int dtype, hipStream_t s) {
+    return dtype == 0 ? swiglu_t<bf16>(p, bwd, s) : swiglu_t<float>(p, bwd, s);
 }
 
 hipError_t launch_adamw(const AdamwParams &p, int dtype, hipStream_t s) {

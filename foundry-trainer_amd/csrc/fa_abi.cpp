@@ -564,6 +564,57 @@ fa_status fa_gelu_fwd(const fa_rows_args *a, void *stream) { return rows_op(a, 1
 fa_status fa_gelu_bwd(const fa_rows_args *a, void *stream) { return rows_op(a, 2, stream); }
 fa_status fa_silu(const fa_rows_args *a, void *stream) { return rows_op(a, 3, stream); }
 
+static fa_status check_swiglu(const fa_swiglu_args *a) {
+    FA_TRY(check_rows_shape(a->dtype, a->rows, a->cols, 1 << 30));
+    FA_TRY(check_row_view("gate", a->gate, a->ldgate, a->cols, a->dtype));
+    FA_TRY(check_row_view("up", a->up, a->ldup, a->cols, a->dtype));
+    return FA_OK;
+}
+
+fa_status fa_swiglu_fwd(const fa_swiglu_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_swiglu(a));
+    FA_TRY(check_row_view("y", a->y, a->ldy, a->cols, a->dtype));
+    FA_TRY(init_current());
+    fa::SwigluParams p{};
+    p.gate = a->gate;
+    p.ldg = a->ldgate;
+    p.up = a->up;
+    p.ldu = a->ldup;
+    p.y = a->y;
+    p.ldy = a->ldy;
+    p.N = a->rows;
+    p.C = a->cols;
+    const hipError_t e = fa::launch_swiglu(p, false, a->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "swiglu launch");
+    return ok();
+}
+
+fa_status fa_swiglu_bwd(const fa_swiglu_bwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_swiglu(&a->fwd));
+    FA_TRY(check_row_view("dy", a->dy, a->lddy, a->fwd.cols, a->fwd.dtype));
+    FA_TRY(check_row_view("dgate", a->dgate, a->lddgate, a->fwd.cols, a->fwd.dtype));
+    FA_TRY(check_row_view("dup", a->dup, a->lddup, a->fwd.cols, a->fwd.dtype));
+    FA_TRY(init_current());
+    fa::SwigluParams p{};
+    p.gate = a->fwd.gate;
+    p.ldg = a->fwd.ldgate;
+    p.up = a->fwd.up;
+    p.ldu = a->fwd.ldup;
+    p.dy = a->dy;
+    p.lddy = a->lddy;
+    p.y = a->dgate;
+    p.ldy = a->lddgate;
+    p.dup = a->dup;
+    p.lddup = a->lddup;
+    p.N = a->fwd.rows;
+    p.C = a->fwd.cols;
+    const hipError_t e = fa::launch_swiglu(p, true, a->fwd.dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "swiglu backward launch");
+    return ok();
+}
+
 fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
     if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)

@@ -123,6 +123,21 @@ struct EltParams {
 };
 hipError_t launch_elementwise(const EltParams &p, int op, int dtype, hipStream_t s);
 
+struct SwigluParams {
+    const void *gate;
+    int64_t ldg;
+    const void *up;
+    int64_t ldu;
+    const void *dy;  // backward only
+    int64_t lddy;
+    void *y;         // forward output, or dgate in the backward
+    int64_t ldy;
+    void *dup;       // backward only
+    int64_t lddup;
+    int N, C;
+};
+hipError_t launch_swiglu(const SwigluParams &p, bool bwd, int dtype, hipStream_t s);
+
 struct AdamwParams {
     void *param;        // dtype of the op
     const float *grad;  // f32

@@ -26,7 +26,7 @@ EXPORTED = [
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
     # include/foundry_block.h
     "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
-    "fa_adamw_step",
+    "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step",
 ]
 
 
@@ -125,6 +125,20 @@ class RowsArgs(ctypes.Structure):
     ]
 
 
+class SwigluArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+        ("gate", ctypes.c_void_p), ("ldgate", ctypes.c_int64), ("up", ctypes.c_void_p),
+        ("ldup", ctypes.c_int64), ("y", ctypes.c_void_p), ("ldy", ctypes.c_int64),
+    ]
+
+
+class SwigluBwdArgs(ctypes.Structure):
+    _fields_ = [("fwd", SwigluArgs), ("dy", ctypes.c_void_p), ("lddy", ctypes.c_int64),
+                ("dgate", ctypes.c_void_p), ("lddgate", ctypes.c_int64), ("dup", ctypes.c_void_p),
+                ("lddup", ctypes.c_int64)]
+
+
 class AdamwArgs(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32), ("n", ctypes.c_int64), ("param", ctypes.c_void_p),
@@ -167,7 +181,8 @@ def lib() -> ctypes.CDLL:
     L.fa_lora_bwd_workspace_size.argtypes = [ctypes.POINTER(LoraBwdArgs)]
     for name, st in (("fa_ln_mod_fwd", LnModArgs), ("fa_ln_mod_bwd", LnModBwdArgs),
                      ("fa_gated_residual", RowsArgs), ("fa_gelu_fwd", RowsArgs),
-                     ("fa_gelu_bwd", RowsArgs), ("fa_silu", RowsArgs), ("fa_adamw_step", AdamwArgs)):
+                     ("fa_gelu_bwd", RowsArgs), ("fa_silu", RowsArgs), ("fa_adamw_step", AdamwArgs),
+                     ("fa_swiglu_fwd", SwigluArgs), ("fa_swiglu_bwd", SwigluBwdArgs)):
         fn = getattr(L, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]

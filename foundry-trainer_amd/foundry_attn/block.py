@@ -127,6 +127,42 @@ def silu(b, out=None):
     return _rows_op("fa_silu", None, None, b, out)
 
 
+def _same_rows(t: torch.Tensor, ref: torch.Tensor, name: str) -> torch.Tensor:
+    _rows(t, name)
+    if t.shape != ref.shape or t.dtype != ref.dtype or t.device != ref.device:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must match {tuple(ref.shape)} {ref.dtype}")
+    return t
+
+
+def _swiglu_args(gate, up):
+    gate = _rows(gate, "gate")
+    _same_rows(up, gate, "up")
+    N, C = gate.shape
+    return _abi.SwigluArgs(dtype=_dtype_code(gate), rows=N, cols=C, gate=_ptr(gate), ldgate=gate.stride(0),
+                           up=_ptr(up), ldup=up.stride(0))
+
+
+def swiglu(gate, up, out=None):
+    """silu(gate) * up (the activation of swiglu, lib.rs:293-297); gate and up
+    may be column slices of one fused projection output."""
+    a = _swiglu_args(gate, up)
+    y = _like(out, gate)
+    a.y, a.ldy = _ptr(y), y.stride(0)
+    check(lib().fa_swiglu_fwd(ctypes.byref(a), _stream(gate)))
+    return y
+
+
+def swiglu_bwd(dy, gate, up, dgate=None, dup=None):
+    """(dgate, dup) of silu(gate) * up for the upstream gradient dy."""
+    fwd = _swiglu_args(gate, up)
+    _same_rows(dy, gate, "dy")
+    dg, du = _like(dgate, gate, "dgate"), _like(dup, gate, "dup")
+    a = _abi.SwigluBwdArgs(fwd=fwd, dy=_ptr(dy), lddy=dy.stride(0), dgate=_ptr(dg), lddgate=dg.stride(0),
+                           dup=_ptr(du), lddup=du.stride(0))
+    check(lib().fa_swiglu_bwd(ctypes.byref(a), _stream(gate)))
+    return dg, du
+
+
 def adamw_step(param, grad, m, v, step: int, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8):
     """adamw_step (lib.rs:477-510) in place on param (bf16/f32) with f32 grad,
     m, v of the same number of elements."""
@@ -225,14 +261,21 @@ class DoubleBlockLoRA:
             for name in STREAMS:
                 n = self.rows[name]
                 for key, width in (("h", C), ("out", C), ("x1", C), ("h2", C), ("y", C), ("t1", C),
-                                   ("t2", C), ("dx1", C), ("pre", F), ("act", F), ("dact", F), ("mlp", C)):
+                                   ("t2", C), ("dx1", C), ("dx", C), ("pre", F), ("act", F), ("dact", F),
+                                   ("mlp", C)):
                     b[f"{key}.{name}"] = torch.empty((n, width), **kw)
             self._buf = b
         return self._buf
 
-    def forward_backward(self, x: Dict[str, torch.Tensor], dy: Dict[str, torch.Tensor]):
+    def forward_backward(self, x: Dict[str, torch.Tensor], dy: Dict[str, torch.Tensor], want_dx: bool = False):
         """Block outputs y[stream] and the f32 LoRA gradients
-        grads[(stream, target)] = (dA, dB) for upstream gradients dy."""
+        grads[(stream, target)] = (dA, dB) for upstream gradients dy.
+
+        want_dx=False forms what one block's LoRA factors need (Candle's
+        autograd stops at the first layer_norm_mod, whose input tracks no
+        variable); want_dx=True also forms the input gradients of a block
+        inside a stack (dX through the frozen qkv projection and the first
+        layer_norm_mod), returned as grads[(stream, "x")]."""
         B = self._buffers()
         C, S, H, D = self.C, self.S, self.H, self.D
         s = self.lora_scale
@@ -242,7 +285,8 @@ class DoubleBlockLoRA:
         for name in STREAMS:
             w, off, n = self.w[name], self.offset[name], self.rows[name]
             sh1, sc1 = w.mod[0], w.mod[1]
-            h = ln_mod_fwd(x[name], sh1, sc1, self.eps, out=B[f"h.{name}"])
+            h, mean1, rstd1 = ln_mod_fwd(x[name], sh1, sc1, self.eps, out=B[f"h.{name}"], stats=True)
+            saved[(name, "ln1")] = (mean1, rstd1)
             rows = qkv[off:off + n]
             torch.mm(h, w.w_qkv.t(), out=rows)
             for j, t in enumerate(("q", "k", "v")):
@@ -292,23 +336,31 @@ class DoubleBlockLoRA:
             qk_prologue_bwd(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, B["dk"],
                             seq_offset=off, eps=self.eps, dx=drows[:, C:2 * C].view(1, n, H, D))
             h = B[f"h.{name}"]
+            dh = torch.mm(drows, w.w_qkv, out=B[f"t2.{name}"]) if want_dx else None
             for j, t in enumerate(("q", "k", "v")):
                 grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
-                                            drows[:, j * C:(j + 1) * C], s)
+                                            drows[:, j * C:(j + 1) * C], s, dx=dh)
             grads[(name, "out")] = saved[(name, "out", "grad")]
+            if want_dx:
+                mean1, rstd1 = saved[(name, "ln1")]
+                grads[(name, "x")] = ln_mod_bwd(x[name], dh, w.mod[1], mean1, rstd1, self.eps,
+                                                dres=B[f"dx1.{name}"], out=B[f"dx.{name}"])
         return y, grads
 
     def apply_adamw(self, grads, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8) -> None:
         self.step_count += 1
-        for (name, t), (da, db) in grads.items():
+        for (name, t), g in grads.items():
+            if t == "x":
+                continue
+            da, db = g
             w = self.w[name]
             adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
             adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
 
-    def train_step(self, x, dy, lr: float = 1e-3):
+    def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = False):
         """One LoRA block step: forward, backward, AdamW (the unit of the
         'LoRA block steps/s' metric)."""
-        y, grads = self.forward_backward(x, dy)
+        y, grads = self.forward_backward(x, dy, want_dx=want_dx)
         self.apply_adamw(grads, lr)
         return y, grads
 
@@ -339,4 +391,178 @@ def random_block(dim: int, heads: int, txt_tokens: int, img_rows: int, img_cols:
                 w.v[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
         ws[name] = w
     return DoubleBlockLoRA(ws, heads, D, txt_tokens, img_rows, img_cols, axes=axes, theta=theta,
+                           lora_scale=alpha / rank)
+
+
+# ---------------------------------------------------------------------------
+# single-stream block (the real klein layout)
+# ---------------------------------------------------------------------------
+SINGLE_LORA_TARGETS = ("to_in", "to_out")
+
+
+@dataclass
+class SingleWeights:
+    """Frozen weights of one single-stream block and its LoRA factors."""
+    w_in: torch.Tensor    # [3C + 2M, C]: Q, K, V, SwiGLU gate, SwiGLU up
+    w_out: torch.Tensor   # [C, C + M]: over cat(attention, activated MLP)
+    q_norm: torch.Tensor  # [D]
+    k_norm: torch.Tensor  # [D]
+    w_mod: torch.Tensor   # [3C, C]: shift, scale, gate
+    lora_a: Dict[str, torch.Tensor] = field(default_factory=dict)
+    lora_b: Dict[str, torch.Tensor] = field(default_factory=dict)
+    m: Dict[str, torch.Tensor] = field(default_factory=dict)
+    v: Dict[str, torch.Tensor] = field(default_factory=dict)
+    mod: Tuple[torch.Tensor, ...] = ()
+
+
+def klein_positions(txt_tokens: int, img_rows: int, img_cols: int) -> np.ndarray:
+    """Joint position ids, txt first: txt (0, 0, 0, l), img (0, h, w, 0)
+    (throughput.rs:724-748, axes T, H, W, L)."""
+    pos = np.zeros((txt_tokens + img_rows * img_cols, 4), np.float32)
+    pos[:txt_tokens, 3] = np.arange(txt_tokens)
+    rr, cc = np.meshgrid(np.arange(img_rows), np.arange(img_cols), indexing="ij")
+    pos[txt_tokens:, 1] = rr.ravel()
+    pos[txt_tokens:, 2] = cc.ravel()
+    return pos
+
+
+class SingleBlockLoRA:
+    """One single-stream block (single_block, throughput.rs:584-629) with LoRA
+    on its fused in-projection and out-projection:
+
+        nh = layer_norm_mod(x, shift, scale)
+        [q | k | v | gate | up] = to_in(nh)            (C, C, C, M, M columns)
+        attn = attention(rope(rms(q)), rope(rms(k)), v)
+        y = x + g * to_out(cat(attn, silu(gate) * up))
+
+    The fused projection output is one [S, 3C + 2M] buffer: the prologue,
+    the attention and the SwiGLU read their column slices in place, and the
+    attention output and the activation are written straight into the two
+    column slices of the [S, C + M] out-projection input (the reference's
+    narrow / cat become strides).  Default RoPE: the real klein assignment,
+    axes (32, 32, 32, 32), theta 2000 (RESEARCH.md:47, 79 in the reference).
+    """
+
+    def __init__(self, weights: SingleWeights, heads: int, head_dim: int, txt_tokens: int, img_rows: int,
+                 img_cols: int, axes: Sequence[int] = (32, 32, 32, 32), theta: float = 2000.0,
+                 lora_scale: float = 1.0, eps: float = 1e-6):
+        self.w = weights
+        self.H, self.D = heads, head_dim
+        self.C = heads * head_dim
+        self.M = (weights.w_in.shape[0] - 3 * self.C) // 2
+        if weights.w_in.shape != (3 * self.C + 2 * self.M, self.C) or \
+                weights.w_out.shape != (self.C, self.C + self.M):
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "w_in must be [3C+2M, C] and w_out [C, C+M]")
+        self.S = txt_tokens + img_rows * img_cols
+        self.axes = tuple(int(a) for a in axes)
+        self.lora_scale = float(lora_scale)
+        self.eps = float(eps)
+        self.attn_scale = 1.0 / math.sqrt(head_dim)
+        self.dtype, self.device = weights.w_in.dtype, weights.w_in.device
+        self.cos, self.sin = rope_tables(klein_positions(txt_tokens, img_rows, img_cols), self.axes, theta,
+                                         dtype=self.dtype, device=self.device)
+        self.step_count = 0
+        self._buf = None
+
+    def set_conditioning(self, c: torch.Tensor) -> None:
+        """Modulation parts chunk3(silu(c) W_mod^T) (the Mod3 of throughput.rs:284-288)."""
+        m = torch.mm(silu(c.reshape(1, -1)), self.w.w_mod.t()).reshape(-1)
+        self.w.mod = tuple(t.contiguous() for t in m.split(self.C))
+
+    def _buffers(self):
+        if self._buf is None:
+            C, M, S, H, D = self.C, self.M, self.S, self.H, self.D
+            kw = dict(dtype=self.dtype, device=self.device)
+            self._buf = {
+                "nh": torch.empty((S, C), **kw), "fused": torch.empty((S, 3 * C + 2 * M), **kw),
+                "dfused": torch.empty((S, 3 * C + 2 * M), **kw), "joined": torch.empty((S, C + M), **kw),
+                "djoined": torch.empty((S, C + M), **kw), "out": torch.empty((S, C), **kw),
+                "y": torch.empty((S, C), **kw), "dout": torch.empty((S, C), **kw),
+                "dnh": torch.empty((S, C), **kw), "dx": torch.empty((S, C), **kw),
+                "q": torch.empty((1, S, H, D), **kw), "k": torch.empty((1, S, H, D), **kw),
+                "dq": torch.empty((1, S, H, D), **kw), "dk": torch.empty((1, S, H, D), **kw),
+                "lse": torch.empty((1, H, S), dtype=torch.float32, device=self.device),
+                "ws": torch.empty(2 * ((H * S * 4 + 255) // 256) * 256, dtype=torch.uint8, device=self.device)}
+        return self._buf
+
+    def _heads(self, t: torch.Tensor) -> torch.Tensor:
+        """[S, C] column slice (any row stride) as a (1, S, H, D) view."""
+        return t.as_strided((1, self.S, self.H, self.D), (self.S * t.stride(0), t.stride(0), self.D, 1))
+
+    def forward_backward(self, x: torch.Tensor, dy: torch.Tensor, want_dx: bool = True):
+        """Block output y and the f32 LoRA gradients grads[target] = (dA, dB);
+        with want_dx (a block inside a stack) also grads["x"] = dL/dx."""
+        B = self._buffers()
+        C, M = self.C, self.M
+        s = self.lora_scale
+        w = self.w
+        sh, sc, g = w.mod
+        fused, dfused, joined, djoined = B["fused"], B["dfused"], B["joined"], B["djoined"]
+        nh, mean, rstd = ln_mod_fwd(x, sh, sc, self.eps, out=B["nh"], stats=True)
+        torch.mm(nh, w.w_in.t(), out=fused)
+        u_in = lora_fwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], fused, s)
+        q_raw, k_raw, v = self._heads(fused[:, :C]), self._heads(fused[:, C:2 * C]), self._heads(fused[:, 2 * C:3 * C])
+        qk_prologue(q_raw, w.q_norm, self.cos, self.sin, self.axes, self.eps, out=B["q"])
+        qk_prologue(k_raw, w.k_norm, self.cos, self.sin, self.axes, self.eps, out=B["k"])
+        o = self._heads(joined[:, :C])
+        attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=o, lse=B["lse"])
+        gate, up = fused[:, 3 * C:3 * C + M], fused[:, 3 * C + M:]
+        swiglu(gate, up, out=joined[:, C:])
+        out = torch.mm(joined, w.w_out.t(), out=B["out"])
+        u_out = lora_fwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], out, s)
+        y = gated_residual(x, g, out, out=B["y"])
+        # backward: y = x + g * to_out(joined)
+        dout = gated_residual(None, g, dy, out=B["dout"])
+        torch.mm(dout, w.w_out, out=djoined)
+        grads = {"to_out": lora_bwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], u_out, dout, s, dx=djoined)}
+        swiglu_bwd(djoined[:, C:], gate, up, dgate=dfused[:, 3 * C:3 * C + M], dup=dfused[:, 3 * C + M:])
+        attn_bwd(B["q"], B["k"], v, o, self._heads(djoined[:, :C]), B["lse"], self.attn_scale, None,
+                 workspace=B["ws"], out=(B["dq"], B["dk"], self._heads(dfused[:, 2 * C:3 * C])))
+        qk_prologue_bwd(q_raw, w.q_norm, self.cos, self.sin, self.axes, B["dq"], eps=self.eps,
+                        dx=self._heads(dfused[:, :C]))
+        qk_prologue_bwd(k_raw, w.k_norm, self.cos, self.sin, self.axes, B["dk"], eps=self.eps,
+                        dx=self._heads(dfused[:, C:2 * C]))
+        dnh = torch.mm(dfused, w.w_in, out=B["dnh"]) if want_dx else None
+        grads["to_in"] = lora_bwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], u_in, dfused, s, dx=dnh)
+        if want_dx:
+            grads["x"] = ln_mod_bwd(x, dnh, sc, mean, rstd, self.eps, dres=dy, out=B["dx"])
+        return y, grads
+
+    def apply_adamw(self, grads, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8) -> None:
+        self.step_count += 1
+        w = self.w
+        for t in SINGLE_LORA_TARGETS:
+            da, db = grads[t]
+            adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
+            adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
+
+    def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = True):
+        y, grads = self.forward_backward(x, dy, want_dx=want_dx)
+        self.apply_adamw(grads, lr)
+        return y, grads
+
+
+def random_single_block(dim: int, heads: int, txt_tokens: int, img_rows: int, img_cols: int,
+                        mlp_ratio: int = 3, rank: int = 16, alpha: float = 16.0, dtype=torch.bfloat16,
+                        device="cuda", seed: int = 20261029, axes=(32, 32, 32, 32),
+                        theta: float = 2000.0) -> SingleBlockLoRA:
+    """Random init as random_block: base W ~ N(0, 0.02) frozen, LoRA A ~
+    N(0, 1/r), B ~ N(0, 1e-3), QK-norm scales 1 + N(0, 0.02)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    C, M = dim, mlp_ratio * dim
+    D = dim // heads
+
+    def rn(*shape, std):
+        return (torch.randn(*shape, generator=g) * std).to(dtype=dtype, device=device)
+
+    w = SingleWeights(w_in=rn(3 * C + 2 * M, C, std=0.02), w_out=rn(C, C + M, std=0.02),
+                      q_norm=(1 + rn(D, std=0.02).float()).to(dtype), k_norm=(1 + rn(D, std=0.02).float()).to(dtype),
+                      w_mod=rn(3 * C, C, std=0.02))
+    for t, (fin, fout) in (("to_in", (C, 3 * C + 2 * M)), ("to_out", (C + M, C))):
+        w.lora_a[t] = rn(rank, fin, std=1.0 / rank)
+        w.lora_b[t] = rn(fout, rank, std=1e-3)
+        for part, shape in (("a", (rank, fin)), ("b", (fout, rank))):
+            w.m[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
+            w.v[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
+    return SingleBlockLoRA(w, heads, D, txt_tokens, img_rows, img_cols, axes=axes, theta=theta,
                            lora_scale=alpha / rank)

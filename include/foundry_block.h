@@ -10,6 +10,9 @@
  *   MLP activation   (c4 block: tanh-GELU; the reference block's SwiGLU,
  *                    lib.rs:293-297, has no tanh-GELU counterpart)
  *                                        fa_gelu_fwd / fa_gelu_bwd
+ *   swiglu           lib.rs:293-297 (the activation between its linears;
+ *                    single block throughput.rs:620)
+ *                                        fa_swiglu_fwd / fa_swiglu_bwd
  *   modulation input silu(temb)  throughput.rs:297-324     fa_silu
  *   adamw_step       lib.rs:477-510      fa_adamw_step
  *
@@ -89,6 +92,38 @@ fa_status fa_gelu_bwd(const fa_rows_args *args, void *stream);
 /* y = b / (1 + exp(-b)) (x unused): the SiLU of the conditioning vector that
  * feeds the frozen modulation linear (throughput.rs:297-324). */
 fa_status fa_silu(const fa_rows_args *args, void *stream);
+
+typedef struct fa_swiglu_args {
+    int32_t dtype;        /* fa_dtype of every view                              */
+    int32_t rows, cols;   /* N >= 1; C % 8 == 0                                  */
+    const void *gate;     /* [N, C] gate projection (pre-activation)             */
+    int64_t ldgate;
+    const void *up;       /* [N, C] up projection                                */
+    int64_t ldup;
+    void *y;              /* [N, C] output (fwd)                                 */
+    int64_t ldy;
+} fa_swiglu_args;
+
+/* y = silu(gate) * up, silu(g) = g / (1 + exp(-g)) rounded to the storage
+ * dtype before the product (Candle's silu op result, then its mul):
+ * replaces the silu + mul of swiglu (lib.rs:293-297) and of the single block
+ * (throughput.rs:620). */
+fa_status fa_swiglu_fwd(const fa_swiglu_args *args, void *stream);
+
+typedef struct fa_swiglu_bwd_args {
+    fa_swiglu_args fwd;   /* gate, up as in the forward; y unused                */
+    const void *dy;       /* [N, C] gradient of y                                */
+    int64_t lddy;
+    void *dgate;          /* [N, C] output: (dy * up) * silu'(gate)              */
+    int64_t lddgate;
+    void *dup;            /* [N, C] output: dy * silu(gate)                      */
+    int64_t lddup;
+} fa_swiglu_bwd_args;
+
+/* The gradients Candle's autograd forms through silu(gate) * up, with
+ * silu'(g) = s(g) (1 + g (1 - s(g))), s = sigmoid; dy*up and dy*silu(gate) are
+ * rounded to the storage dtype as the mul's backward products. */
+fa_status fa_swiglu_bwd(const fa_swiglu_bwd_args *args, void *stream);
 
 typedef struct fa_adamw_args {
     int32_t dtype;        /* fa_dtype of param                                   */

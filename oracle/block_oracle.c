@@ -100,6 +100,33 @@ void oracle_silu(const float *b, long n, int bf16, float *y) {
     for (long i = 0; i < n; ++i) y[i] = rnd((float)(b[i] / (1.0 + exp(-(double)b[i]))), bf16);
 }
 
+/* swiglu activation, lib.rs:293-297 (and gen_block.py:167, throughput.rs:620):
+ * y = silu(gate) * up, the silu op's result rounded to the tensor dtype
+ * before the mul.  Computed in f64, rounded at the two op results. */
+void oracle_swiglu_fwd(const float *gate, const float *up, long n, int bf16, float *y) {
+    for (long i = 0; i < n; ++i) {
+        const double g = gate[i];
+        const float s = rnd((float)(g / (1.0 + exp(-g))), bf16);
+        y[i] = rnd((float)((double)s * up[i]), bf16);
+    }
+}
+
+/* Backward of the above by the chain rule (the autograd of mul, then silu):
+ *   dup   = dy * silu(gate)                     (mul backward, one product)
+ *   dgate = (dy * up) * sig(g) (1 + g (1 - sig(g)))
+ * dy * up and each result rounded to the tensor dtype. */
+void oracle_swiglu_bwd(const float *dy, const float *gate, const float *up, long n, int bf16, float *dgate,
+                       float *dup) {
+    for (long i = 0; i < n; ++i) {
+        const double g = gate[i];
+        const double sg = 1.0 / (1.0 + exp(-g));
+        const float s = rnd((float)(g * sg), bf16);
+        dup[i] = rnd((float)((double)dy[i] * s), bf16);
+        const float dgu = rnd((float)((double)dy[i] * up[i]), bf16);
+        dgate[i] = rnd((float)((double)dgu * sg * (1.0 + g * (1.0 - sg))), bf16);
+    }
+}
+
 /* lib.rs:477-510 with f32 tensors: the AdamW constants are f64, and
  * affine(mul, add) multiplies / adds them cast to f32; 1 - beta and
  * bc = 1 - beta^step are formed in f64.  bf16 != 0 rounds the updated

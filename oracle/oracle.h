@@ -83,6 +83,9 @@ void oracle_gated_residual(const float *x, const float *g, const float *b, long 
 void oracle_gelu_fwd(const float *b, long n, int bf16, float *y);
 void oracle_gelu_bwd(const float *dy, const float *b, long n, int bf16, float *y);
 void oracle_silu(const float *b, long n, int bf16, float *y);
+void oracle_swiglu_fwd(const float *gate, const float *up, long n, int bf16, float *y);
+void oracle_swiglu_bwd(const float *dy, const float *gate, const float *up, long n, int bf16, float *dgate,
+                       float *dup);
 void oracle_adamw_step(float *param, const float *grad, float *m, float *v, long n, double lr, double beta1,
                        double beta2, double eps, int step, int bf16);
 

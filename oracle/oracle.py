@@ -75,6 +75,8 @@ def lib():
         L.oracle_gelu_fwd.argtypes = [_f32p, ctypes.c_long, ctypes.c_int, _f32p]
         L.oracle_gelu_bwd.argtypes = [_f32p, _f32p, ctypes.c_long, ctypes.c_int, _f32p]
         L.oracle_silu.argtypes = [_f32p, ctypes.c_long, ctypes.c_int, _f32p]
+        L.oracle_swiglu_fwd.argtypes = [_f32p, _f32p, ctypes.c_long, ctypes.c_int, _f32p]
+        L.oracle_swiglu_bwd.argtypes = [_f32p, _f32p, _f32p, ctypes.c_long, ctypes.c_int, _f32p, _f32p]
         L.oracle_adamw_step.argtypes = [_f32p] * 4 + [ctypes.c_long] + [ctypes.c_double] * 4 + [
             ctypes.c_int, ctypes.c_int]
         _lib = L
@@ -279,6 +281,22 @@ def silu(b, bf16=False):
     y = np.empty_like(b)
     lib().oracle_silu(_p(b), b.size, int(bf16), _p(y))
     return y
+
+
+def swiglu_fwd(gate, up, bf16=False):
+    """silu(gate) * up (lib.rs:293-297)."""
+    g, u = _c(gate), _c(up)
+    y = np.empty_like(g)
+    lib().oracle_swiglu_fwd(_p(g), _p(u), g.size, int(bf16), _p(y))
+    return y
+
+
+def swiglu_bwd(dy, gate, up, bf16=False):
+    """(dgate, dup) of silu(gate) * up."""
+    g, u, d = _c(gate), _c(up), _c(dy)
+    dg, du = np.empty_like(g), np.empty_like(g)
+    lib().oracle_swiglu_bwd(_p(d), _p(g), _p(u), g.size, int(bf16), _p(dg), _p(du))
+    return dg, du
 
 
 def adamw_step(param, grad, m, v, step, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, bf16=False):

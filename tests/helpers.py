@@ -44,6 +44,25 @@ def load_block_golden(tag: str) -> dict:
             load_file(os.path.join(GOLDEN, f"block_fixture_{tag}.safetensors")).items()}
 
 
+def load_pipeline_golden(tag: str) -> dict:
+    """Everything the reference fixture's whole pipeline touches, as float32
+    numpy: the attention, block and pipeline subsets merged.  For bf16 the
+    weights are the bf16 casts of the fp32 ones (what the reference fixture
+    holds, checked when the subsets were extracted) and the activations,
+    gradients and targets come from the bf16 files."""
+    from safetensors.torch import load_file
+    f = {}
+    for name in ("attn", "block", "pipeline"):
+        f.update({k: v.float().numpy() for k, v in
+                  load_file(os.path.join(GOLDEN, f"{name}_fixture_fp32.safetensors")).items()})
+    if tag == "bf16":
+        f = {k: (bf16_round(v) if k.startswith(("weights/", "inputs/")) else v) for k, v in f.items()}
+        for name in ("attn", "block", "pipeline"):
+            f.update({k: v.float().numpy() for k, v in
+                      load_file(os.path.join(GOLDEN, f"{name}_fixture_bf16.safetensors")).items()})
+    return f
+
+
 def bf16_round(a):
     import oracle
     return oracle.bf16_round(a)

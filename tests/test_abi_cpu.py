@@ -50,7 +50,8 @@ def test_struct_layouts_match_header(tmp_path):
                "fa_qk_prologue_bwd_args": _abi.QkPrologueBwdArgs, "fa_lora_args": _abi.LoraArgs,
                "fa_lora_bwd_args": _abi.LoraBwdArgs, "fa_ln_mod_args": _abi.LnModArgs,
                "fa_ln_mod_bwd_args": _abi.LnModBwdArgs, "fa_rows_args": _abi.RowsArgs,
-               "fa_adamw_args": _abi.AdamwArgs}
+               "fa_adamw_args": _abi.AdamwArgs, "fa_swiglu_args": _abi.SwigluArgs,
+               "fa_swiglu_bwd_args": _abi.SwigluBwdArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{BLOCK_HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -226,3 +227,25 @@ def test_block_ops_validate_before_device_work():
         setattr(bad, field, val)
         assert L.fa_adamw_step(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
 
+
+
+def test_swiglu_validate_before_device_work():
+    L = lib()
+    ok_dev = _abi.FA_OK if gpu_available() else _abi.FA_ERR_NO_DEVICE
+    sw = _abi.SwigluArgs(dtype=0, rows=4, cols=9216, gate=_FAKE, ldgate=27648, up=_FAKE + 18432,
+                         ldup=27648, y=_FAKE, ldy=12288)
+    if not gpu_available():
+        assert L.fa_swiglu_fwd(ctypes.byref(sw), None) == ok_dev
+    for field, val in (("cols", 9212), ("rows", 0), ("dtype", 3), ("gate", 0), ("up", _FAKE + 2),
+                       ("ldgate", 9000), ("ldy", 12290), ("y", 0)):
+        bad = _abi.SwigluArgs.from_buffer_copy(sw)
+        setattr(bad, field, val)
+        assert L.fa_swiglu_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+    bw = _abi.SwigluBwdArgs(fwd=sw, dy=_FAKE, lddy=9216, dgate=_FAKE, lddgate=27648, dup=_FAKE,
+                            lddup=27648)
+    if not gpu_available():
+        assert L.fa_swiglu_bwd(ctypes.byref(bw), None) == ok_dev
+    for field, val in (("dy", 0), ("dgate", _FAKE + 8), ("lddup", 100)):
+        bad = _abi.SwigluBwdArgs.from_buffer_copy(bw)
+        setattr(bad, field, val)
+        assert L.fa_swiglu_bwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field

@@ -11,7 +11,7 @@ import torch
 
 import block_ref  # noqa: E402  (oracle/ on sys.path via conftest)
 import oracle
-from block_case import make_case, oracle_mods
+from block_case import make_case, make_single_case, oracle_mods, single_oracle_mods
 from foundry_attn import block as fb
 from helpers import max_abs, rel_l2
 
@@ -66,6 +66,39 @@ def test_block_ops_match_oracle(dtype, C):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_swiglu_fused_views_match_oracle(dtype):
+    """silu(gate) * up and its gradients with gate and up read as column
+    slices of one fused projection output [N, 3C + 2M] (the single block's
+    layout) and the results written into column slices of wider buffers."""
+    bf = dtype == torch.bfloat16
+    rng = np.random.default_rng(7)
+    rnd = (lambda a: oracle.bf16_round(a.astype(np.float32))) if bf else (lambda a: a.astype(np.float32))
+    N, C, M = 333, 256, 768
+    fused = rnd(2.0 * rng.standard_normal((N, 3 * C + 2 * M)))
+    gate, up = fused[:, 3 * C:3 * C + M], fused[:, 3 * C + M:]
+    dy = rnd(rng.standard_normal((N, M)))
+    tf = dev(fused, dtype)
+    tg, tu = tf[:, 3 * C:3 * C + M], tf[:, 3 * C + M:]
+    joined = torch.zeros(N, C + M, dtype=dtype, device="cuda")
+    y = fb.swiglu(tg, tu, out=joined[:, C:])
+    assert y.data_ptr() == joined[:, C:].data_ptr()
+    wy = oracle.swiglu_fwd(gate, up, bf16=bf)
+    dfused = torch.zeros_like(tf)
+    dg, du = fb.swiglu_bwd(dev(dy, dtype), tg, tu, dgate=dfused[:, 3 * C:3 * C + M], dup=dfused[:, 3 * C + M:])
+    wdg, wdu = oracle.swiglu_bwd(dy, gate, up, bf16=bf)
+    for name, got, want in (("swiglu", host(joined[:, C:]), wy), ("dgate", host(dg), wdg), ("dup", host(du), wdu)):
+        r = rel_l2(got, want)
+        print(f"  {name} {dtype}: rel_l2={r:.2e} max_abs={max_abs(got, want):.2e}", flush=True)
+        if bf:
+            assert r <= 1e-2 and max_abs(got, want) <= 2e-2 * max(1.0, float(np.abs(want).max())), name
+        else:
+            assert r <= 1e-5, name
+    # nothing outside the slices was written
+    assert float(joined[:, :C].abs().max()) == 0.0
+    assert float(dfused[:, :3 * C].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_adamw_matches_oracle_over_steps(dtype):
     bf = dtype == torch.bfloat16
     rng = np.random.default_rng(1)
@@ -113,7 +146,8 @@ def device_block(case, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_block_step_matches_oracle(dtype):
+@pytest.mark.parametrize("want_dx", [False, True])
+def test_block_step_matches_oracle(dtype, want_dx):
     bf = dtype == torch.bfloat16
     case = oracle_mods(make_case(C=256, H=2, T=16, rows=4, cols=8, r=4, bf16=bf, seed=5))
     blk = device_block(case, dtype)
@@ -123,16 +157,23 @@ def test_block_step_matches_oracle(dtype):
             assert r <= (1e-2 if bf else 1e-5), (name, i, r)
     x = {k: dev(v, dtype) for k, v in case["x"].items()}
     dy = {k: dev(v, dtype) for k, v in case["dy"].items()}
-    y, grads = blk.train_step(x, dy)
+    y, grads = blk.train_step(x, dy, want_dx=want_dx)
     torch.cuda.synchronize()
     wy, wgrads, wupd = block_ref.block_step(case["x"], case["dy"], case["W"], case["H"], case["D"], case["cos"],
-                                            case["sin"], case["axes"], case["scale"], bf16=bf)
+                                            case["sin"], case["axes"], case["scale"], bf16=bf, want_dx=want_dx)
     gate = 2e-2 if bf else 1e-3
     for name in ("txt", "img"):
         r = rel_l2(host(y[name]), wy[name])
         print(f"  y.{name}: rel_l2={r:.2e}", flush=True)
         assert r <= gate
-    for key, (wa, wb) in wgrads.items():
+        if want_dx:
+            r = rel_l2(host(grads[(name, "x")]), wgrads[(name, "x")])
+            print(f"  dx.{name}: rel_l2={r:.2e}", flush=True)
+            assert r <= gate
+    for key, g in wgrads.items():
+        if key[1] == "x":
+            continue
+        wa, wb = g
         da, db = grads[key]
         ra, rb = rel_l2(host(da), wa), rel_l2(host(db), wb)
         print(f"  grad {key}: dA {ra:.2e} dB {rb:.2e}", flush=True)
@@ -180,3 +221,81 @@ def test_c4_block_step_properties():
     for k, (a0, b0) in before.items():
         assert not torch.equal(a0, blk.w[k[0]].lora_a[k[1]]), k
         assert not torch.equal(b0, blk.w[k[0]].lora_b[k[1]]), k
+
+
+def device_single_block(case, dtype):
+    W = case["W"]
+    w = fb.SingleWeights(w_in=dev(W["w_in"], dtype), w_out=dev(W["w_out"], dtype), q_norm=dev(W["q_norm"], dtype),
+                         k_norm=dev(W["k_norm"], dtype), w_mod=dev(W["w_mod"], dtype))
+    for t in fb.SINGLE_LORA_TARGETS:
+        w.lora_a[t], w.lora_b[t] = dev(W["lora_a"][t], dtype), dev(W["lora_b"][t], dtype)
+        for part, arr in (("a", W["lora_a"][t]), ("b", W["lora_b"][t])):
+            w.m[f"{t}.{part}"] = torch.zeros(arr.shape, dtype=torch.float32, device="cuda")
+            w.v[f"{t}.{part}"] = torch.zeros(arr.shape, dtype=torch.float32, device="cuda")
+    blk = fb.SingleBlockLoRA(w, case["H"], case["D"], case["T"], case["rows"], case["cols"], axes=case["axes"],
+                             theta=case["theta"], lora_scale=case["scale"])
+    blk.set_conditioning(dev(case["c"], dtype))
+    return blk
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_single_block_step_matches_oracle(dtype):
+    """The single-stream klein block (fused to_in -> q/k/v + SwiGLU, fused
+    to_out over cat(attention, activation), one gate), LoRA on both fused
+    projections, klein RoPE (axes 32 x 4, theta 2000, txt (0,0,0,l), img
+    (0,h,w,0)); one train step with the input gradient, against the oracle
+    restatement."""
+    bf = dtype == torch.bfloat16
+    case = single_oracle_mods(make_single_case(C=256, H=2, T=40, rows=8, cols=12, r=4, bf16=bf, seed=9))
+    blk = device_single_block(case, dtype)
+    for i in range(3):
+        r = rel_l2(host(blk.w.mod[i]), case["W"]["mod"][i])
+        assert r <= (1e-2 if bf else 1e-5), (i, r)
+    np.testing.assert_array_equal(host(blk.cos), case["cos"])
+    y, grads = blk.train_step(dev(case["x"], dtype), dev(case["dy"], dtype))
+    torch.cuda.synchronize()
+    wy, wgrads, wupd, wdx = block_ref.single_block_step(case["x"], case["dy"], case["W"], case["H"], case["D"],
+                                                        case["cos"], case["sin"], case["axes"], case["scale"],
+                                                        bf16=bf)
+    gate = 2e-2 if bf else 1e-3
+    for name, got, want in (("y", host(y), wy), ("dx", host(grads["x"]), wdx)):
+        r = rel_l2(got, want)
+        print(f"  {name}: rel_l2={r:.2e}", flush=True)
+        assert r <= gate, name
+    for t in fb.SINGLE_LORA_TARGETS:
+        (da, db), (wa, wb) = grads[t], wgrads[t]
+        ra, rb = rel_l2(host(da), wa), rel_l2(host(db), wb)
+        print(f"  grad {t}: dA {ra:.2e} dB {rb:.2e}", flush=True)
+        assert ra <= gate and rb <= gate, t
+        a1, b1 = wupd[t]
+        step_a = host(blk.w.lora_a[t]) - case["W"]["lora_a"][t]
+        step_b = host(blk.w.lora_b[t]) - case["W"]["lora_b"][t]
+        agree = (np.mean(np.sign(step_a) == np.sign(a1 - case["W"]["lora_a"][t])),
+                 np.mean(np.sign(step_b) == np.sign(b1 - case["W"]["lora_b"][t])))
+        print(f"  update {t}: sign agreement {agree[0]:.4f} {agree[1]:.4f}", flush=True)
+        assert min(agree) >= (0.97 if bf else 0.999), t
+
+
+def test_klein_single_block_step_properties():
+    """The single block at klein size (dim 3072, 24 heads, MLP 3 x dim, 512 txt
+    + 4096 img tokens): finite outputs and gradients, bit-for-bit repeatable,
+    nonzero LoRA gradients."""
+    from foundry_attn.configs import C4
+    rows = int(C4.img_tokens ** 0.5)
+    blk = fb.random_single_block(C4.hidden, C4.heads, C4.txt_tokens, rows, C4.img_tokens // rows,
+                                 rank=C4.lora_rank, alpha=C4.lora_alpha)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    blk.set_conditioning(torch.randn(C4.hidden, device="cuda", generator=g).to(torch.bfloat16))
+    S = C4.txt_tokens + C4.img_tokens
+    x = torch.randn(S, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(S, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    y1, g1 = blk.forward_backward(x, dy)
+    y1 = y1.clone()
+    g1 = {k: (tuple(t.clone() for t in v) if isinstance(v, tuple) else v.clone()) for k, v in g1.items()}
+    y2, g2 = blk.forward_backward(x, dy)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y1.float()).all() and torch.equal(y1, y2)
+    assert torch.isfinite(g1["x"].float()).all() and torch.equal(g1["x"], g2["x"])
+    for t in fb.SINGLE_LORA_TARGETS:
+        for a, b in zip(g1[t], g2[t]):
+            assert torch.isfinite(a).all() and float(a.abs().max()) > 0 and torch.equal(a, b), t
