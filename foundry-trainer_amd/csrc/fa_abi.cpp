@@ -263,6 +263,8 @@ static fa_status check_prologue(const fa_qk_prologue_args *a) {
         return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", a->dtype);
     if (a->batch < 1 || a->tokens < 1 || a->heads < 1)
         return fail(FA_ERR_INVALID_ARG, "batch/tokens/heads must be >= 1");
+    if ((int64_t)a->tokens * a->heads >= (int64_t(1) << 31) || a->batch > 65535)
+        return fail(FA_ERR_UNSUPPORTED, "tokens * heads must be < 2^31 and batch <= 65535");
     if (a->head_dim != 64 && a->head_dim != 128)
         return fail(FA_ERR_UNSUPPORTED, "head_dim %d: this build implements 64 and 128", a->head_dim);
     if (!(a->eps >= 0.f) || !isfinite(a->eps)) return fail(FA_ERR_INVALID_ARG, "eps must be finite, >= 0");

@@ -64,6 +64,7 @@ struct QkPrologueParams {
     float eps;
     int n_axes;
     int axes[8];
+    float inv_h;  // 1 / H, set by the launcher
 };
 
 hipError_t launch_qk_prologue_fwd(const QkPrologueParams &p, int dtype, hipStream_t s);

@@ -19,6 +19,8 @@
 //   dx = (dn - n * mean(dn * n)) / sigma
 #include <math.h>
 
+#include <type_traits>
+
 #include "fa_device.hpp"
 #include "fa_kernels.hpp"
 
@@ -62,151 +64,262 @@ __device__ __forceinline__ void rope_partner(const QkPrologueParams &p, int d, i
     }
 }
 
-template <typename T, int D>
+// x / d for every x of a row with one reciprocal per row: q0 = x * r (r =
+// v_rcp_f32(d), within 1 ulp), the exact remainder e = x - q0 * d by FMA, and
+// q = q0 + e * r: the correctly rounded quotient except for rare operands
+// within a fraction of an ulp of a rounding midpoint (Markstein's correction
+// step).  Replaces the IEEE division sequence, about 10 instructions each.
+__device__ __forceinline__ float div_by(float x, float d, float r) {
+    const float q0 = x * r;
+    const float e = __builtin_fmaf(-q0, d, x);
+    return __builtin_fmaf(e, r, q0);
+}
+
+// 16 / sizeof(T) consecutive elements as f32: one 16-byte load when VEC (the
+// pointer is 16-byte aligned), else element loads.
+template <typename T, bool VEC>
+__device__ __forceinline__ void load_row_part(const T *ptr, float (&v)[16 / sizeof(T)]) {
+    constexpr int EPL = 16 / sizeof(T);
+    if constexpr (VEC) {
+        const u32x4 raw = ld_global_16(ptr);
+        const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) v[i] = (float)e[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) v[i] = (float)ptr[i];
+    }
+}
+
+// Sum over the LPR consecutive lanes holding one row; every lane gets the
+// sum.  LPR <= 16 stays in registers through DPP (quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror: each step adds a disjoint partner
+// group, so after log2(LPR) steps every lane holds the full sum); wider rows
+// (the f32 D = 128 layout) use cross-lane shuffles.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+    if constexpr (LPR <= 16) {
+        auto dpp = [](float x, auto ctrl) {
+            return __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value, 0xF, 0xF, false));
+        };
+        v += dpp(v, std::integral_constant<int, 0xB1>{});
+        if constexpr (LPR >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});
+        if constexpr (LPR >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});
+        if constexpr (LPR >= 16) v += dpp(v, std::integral_constant<int, 0x140>{});
+    } else {
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    }
+    return v;
+}
+
+// Rotate-half partner table: tab[d] = partner(d) - d, whose sign gives the
+// sign of rot (first half of a segment takes -x[d + half]).  Threads d < D
+// fill it; the kernel's barrier orders the fill before any read.
+template <int D>
+__device__ __forceinline__ void fill_partner_table(const QkPrologueParams &p, signed char *tab) {
+    const int d = threadIdx.x;
+    if (d < D) {
+        int pd;
+        float sg;
+        rope_partner(p, d, pd, sg);
+        tab[d] = (signed char)(pd - d);
+    }
+}
+
+// Token and head of row r0 + off of batch item blockIdx.y, with (t0, h0) the
+// workgroup's first row: off < 64 and h0 < H keep u = h0 + off small enough
+// for an exact f32 quotient estimate, corrected by one step either way.
+__device__ __forceinline__ void row_token_head(const QkPrologueParams &p, int t0, int h0, int off, int &t, int &h) {
+    const int u = h0 + off;
+    int q = (int)((float)u * p.inv_h);
+    int r = u - q * p.H;
+    if (r >= p.H) {
+        ++q;
+        r -= p.H;
+    } else if (r < 0) {
+        --q;
+        r += p.H;
+    }
+    t = t0 + q;
+    h = r;
+}
+
+// Rows are (b, token, head) triples in row-major order; a workgroup covers
+// R passes of RPP rows, every lane holding 16 bytes of one row per pass.  All
+// global loads of the R rows (x, and the token's cos / sin rows) are issued
+// before any arithmetic.  Rows past the end load the last row and store
+// nothing.  VEC: cos, sin and weight are 16-byte aligned.
+template <typename T, int D, int R, bool VEC>
 __global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QkPrologueParams p) {
     // one rounding per reference op: no FMA contraction of x*cos + rot*sin
 #pragma clang fp contract(off)
     constexpr int EPL = 16 / sizeof(T);   // elements per lane
     constexpr int LPR = D / EPL;          // lanes per row
-    constexpr int RPB = 256 / LPR;        // rows per block
-    __shared__ float buf[RPB][D];
+    constexpr int RPP = 256 / LPR;        // rows per pass
+    __shared__ __attribute__((aligned(16))) float buf[R][RPP][D];
     const int tid = threadIdx.x, lr = tid / LPR, part = tid % LPR;
-    const int64_t rows = (int64_t)p.B * p.T * p.H;
-    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
-    const bool live = row < rows;
-    int b = 0, t = 0, h = 0;
-    if (live) {
-        h = row % p.H;
-        t = (row / p.H) % p.T;
-        b = row / ((int64_t)p.H * p.T);
+    const int rows = p.T * p.H;  // per batch item (< 2^31, checked by the ABI)
+    const int64_t b = blockIdx.y;
+    const int r0 = (int)blockIdx.x * (R * RPP);
+    const int t0 = r0 / p.H, h0 = r0 - t0 * p.H;
+    __shared__ __attribute__((aligned(16))) signed char ptab[D];
+    fill_partner_table<D>(p, ptab);
+    float wv[EPL];
+    load_row_part<T, VEC>(static_cast<const T *>(p.w) + part * EPL, wv);
+    float xv[R][EPL], cv[R][EPL], sv[R][EPL];
+    int64_t yoff[R];
+    bool live[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int off0 = k * RPP + lr;
+        live[k] = r0 + off0 < rows;
+        const int off = live[k] ? off0 : rows - 1 - r0;
+        int ti, hi;
+        row_token_head(p, t0, h0, off, ti, hi);
+        const int64_t t = ti, h = hi;
+        const T *x = static_cast<const T *>(p.x) + b * p.x_sb + t * p.x_ss + h * p.x_sh;
+        load_row_part<T, true>(x + part * EPL, xv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + t * D + part * EPL, cv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + t * D + part * EPL, sv[k]);
+        yoff[k] = b * p.y_sb + (p.y_off + t) * p.y_ss + h * p.y_sh + part * EPL;
     }
-    const T *x = static_cast<const T *>(p.x) + b * p.x_sb + t * p.x_ss + h * p.x_sh;
-    float xv[EPL];
-    float ss = 0.f;
-    if (live) {
-        const u32x4 raw = ld_global_16(x + part * EPL);
-        const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) ss += xv[k][i] * xv[k][i];
+        ss = row_sum<LPR>(ss);
+        const float sc = sqrtf(ss / (float)D + p.eps);
+        const float rc = __builtin_amdgcn_rcpf(sc);
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
-            xv[i] = (float)e[i];
-            ss += xv[i] * xv[i];
+            const float nv = round_dt<T>(div_by(xv[k][i], sc, rc));
+            xv[k][i] = round_dt<T>(nv * wv[i]);  // the normed, weighted row (n * w)
+            buf[k][lr][part * EPL + i] = xv[k][i];
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) xv[i] = 0.f;
-    }
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    const float sc = sqrtf(ss / (float)D + p.eps);
-    const T *w = static_cast<const T *>(p.w);
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int d = part * EPL + i;
-        const float nv = round_dt<T>(xv[i] / sc);
-        buf[lr][d] = round_dt<T>(nv * ld_elt(w, d));
     }
     __syncthreads();
-    if (!live) return;
-    const T *cs = static_cast<const T *>(p.cos) + (int64_t)t * D;
-    const T *sn = static_cast<const T *>(p.sin) + (int64_t)t * D;
-    T out[EPL];
+    int pd[EPL];
+    float sg[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-        const int d = part * EPL + i;
-        int pd;
-        float sg;
-        rope_partner(p, d, pd, sg);
-        const float a = buf[lr][d] * ld_elt(cs, d);
-        const float r = sg * buf[lr][pd] * ld_elt(sn, d);
-        out[i] = cast_out<T>(a + r);
+        const int o = ptab[part * EPL + i];
+        pd[i] = part * EPL + i + o;
+        sg[i] = o > 0 ? -1.f : 1.f;
     }
-    T *y = static_cast<T *>(p.y) + b * p.y_sb + (int64_t)(p.y_off + t) * p.y_ss + h * p.y_sh;
-    st_global_16(y + part * EPL, *reinterpret_cast<const u32x4 *>(out));
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        if (!live[k]) continue;
+        T out[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const float a = xv[k][i] * cv[k][i];
+            const float r = sg[i] * buf[k][lr][pd[i]] * sv[k][i];
+            out[i] = cast_out<T>(a + r);
+        }
+        st_global_16(static_cast<T *>(p.y) + yoff[k], *reinterpret_cast<const u32x4 *>(out));
+    }
 }
 
-template <typename T, int D>
+template <typename T, int D, int R, bool VEC>
 __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QkPrologueParams p) {
     constexpr int EPL = 16 / sizeof(T);
     constexpr int LPR = D / EPL;
-    constexpr int RPB = 256 / LPR;
-    __shared__ float buf[RPB][D];
+    constexpr int RPP = 256 / LPR;
+    __shared__ __attribute__((aligned(16))) float buf[R][RPP][D];
     const int tid = threadIdx.x, lr = tid / LPR, part = tid % LPR;
-    const int64_t rows = (int64_t)p.B * p.T * p.H;
-    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
-    const bool live = row < rows;
-    int b = 0, t = 0, h = 0;
-    if (live) {
-        h = row % p.H;
-        t = (row / p.H) % p.T;
-        b = row / ((int64_t)p.H * p.T);
-    }
-    const T *cs = static_cast<const T *>(p.cos) + (int64_t)t * D;
-    const T *sn = static_cast<const T *>(p.sin) + (int64_t)t * D;
-    float xv[EPL], dyv[EPL];
-    float ss = 0.f;
-    if (live) {
+    const int rows = p.T * p.H;
+    const int64_t b = blockIdx.y;
+    const int r0 = (int)blockIdx.x * (R * RPP);
+    const int t0 = r0 / p.H, h0 = r0 - t0 * p.H;
+    __shared__ __attribute__((aligned(16))) signed char ptab[D];
+    fill_partner_table<D>(p, ptab);
+    float wv[EPL];
+    load_row_part<T, VEC>(static_cast<const T *>(p.w) + part * EPL, wv);
+    float xv[R][EPL], dyv[R][EPL], cv[R][EPL], sv[R][EPL];
+    int64_t dxoff[R];
+    bool live[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int off0 = k * RPP + lr;
+        live[k] = r0 + off0 < rows;
+        const int off = live[k] ? off0 : rows - 1 - r0;
+        int ti, hi;
+        row_token_head(p, t0, h0, off, ti, hi);
+        const int64_t t = ti, h = hi;
         const T *x = static_cast<const T *>(p.x) + b * p.x_sb + t * p.x_ss + h * p.x_sh;
-        const T *dy =
-            static_cast<const T *>(p.dy) + b * p.y_sb + (int64_t)(p.y_off + t) * p.y_ss + h * p.y_sh;
-        const u32x4 rx = ld_global_16(x + part * EPL), rd = ld_global_16(dy + part * EPL);
-        const T *ex = reinterpret_cast<const T *>(&rx);
-        const T *ed = reinterpret_cast<const T *>(&rd);
+        const T *dy = static_cast<const T *>(p.dy) + b * p.y_sb + (p.y_off + t) * p.y_ss + h * p.y_sh;
+        load_row_part<T, true>(x + part * EPL, xv[k]);
+        load_row_part<T, true>(dy + part * EPL, dyv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + t * D + part * EPL, cv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + t * D + part * EPL, sv[k]);
+        dxoff[k] = b * p.dx_sb + t * p.dx_ss + h * p.dx_sh + part * EPL;
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) buf[k][lr][part * EPL + i] = dyv[k][i] * sv[k][i];
+    __syncthreads();
+    int pd[EPL];
+    float sg[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const int o = ptab[part * EPL + i];
+        pd[i] = part * EPL + i + o;
+        sg[i] = o > 0 ? -1.f : 1.f;
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) ss += xv[k][i] * xv[k][i];
+        ss = row_sum<LPR>(ss);
+        const float sigma = sqrtf(ss / (float)D + p.eps);
+        const float rs = __builtin_amdgcn_rcpf(sigma);
+        float dn[EPL], nv[EPL];
+        float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
-            xv[i] = (float)ex[i];
-            dyv[i] = (float)ed[i];
-            ss += xv[i] * xv[i];
+            // rot^T takes the partner with the opposite sign of rot
+            const float gv = dyv[k][i] * cv[k][i] - sg[i] * buf[k][lr][pd[i]];
+            dn[i] = gv * wv[i];
+            nv[i] = div_by(xv[k][i], sigma, rs);
+            dot += dn[i] * nv[i];
         }
-    } else {
+        dot = row_sum<LPR>(dot);
+        if (!live[k]) continue;
+        const float mdot = dot * (1.f / (float)D);
+        T out[EPL];
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) xv[i] = dyv[i] = 0.f;
+        for (int i = 0; i < EPL; ++i) out[i] = cast_out<T>(div_by(dn[i] - nv[i] * mdot, sigma, rs));
+        st_global_16(static_cast<T *>(p.dx) + dxoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    const float sigma = sqrtf(ss / (float)D + p.eps);
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int d = part * EPL + i;
-        buf[lr][d] = live ? dyv[i] * ld_elt(sn, d) : 0.f;
-    }
-    __syncthreads();
-    const T *w = static_cast<const T *>(p.w);
-    float dn[EPL], nv[EPL];
-    float dot = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int d = part * EPL + i;
-        int pd;
-        float sg;
-        rope_partner(p, d, pd, sg);
-        // rot^T takes the partner with the opposite sign of rot
-        const float gv = live ? dyv[i] * ld_elt(cs, d) - sg * buf[lr][pd] : 0.f;
-        dn[i] = gv * ld_elt(w, d);
-        nv[i] = xv[i] / sigma;
-        dot += dn[i] * nv[i];
-    }
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
-    if (!live) return;
-    const float mdot = dot / (float)D;
-    T out[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) out[i] = cast_out<T>((dn[i] - nv[i] * mdot) / sigma);
-    T *dx = static_cast<T *>(p.dx) + b * p.dx_sb + t * p.dx_ss + h * p.dx_sh;
-    st_global_16(dx + part * EPL, *reinterpret_cast<const u32x4 *>(out));
+}
+
+constexpr int kPrologueRows = 2;  // rows per lane (passes per workgroup)
+
+template <typename T, int D, bool BWD, bool VEC>
+hipError_t launch_prologue_v(const QkPrologueParams &p, hipStream_t s) {
+    constexpr int LPR = D * sizeof(T) / 16;
+    constexpr int RPB = 256 / LPR * kPrologueRows;
+    const int64_t rows = (int64_t)p.T * p.H;
+    const dim3 grid((unsigned)((rows + RPB - 1) / RPB), (unsigned)p.B), block(256);
+    QkPrologueParams q = p;
+    q.inv_h = 1.f / (float)p.H;
+    if (BWD)
+        hipLaunchKernelGGL((qk_prologue_bwd_kernel<T, D, kPrologueRows, VEC>), grid, block, 0, s, q);
+    else
+        hipLaunchKernelGGL((qk_prologue_fwd_kernel<T, D, kPrologueRows, VEC>), grid, block, 0, s, q);
+    return hipGetLastError();
 }
 
 template <typename T, int D, bool BWD>
 hipError_t launch_prologue(const QkPrologueParams &p, hipStream_t s) {
-    constexpr int LPR = D * sizeof(T) / 16;
-    constexpr int RPB = 256 / LPR;
-    const int64_t rows = (int64_t)p.B * p.T * p.H;
-    const dim3 grid((unsigned)((rows + RPB - 1) / RPB)), block(256);
-    if (BWD)
-        hipLaunchKernelGGL((qk_prologue_bwd_kernel<T, D>), grid, block, 0, s, p);
-    else
-        hipLaunchKernelGGL((qk_prologue_fwd_kernel<T, D>), grid, block, 0, s, p);
-    return hipGetLastError();
+    const bool vec = reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && reinterpret_cast<uintptr_t>(p.cos) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(p.sin) % 16 == 0;
+    return vec ? launch_prologue_v<T, D, BWD, true>(p, s) : launch_prologue_v<T, D, BWD, false>(p, s);
 }
 
 template <bool BWD>

@@ -139,6 +139,9 @@ def test_prologue_validation():
     assert b"sum" in lib().fa_last_error()
     a.axes[2] = 55  # odd width
     assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
+    a.axes[2] = 56
+    a.tokens, a.heads = 1 << 26, 32  # tokens * heads = 2^31 rows per batch item
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
 
 
 def test_lora_validation():
