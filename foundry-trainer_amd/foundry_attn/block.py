@@ -267,7 +267,15 @@ class DoubleBlockLoRA:
             self._buf = b
         return self._buf
 
-    def forward_backward(self, x: Dict[str, torch.Tensor], dy: Dict[str, torch.Tensor], want_dx: bool = False):
+    def forward(self, x: Dict[str, torch.Tensor], keep_attention: bool = False):
+        """Block outputs y[stream] only (the detached forward of a checkpointed
+        stack).  keep_attention also returns copies of the joint attention
+        output and its LSE, (O, LSE), which forward_backward can reuse."""
+        y, att = self._run(x, None, False, None, keep_attention)
+        return (y, att) if keep_attention else y
+
+    def forward_backward(self, x: Dict[str, torch.Tensor], dy: Dict[str, torch.Tensor], want_dx: bool = False,
+                         attention=None):
         """Block outputs y[stream] and the f32 LoRA gradients
         grads[(stream, target)] = (dA, dB) for upstream gradients dy.
 
@@ -275,7 +283,12 @@ class DoubleBlockLoRA:
         autograd stops at the first layer_norm_mod, whose input tracks no
         variable); want_dx=True also forms the input gradients of a block
         inside a stack (dX through the frozen qkv projection and the first
-        layer_norm_mod), returned as grads[(stream, "x")]."""
+        layer_norm_mod), returned as grads[(stream, "x")].  attention: the
+        (O, LSE) a forward(keep_attention=True) of the same x returned; the
+        attention forward is then skipped (the backward takes P from the LSE)."""
+        return self._run(x, dy, want_dx, attention, False)
+
+    def _run(self, x, dy, want_dx, attention, keep_attention):
         B = self._buffers()
         C, S, H, D = self.C, self.S, self.H, self.D
         s = self.lora_scale
@@ -297,13 +310,17 @@ class DoubleBlockLoRA:
             qk_prologue(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, self.eps,
                         out=B["k"], seq_offset=off)
         v = qkv[:, 2 * C:].view(1, S, H, D)
-        attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=B["o"], lse=B["lse"])
+        if attention is None:
+            o_t, lse_t = attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=B["o"], lse=B["lse"])
+        else:
+            o_t, lse_t = attention
+        kept = (o_t.clone(), lse_t.clone()) if keep_attention else None
         y = {}
         # out projection, gated residuals, MLP, and the backward down to dO
         for name in STREAMS:
             w, off, n = self.w[name], self.offset[name], self.rows[name]
             sh2, sc2, g1, g2 = w.mod[3], w.mod[4], w.mod[2], w.mod[5]
-            a = B["o"][0, off:off + n].reshape(n, C)
+            a = o_t[0, off:off + n].reshape(n, C)
             out = torch.mm(a, w.w_out.t(), out=B[f"out.{name}"])
             u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s)
             x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
@@ -312,6 +329,8 @@ class DoubleBlockLoRA:
             act = gelu(pre, out=B[f"act.{name}"])
             mlp = torch.mm(act, w.w2.t(), out=B[f"mlp.{name}"])
             y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
+            if dy is None:
+                continue
             # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
             dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
             dact = torch.mm(dmlp, w.w2, out=B[f"dact.{name}"])
@@ -323,8 +342,10 @@ class DoubleBlockLoRA:
             torch.mm(dout, w.w_out, out=do_rows)
             saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
                                                     dx=do_rows)
+        if dy is None:
+            return y, kept
         dv = dqkv[:, 2 * C:].view(1, S, H, D)
-        attn_bwd(B["q"], B["k"], v, B["o"], B["do"], B["lse"], self.attn_scale, None, workspace=B["ws"],
+        attn_bwd(B["q"], B["k"], v, o_t, B["do"], lse_t, self.attn_scale, None, workspace=B["ws"],
                  out=(B["dq"], B["dk"], dv))
         grads = {}
         for name in STREAMS:
@@ -489,9 +510,20 @@ class SingleBlockLoRA:
         """[S, C] column slice (any row stride) as a (1, S, H, D) view."""
         return t.as_strided((1, self.S, self.H, self.D), (self.S * t.stride(0), t.stride(0), self.D, 1))
 
-    def forward_backward(self, x: torch.Tensor, dy: torch.Tensor, want_dx: bool = True):
+    def forward(self, x: torch.Tensor, keep_attention: bool = False):
+        """Block output y only; keep_attention also returns copies of the
+        attention output and its LSE, (O, LSE), for forward_backward."""
+        y, att = self._run(x, None, False, None, keep_attention)
+        return (y, att) if keep_attention else y
+
+    def forward_backward(self, x: torch.Tensor, dy: torch.Tensor, want_dx: bool = True, attention=None):
         """Block output y and the f32 LoRA gradients grads[target] = (dA, dB);
-        with want_dx (a block inside a stack) also grads["x"] = dL/dx."""
+        with want_dx (a block inside a stack) also grads["x"] = dL/dx.
+        attention: (O, LSE) from forward(keep_attention=True) of the same x;
+        the attention forward is then skipped."""
+        return self._run(x, dy, want_dx, attention, False)
+
+    def _run(self, x, dy, want_dx, attention, keep_attention):
         B = self._buffers()
         C, M = self.C, self.M
         s = self.lora_scale
@@ -505,18 +537,25 @@ class SingleBlockLoRA:
         qk_prologue(q_raw, w.q_norm, self.cos, self.sin, self.axes, self.eps, out=B["q"])
         qk_prologue(k_raw, w.k_norm, self.cos, self.sin, self.axes, self.eps, out=B["k"])
         o = self._heads(joined[:, :C])
-        attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=o, lse=B["lse"])
+        if attention is None:
+            _, lse = attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=o, lse=B["lse"])
+        else:
+            o.copy_(attention[0])
+            lse = attention[1]
+        kept = (o.clone(memory_format=torch.contiguous_format), lse.clone()) if keep_attention else None
         gate, up = fused[:, 3 * C:3 * C + M], fused[:, 3 * C + M:]
         swiglu(gate, up, out=joined[:, C:])
         out = torch.mm(joined, w.w_out.t(), out=B["out"])
         u_out = lora_fwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], out, s)
         y = gated_residual(x, g, out, out=B["y"])
+        if dy is None:
+            return y, kept
         # backward: y = x + g * to_out(joined)
         dout = gated_residual(None, g, dy, out=B["dout"])
         torch.mm(dout, w.w_out, out=djoined)
         grads = {"to_out": lora_bwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], u_out, dout, s, dx=djoined)}
         swiglu_bwd(djoined[:, C:], gate, up, dgate=dfused[:, 3 * C:3 * C + M], dup=dfused[:, 3 * C + M:])
-        attn_bwd(B["q"], B["k"], v, o, self._heads(djoined[:, :C]), B["lse"], self.attn_scale, None,
+        attn_bwd(B["q"], B["k"], v, o, self._heads(djoined[:, :C]), lse, self.attn_scale, None,
                  workspace=B["ws"], out=(B["dq"], B["dk"], self._heads(dfused[:, 2 * C:3 * C])))
         qk_prologue_bwd(q_raw, w.q_norm, self.cos, self.sin, self.axes, B["dq"], eps=self.eps,
                         dx=self._heads(dfused[:, :C]))
