@@ -163,6 +163,42 @@ def single_block_bench(torch, steps: int, warmup: int):
             "tflops": round(flops / wall / 1e12, 1), "step_tflop": round(flops / 1e12, 3)}
 
 
+def stack_bench(torch, steps: int, warmup: int):
+    """A checkpointed klein stack step (checkpointed_backward, lib.rs:541-638):
+    the c4 double block, cat, the single block, split; MSE seed, recompute and
+    backward stage by stage, AdamW.  Timed twice: recomputing each attention
+    forward (the reference's scheme) and reusing the saved attention output
+    and LSE."""
+    from foundry_attn import block as fb
+    from foundry_attn import checkpoint as ck
+    from foundry_attn.configs import C4
+    rows = int(round(C4.img_tokens ** 0.5))
+    dbl = fb.random_block(C4.hidden, C4.heads, C4.txt_tokens, rows, C4.img_tokens // rows, C4.mlp_ratio,
+                          C4.lora_rank, C4.lora_alpha)
+    sgl = fb.random_single_block(C4.hidden, C4.heads, C4.txt_tokens, rows, C4.img_tokens // rows,
+                                 rank=C4.lora_rank, alpha=C4.lora_alpha)
+    g = torch.Generator(device="cuda").manual_seed(20261030)
+    c = torch.randn(C4.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    dbl.set_conditioning(c)
+    sgl.set_conditioning(c)
+    stages = [ck.DoubleStage(dbl), ck.JoinStage(C4.txt_tokens), ck.SingleStage(sgl), ck.SplitStage(C4.txt_tokens)]
+    mk = lambda n: torch.randn(n, C4.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    inputs = [mk(C4.txt_tokens), mk(C4.img_tokens)]
+    seed = ck.mse_seed([mk(C4.txt_tokens), mk(C4.img_tokens)])
+    out = {"workload": "checkpointed klein stack step: c4 double block -> cat -> single block -> split, MSE "
+                       "seed, recompute + backward per stage, AdamW; 4608 tokens, dim 3072",
+           "steps": steps, "warmup": warmup}
+    for save in (False, True):
+        def step():
+            _, _, grads = ck.checkpointed_step(stages, inputs, seed, save_attention=save)
+            ck.apply_adamw(stages, grads)
+        wall, gpu = _time_steps(torch, step, steps, warmup)
+        key = "saved_attention" if save else "recompute_attention"
+        out[key] = {"steps_per_s": round(1.0 / wall, 2), "ms_per_step": round(wall * 1e3, 3),
+                    "gpu_ms_per_step": round(gpu * 1e3, 3)}
+    return out
+
+
 def cpu_baseline(cfg, budget_s: float):
     """The oracle (port of the reference's Candle CPU path) on whole heads of
     the same workload, f32 arithmetic on bf16-valued inputs, all host cores."""
@@ -318,6 +354,7 @@ def main():
     if args.block_steps > 0:
         rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
         rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.warmup // 4))
+        rec["checkpointed_stack"] = stack_bench(torch, args.block_steps, max(2, args.warmup // 4))
     if args.cpu_seconds > 0:
         rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     else:
