@@ -24,6 +24,7 @@ projection.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 from dataclasses import dataclass, field
@@ -213,7 +214,7 @@ class DoubleBlockLoRA:
 
     def __init__(self, weights: Dict[str, StreamWeights], heads: int, head_dim: int, txt_tokens: int,
                  img_rows: int, img_cols: int, axes: Sequence[int] = (16, 56, 56), theta: float = 1e4,
-                 lora_scale: float = 1.0, eps: float = 1e-6):
+                 lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True):
         self.w = weights
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
@@ -237,6 +238,7 @@ class DoubleBlockLoRA:
         self.rows = {"txt": self.T, "img": self.I}
         self.step_count = 0
         self._buf = None
+        self._side = torch.cuda.Stream(device=self.device) if overlap_streams else None
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
@@ -288,84 +290,125 @@ class DoubleBlockLoRA:
         attention forward is then skipped (the backward takes P from the LSE)."""
         return self._run(x, dy, want_dx, attention, False)
 
+    # -- txt / img overlap ----------------------------------------------
+    # Between the joint attention calls the two streams touch disjoint rows
+    # of the joint buffers, so the txt stream's ops run on a second HIP
+    # stream (default priority) beside the img stream's, joined by events.
+    def _fork(self):
+        if self._side is not None:
+            self._side.wait_stream(torch.cuda.current_stream(self.device))
+
+    def _join(self):
+        if self._side is not None:
+            torch.cuda.current_stream(self.device).wait_stream(self._side)
+
+    def _on(self, name):
+        if self._side is not None and name == "txt":
+            return torch.cuda.stream(self._side)
+        return contextlib.nullcontext()
+
+    def _qkv_phase(self, name, x, saved):
+        """layer_norm_mod -> frozen fused qkv + three adapters -> prologue."""
+        B, C, H, D, s = self._buf, self.C, self.H, self.D, self.lora_scale
+        w, off, n = self.w[name], self.offset[name], self.rows[name]
+        h, mean1, rstd1 = ln_mod_fwd(x[name], w.mod[0], w.mod[1], self.eps, out=B[f"h.{name}"], stats=True)
+        saved[(name, "ln1")] = (mean1, rstd1)
+        rows = B["qkv"][off:off + n]
+        torch.mm(h, w.w_qkv.t(), out=rows)
+        for j, t in enumerate(("q", "k", "v")):
+            saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
+        cos, sin = self.rope[name]
+        qk_prologue(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, self.eps,
+                    out=B["q"], seq_offset=off)
+        qk_prologue(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, self.eps,
+                    out=B["k"], seq_offset=off)
+
+    def _out_phase(self, name, x, dy, o_t, y, saved):
+        """Out projection, gated residuals, MLP; with dy, the backward down to dO."""
+        B, C, s = self._buf, self.C, self.lora_scale
+        w, off, n = self.w[name], self.offset[name], self.rows[name]
+        sh2, sc2, g1, g2 = w.mod[3], w.mod[4], w.mod[2], w.mod[5]
+        a = o_t[0, off:off + n].reshape(n, C)
+        out = torch.mm(a, w.w_out.t(), out=B[f"out.{name}"])
+        u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s)
+        x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
+        h2, mean2, rstd2 = ln_mod_fwd(x1, sh2, sc2, self.eps, out=B[f"h2.{name}"], stats=True)
+        pre = torch.mm(h2, w.w1.t(), out=B[f"pre.{name}"])
+        act = gelu(pre, out=B[f"act.{name}"])
+        mlp = torch.mm(act, w.w2.t(), out=B[f"mlp.{name}"])
+        y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
+        if dy is None:
+            return
+        # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
+        dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
+        dact = torch.mm(dmlp, w.w2, out=B[f"dact.{name}"])
+        gelu_bwd(dact, pre, out=dact)
+        dh2 = torch.mm(dact, w.w1, out=B[f"t2.{name}"])
+        dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
+        dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
+        do_rows = B["do"][0, off:off + n].reshape(n, C)
+        torch.mm(dout, w.w_out, out=do_rows)
+        saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
+                                                dx=do_rows)
+
+    def _qkv_bwd_phase(self, name, x, want_dx, saved, grads):
+        """Prologue backward, the three adapters' gradients, and the input gradient."""
+        B, C, H, D, s = self._buf, self.C, self.H, self.D, self.lora_scale
+        w, off, n = self.w[name], self.offset[name], self.rows[name]
+        rows, drows = B["qkv"][off:off + n], B["dqkv"][off:off + n]
+        cos, sin = self.rope[name]
+        qk_prologue_bwd(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, B["dq"],
+                        seq_offset=off, eps=self.eps, dx=drows[:, :C].view(1, n, H, D))
+        qk_prologue_bwd(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, B["dk"],
+                        seq_offset=off, eps=self.eps, dx=drows[:, C:2 * C].view(1, n, H, D))
+        h = B[f"h.{name}"]
+        dh = torch.mm(drows, w.w_qkv, out=B[f"t2.{name}"]) if want_dx else None
+        for j, t in enumerate(("q", "k", "v")):
+            grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
+                                        drows[:, j * C:(j + 1) * C], s, dx=dh)
+        grads[(name, "out")] = saved[(name, "out", "grad")]
+        if want_dx:
+            mean1, rstd1 = saved[(name, "ln1")]
+            grads[(name, "x")] = ln_mod_bwd(x[name], dh, w.mod[1], mean1, rstd1, self.eps,
+                                            dres=B[f"dx1.{name}"], out=B[f"dx.{name}"])
+
     def _run(self, x, dy, want_dx, attention, keep_attention):
         B = self._buffers()
         C, S, H, D = self.C, self.S, self.H, self.D
-        s = self.lora_scale
-        qkv, dqkv = B["qkv"], B["dqkv"]
-        saved = {}
-        # q / k / v: layer_norm_mod -> frozen fused qkv + three adapters -> prologue
+        main = torch.cuda.current_stream(self.device)
+        saved, y, grads = {}, {}, {}
+        self._fork()
         for name in STREAMS:
-            w, off, n = self.w[name], self.offset[name], self.rows[name]
-            sh1, sc1 = w.mod[0], w.mod[1]
-            h, mean1, rstd1 = ln_mod_fwd(x[name], sh1, sc1, self.eps, out=B[f"h.{name}"], stats=True)
-            saved[(name, "ln1")] = (mean1, rstd1)
-            rows = qkv[off:off + n]
-            torch.mm(h, w.w_qkv.t(), out=rows)
-            for j, t in enumerate(("q", "k", "v")):
-                saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
-            cos, sin = self.rope[name]
-            qk_prologue(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, self.eps,
-                        out=B["q"], seq_offset=off)
-            qk_prologue(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, self.eps,
-                        out=B["k"], seq_offset=off)
-        v = qkv[:, 2 * C:].view(1, S, H, D)
+            with self._on(name):
+                self._qkv_phase(name, x, saved)
+        self._join()
+        v = B["qkv"][:, 2 * C:].view(1, S, H, D)
         if attention is None:
             o_t, lse_t = attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=B["o"], lse=B["lse"])
         else:
             o_t, lse_t = attention
         kept = (o_t.clone(), lse_t.clone()) if keep_attention else None
-        y = {}
-        # out projection, gated residuals, MLP, and the backward down to dO
+        self._fork()
         for name in STREAMS:
-            w, off, n = self.w[name], self.offset[name], self.rows[name]
-            sh2, sc2, g1, g2 = w.mod[3], w.mod[4], w.mod[2], w.mod[5]
-            a = o_t[0, off:off + n].reshape(n, C)
-            out = torch.mm(a, w.w_out.t(), out=B[f"out.{name}"])
-            u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s)
-            x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
-            h2, mean2, rstd2 = ln_mod_fwd(x1, sh2, sc2, self.eps, out=B[f"h2.{name}"], stats=True)
-            pre = torch.mm(h2, w.w1.t(), out=B[f"pre.{name}"])
-            act = gelu(pre, out=B[f"act.{name}"])
-            mlp = torch.mm(act, w.w2.t(), out=B[f"mlp.{name}"])
-            y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
-            if dy is None:
-                continue
-            # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
-            dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
-            dact = torch.mm(dmlp, w.w2, out=B[f"dact.{name}"])
-            gelu_bwd(dact, pre, out=dact)
-            dh2 = torch.mm(dact, w.w1, out=B[f"t2.{name}"])
-            dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
-            dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
-            do_rows = B["do"][0, off:off + n].reshape(n, C)
-            torch.mm(dout, w.w_out, out=do_rows)
-            saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
-                                                    dx=do_rows)
+            with self._on(name):
+                self._out_phase(name, x, dy, o_t, y, saved)
+        self._join()
         if dy is None:
             return y, kept
-        dv = dqkv[:, 2 * C:].view(1, S, H, D)
+        dv = B["dqkv"][:, 2 * C:].view(1, S, H, D)
         attn_bwd(B["q"], B["k"], v, o_t, B["do"], lse_t, self.attn_scale, None, workspace=B["ws"],
                  out=(B["dq"], B["dk"], dv))
-        grads = {}
+        self._fork()
         for name in STREAMS:
-            w, off, n = self.w[name], self.offset[name], self.rows[name]
-            rows, drows = qkv[off:off + n], dqkv[off:off + n]
-            cos, sin = self.rope[name]
-            qk_prologue_bwd(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, B["dq"],
-                            seq_offset=off, eps=self.eps, dx=drows[:, :C].view(1, n, H, D))
-            qk_prologue_bwd(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, B["dk"],
-                            seq_offset=off, eps=self.eps, dx=drows[:, C:2 * C].view(1, n, H, D))
-            h = B[f"h.{name}"]
-            dh = torch.mm(drows, w.w_qkv, out=B[f"t2.{name}"]) if want_dx else None
-            for j, t in enumerate(("q", "k", "v")):
-                grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
-                                            drows[:, j * C:(j + 1) * C], s, dx=dh)
-            grads[(name, "out")] = saved[(name, "out", "grad")]
-            if want_dx:
-                mean1, rstd1 = saved[(name, "ln1")]
-                grads[(name, "x")] = ln_mod_bwd(x[name], dh, w.mod[1], mean1, rstd1, self.eps,
-                                                dres=B[f"dx1.{name}"], out=B[f"dx.{name}"])
+            with self._on(name):
+                self._qkv_bwd_phase(name, x, want_dx, saved, grads)
+        self._join()
+        if self._side is not None:
+            # tensors made on the side stream and consumed on this one
+            for key, g in grads.items():
+                if key[0] == "txt" and key[1] != "x":
+                    for t in g:
+                        t.record_stream(main)
         return y, grads
 
     def apply_adamw(self, grads, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8) -> None:
