@@ -445,6 +445,72 @@ fa_status fa_lora_bwd(const fa_lora_bwd_args *a, void *stream) {
     return ok();
 }
 
+static fa_status check_lora_part(int32_t dtype, int32_t tokens, int32_t features, int32_t rank, float scale,
+                                 const char *fname) {
+    if (dtype != FA_DTYPE_BF16) return fail(FA_ERR_UNSUPPORTED, "adapter pieces are bf16 only");
+    if (tokens < 1 || rank < 1 || rank > 32) return fail(FA_ERR_INVALID_ARG, "tokens >= 1 and rank 1..32");
+    if (features < 16 || features % 16) return fail(FA_ERR_UNSUPPORTED, "%s must be a multiple of 16", fname);
+    if (!isfinite(scale)) return fail(FA_ERR_INVALID_ARG, "scale must be finite");
+    return FA_OK;
+}
+
+static fa_status check_rank_view(const char *name, const void *p, int64_t ld, int32_t rank) {
+    if (!p || !aligned(p, 2)) return fail(FA_ERR_INVALID_ARG, "%s is NULL or misaligned", name);
+    if (ld < rank) return fail(FA_ERR_INVALID_ARG, "%s: ld %lld < rank %d", name, (long long)ld, rank);
+    return FA_OK;
+}
+
+fa_status fa_lora_down(const fa_lora_down_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_lora_part(a->dtype, a->tokens, a->in_features, a->rank, a->scale, "in_features"));
+    if (!a->x || !aligned(a->x, 16) || a->ldx < a->in_features || (a->ldx * 2) % 16)
+        return fail(FA_ERR_INVALID_ARG, "x is NULL, misaligned, or ldx < in_features");
+    if (!a->a || !aligned(a->a, 16)) return fail(FA_ERR_INVALID_ARG, "a is NULL or not 16-byte aligned");
+    FA_TRY(check_rank_view("u", a->u, a->ldu, a->rank));
+    FA_TRY(init_current());
+    const hipError_t e = fa::launch_lora_down_bf16(a->x, a->ldx, a->a, a->tokens, a->in_features, a->rank, a->scale,
+                                                   a->u, a->ldu, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lora down launch");
+    return ok();
+}
+
+fa_status fa_lora_up(const fa_lora_up_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_lora_part(a->dtype, a->tokens, a->out_features, a->rank, a->scale, "out_features"));
+    FA_TRY(check_rank_view("u", a->u, a->ldu, a->rank));
+    if (!a->b || !aligned(a->b, 2)) return fail(FA_ERR_INVALID_ARG, "b is NULL or misaligned");
+    if (!a->y || !aligned(a->y, 2) || a->ldy < a->out_features)
+        return fail(FA_ERR_INVALID_ARG, "y is NULL, misaligned, or ldy < out_features");
+    FA_TRY(init_current());
+    const hipError_t e = fa::launch_lora_up_bf16(a->u, a->ldu, a->b, a->tokens, a->out_features, a->rank, a->scale,
+                                                 a->y, a->ldy, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lora up launch");
+    return ok();
+}
+
+size_t fa_lora_grad_workspace_size(const fa_lora_grad_args *a) {
+    if (!a || a->tokens < 1 || a->features < 1) return 0;
+    return fa::lora_grad_workspace_bytes(a->tokens, a->features);
+}
+
+fa_status fa_lora_grad(const fa_lora_grad_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_lora_part(a->dtype, a->tokens, a->features, a->rank, a->scale, "features"));
+    FA_TRY(check_rank_view("u", a->u, a->ldu, a->rank));
+    if (!a->x || !aligned(a->x, 16) || a->ldx < a->features || (a->ldx * 2) % 16)
+        return fail(FA_ERR_INVALID_ARG, "x is NULL, misaligned, or ldx < features");
+    if (!a->grad || !aligned(a->grad, 4)) return fail(FA_ERR_INVALID_ARG, "grad is NULL or misaligned");
+    const size_t need = fa::lora_grad_workspace_bytes(a->tokens, a->features);
+    if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < need)
+        return fail(FA_ERR_INVALID_ARG, "workspace is NULL, not 256-byte aligned, or smaller than %zu bytes", need);
+    FA_TRY(init_current());
+    const hipError_t e = fa::launch_lora_grad_bf16(a->u, a->ldu, a->x, a->ldx, a->tokens, a->features, a->rank,
+                                                   a->scale, a->grad, a->transpose != 0, a->workspace,
+                                                   static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lora grad launch");
+    return ok();
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

@@ -103,9 +103,9 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(const float *__restric
 // at a time with all their loads issued before the MFMAs, and the 8 partial
 // tiles are summed in LDS in a fixed order (deterministic, no workspace).
 // Rows >= N and j >= R load from a clamped (valid) row and are zeroed.
-template <int NT>
+template <int NT, typename TO>
 __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restrict__ X, int64_t ldx,
-                                                            const bf16 *__restrict__ W, float *out, int64_t ldo,
+                                                            const bf16 *__restrict__ W, TO *out, int64_t ldo,
                                                             int N, int K, int R, float s) {
     __shared__ float part[8][NT][4][64];
     const int lane = threadIdx.x & 63;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
 #pragma unroll
             for (int w = 1; w < 8; ++w) v += part[w][t][e][lane];
             const int row = row0 + 4 * q + e;
-            if (row < N && col < R) out[(int64_t)row * ldo + col] = v * s;
+            if (row < N && col < R) out[(int64_t)row * ldo + col] = (TO)(v * s);
         }
     }
 }
@@ -180,7 +180,15 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
 // 64 columns (two 32x32 output tiles, k = j).  VEC (16-byte loads of U and
 // Wt rows) needs R % 8 == 0 and 16-byte aligned U and Wt.
 template <bool VEC>
-__device__ __forceinline__ bf16x8 load8_guarded_f32_as_bf16(const float *p, int j0, int R) {
+__device__ __forceinline__ bf16x8 load8_u_as_bf16(const bf16 *p, int j0, int R) {
+    if (VEC && j0 + 8 <= R) return as_bf16x8(ld_global_16(p));
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = j0 + e < R ? p[e] : (bf16)0.f;
+    return o;
+}
+template <bool VEC>
+__device__ __forceinline__ bf16x8 load8_u_as_bf16(const float *p, int j0, int R) {
     float v[8];
     if (VEC && j0 + 8 <= R) {
         const f32x4 a = __builtin_bit_cast(f32x4, ld_global_16(p));
@@ -208,8 +216,8 @@ __device__ __forceinline__ bf16x8 load8_guarded_bf16(const bf16 *p, int j0, int 
     return o;
 }
 
-template <bool VEC, bool Y16>
-__global__ __launch_bounds__(256) void lora_expand_mfma_kernel(const float *__restrict__ U, int64_t ldu,
+template <bool VEC, bool Y16, typename TU>
+__global__ __launch_bounds__(256) void lora_expand_mfma_kernel(const TU *__restrict__ U, int64_t ldu,
                                                                const bf16 *__restrict__ Wt, bf16 *Y, int64_t ldy,
                                                                int N, int C, int R, float s) {
     // per-wave 32 x 64 f32 result tile; rows padded to 68 floats (16-byte aligned)
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(256) void lora_expand_mfma_kernel(const float *__re
     if (active) {
         for (int j0 = 0; j0 < R; j0 += 16) {
             const int ja = j0 + g * 8;
-            const bf16x8 a = ja < R ? load8_guarded_f32_as_bf16<VEC>(U + (int64_t)urow * ldu + ja, ja, R)
+            const bf16x8 a = ja < R ? load8_u_as_bf16<VEC>(U + (int64_t)urow * ldu + ja, ja, R)
                                     : as_bf16x8(u32x4{0, 0, 0, 0});
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -317,13 +325,14 @@ __global__ __launch_bounds__(256) void lora_colsum_kernel(const float *__restric
 // {0..3, 8..11, 4..7, 12..15}: lane half g of the B operand then reads its 8
 // values {4g..4g+3, 8+4g..8+4g+3} — the k order of the transpose-read A
 // operand — as one 16-byte chunk.  Rows j >= R and tokens >= N are zero.
-__global__ void lora_ut_kernel(const float *__restrict__ U, int64_t ldu, bf16 *ut, int N, int R, int npad) {
+template <typename TU>
+__global__ void lora_ut_kernel(const TU *__restrict__ U, int64_t ldu, bf16 *ut, int N, int R, int npad) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= (int64_t)32 * npad) return;
     const int j = (int)(e / npad), p = (int)(e % npad);
     const int grp = p >> 4, q = p & 15;
     const int n = grp * 16 + ((q & 4) ? 8 : 0) + ((q & 8) ? 4 : 0) + (q & 3);
-    ut[e] = f32_to_bf16(j < R && n < N ? U[(int64_t)n * ldu + j] : 0.f);
+    ut[e] = j < R && n < N ? (bf16)U[(int64_t)n * ldu + j] : (bf16)0.f;
 }
 
 constexpr int kCsCols = 128;  // columns per workgroup (4 waves x 32)
@@ -416,9 +425,9 @@ hipError_t rowdot(const T *X, int64_t ldx, const T *W, float *out, int64_t ldo, 
     if constexpr (sizeof(T) == 2) {
         const dim3 grid((unsigned)((N + 15) / 16)), block(512);
         if (R <= 16)
-            hipLaunchKernelGGL(lora_rowdot16_kernel<1>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+            hipLaunchKernelGGL((lora_rowdot16_kernel<1, float>), grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
         else
-            hipLaunchKernelGGL(lora_rowdot16_kernel<2>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+            hipLaunchKernelGGL((lora_rowdot16_kernel<2, float>), grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
     } else {
         const dim3 grid((N + 127) / 128), block(256);
         hipLaunchKernelGGL(lora_rowdot_kernel<T>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
@@ -426,19 +435,25 @@ hipError_t rowdot(const T *X, int64_t ldx, const T *W, float *out, int64_t ldo, 
     return hipGetLastError();
 }
 
+// bf16 Y += s * U Wt^T, U f32 or bf16 rows of stride ldu (16-byte U loads
+// when each U row of R elements starts 16-byte aligned).
+template <typename TU>
+hipError_t expand_mfma(const TU *U, int64_t ldu, const bf16 *Wt, bf16 *Y, int64_t ldy, int N, int C, int R, float s,
+                       hipStream_t st) {
+    const dim3 grid((unsigned)((C + 255) / 256), (unsigned)((N + 31) / 32)), block(256);
+    const bool vec = R % 8 == 0 && (ldu * (int64_t)sizeof(TU)) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(U) % 16 == 0 && reinterpret_cast<uintptr_t>(Wt) % 16 == 0;
+    const bool y16 = ldy % 8 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0;
+    auto kern = vec ? (y16 ? lora_expand_mfma_kernel<true, true, TU> : lora_expand_mfma_kernel<true, false, TU>)
+                    : (y16 ? lora_expand_mfma_kernel<false, true, TU> : lora_expand_mfma_kernel<false, false, TU>);
+    hipLaunchKernelGGL(kern, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s);
+    return hipGetLastError();
+}
+
 template <typename T>
 hipError_t expand(const float *U, int64_t ldu, const T *Wt, T *Y, int64_t ldy, int N, int C,
                   int R, float s, hipStream_t st) {
-    if constexpr (sizeof(T) == 2) {
-        const dim3 grid((unsigned)((C + 255) / 256), (unsigned)((N + 31) / 32)), block(256);
-        const bool vec = R % 8 == 0 && ldu % 4 == 0 && reinterpret_cast<uintptr_t>(U) % 16 == 0 &&
-                         reinterpret_cast<uintptr_t>(Wt) % 16 == 0;
-        const bool y16 = ldy % 8 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0;
-        auto kern = vec ? (y16 ? lora_expand_mfma_kernel<true, true> : lora_expand_mfma_kernel<true, false>)
-                        : (y16 ? lora_expand_mfma_kernel<false, true> : lora_expand_mfma_kernel<false, false>);
-        hipLaunchKernelGGL(kern, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s);
-        return hipGetLastError();
-    }
+    if constexpr (sizeof(T) == 2) return expand_mfma<float>(U, ldu, Wt, Y, ldy, N, C, R, s, st);
     const int rpb = 64;
     const dim3 grid((C + 63) / 64, (N + rpb - 1) / rpb), block(256);
     hipLaunchKernelGGL(lora_expand_kernel<T>, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s,
@@ -458,12 +473,13 @@ inline int colsum_splits(int N, int C) {
 inline int colsum_npad(int N) { return (N + kCsRows - 1) / kCsRows * kCsRows; }
 
 // bf16: U (f32 [N, R]) -> ut (bf16, operand order) -> split partials -> out.
-hipError_t colsum_bf16(const float *U, int64_t ldu, const bf16 *X, int64_t ldx, float *out, int64_t os_j,
+template <typename TU>
+hipError_t colsum_bf16(const TU *U, int64_t ldu, const bf16 *X, int64_t ldx, float *out, int64_t os_j,
                        int64_t os_c, int N, int C, int R, float s, bf16 *ut, float *part, hipStream_t st) {
     const int npad = colsum_npad(N), splits = colsum_splits(N, C);
     const int stages = npad / kCsRows;
     const int chunk = (stages + splits - 1) / splits * kCsRows;
-    hipLaunchKernelGGL(lora_ut_kernel, dim3((unsigned)((32 * (int64_t)npad + 255) / 256)), dim3(256), 0, st, U,
+    hipLaunchKernelGGL(lora_ut_kernel<TU>, dim3((unsigned)((32 * (int64_t)npad + 255) / 256)), dim3(256), 0, st, U,
                        ldu, ut, N, R, npad);
     hipLaunchKernelGGL(lora_colsum_mfma_kernel, dim3((unsigned)((C + kCsCols - 1) / kCsCols), (unsigned)splits),
                        dim3(256), 0, st, X, ldx, ut, npad, part, N, C, chunk);
@@ -518,8 +534,8 @@ hipError_t lora_bwd_t(const LoraParams &p, hipStream_t st) {
     hipError_t e;
     // dB[o][j] = s * sum_n dy[n][o] u[n][j]
     if constexpr (sizeof(T) == 2)
-        e = colsum_bf16(p.u, p.r, static_cast<const bf16 *>(p.dy), p.lddy, p.db, 1, p.r, p.N, p.M, p.r, p.scale,
-                        ut, part, st);
+        e = colsum_bf16<float>(p.u, p.r, static_cast<const bf16 *>(p.dy), p.lddy, p.db, 1, p.r, p.N, p.M, p.r,
+                               p.scale, ut, part, st);
     else
         e = colsum<T>(p.u, p.r, static_cast<const T *>(p.dy), p.lddy, p.db, 1, p.r, p.N, p.M, p.r, p.scale, st);
     if (e != hipSuccess) return e;
@@ -530,8 +546,8 @@ hipError_t lora_bwd_t(const LoraParams &p, hipStream_t st) {
         return e;
     // dA[j][k] = sum_n du[n][j] x[n][k]
     if constexpr (sizeof(T) == 2)
-        e = colsum_bf16(du, p.r, static_cast<const bf16 *>(p.x), p.ldx, p.da, p.K, 1, p.N, p.K, p.r, 1.f, ut,
-                        part, st);
+        e = colsum_bf16<float>(du, p.r, static_cast<const bf16 *>(p.x), p.ldx, p.da, p.K, 1, p.N, p.K, p.r, 1.f,
+                               ut, part, st);
     else
         e = colsum<T>(du, p.r, static_cast<const T *>(p.x), p.ldx, p.da, p.K, 1, p.N, p.K, p.r, 1.f, st);
     if (e != hipSuccess) return e;
@@ -561,6 +577,39 @@ hipError_t launch_lora_fwd(const LoraParams &p, int dtype, hipStream_t s) {
 
 hipError_t launch_lora_bwd(const LoraParams &p, int dtype, hipStream_t s) {
     return dtype == 0 ? lora_bwd_t<bf16>(p, s) : lora_bwd_t<float>(p, s);
+}
+
+// ---- bf16 pieces for adapters folded into the base GEMMs -----------------
+hipError_t launch_lora_down_bf16(const void *x, int64_t ldx, const void *a, int N, int K, int R, float scale,
+                                 void *u, int64_t ldu, hipStream_t st) {
+    const dim3 grid((unsigned)((N + 15) / 16)), block(512);
+    const bf16 *X = static_cast<const bf16 *>(x), *A = static_cast<const bf16 *>(a);
+    bf16 *U = static_cast<bf16 *>(u);
+    if (R <= 16)
+        hipLaunchKernelGGL((lora_rowdot16_kernel<1, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+    else
+        hipLaunchKernelGGL((lora_rowdot16_kernel<2, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_up_bf16(const void *u, int64_t ldu, const void *b, int N, int M, int R, float scale, void *y,
+                               int64_t ldy, hipStream_t st) {
+    return expand_mfma<bf16>(static_cast<const bf16 *>(u), ldu, static_cast<const bf16 *>(b), static_cast<bf16 *>(y),
+                             ldy, N, M, R, scale, st);
+}
+
+size_t lora_grad_workspace_bytes(int N, int C) {
+    return al256((size_t)32 * colsum_npad(N) * 2) + al256((size_t)colsum_splits(N, C) * C * 32 * 4);
+}
+
+hipError_t launch_lora_grad_bf16(const void *u, int64_t ldu, const void *x, int64_t ldx, int N, int C, int R,
+                                 float scale, float *grad, bool transpose, void *work, hipStream_t st) {
+    char *ws = static_cast<char *>(work);
+    bf16 *ut = reinterpret_cast<bf16 *>(ws);
+    float *part = reinterpret_cast<float *>(ws + al256((size_t)32 * colsum_npad(N) * 2));
+    // grad [R, C] (lora_a layout): element (j, c) at j * C + c; transposed [C, R]: c * R + j
+    return colsum_bf16<bf16>(static_cast<const bf16 *>(u), ldu, static_cast<const bf16 *>(x), ldx, grad,
+                             transpose ? 1 : C, transpose ? R : 1, N, C, R, scale, ut, part, st);
 }
 
 }  // namespace fa

@@ -27,6 +27,7 @@ EXPORTED = [
     # include/foundry_block.h
     "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
     "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step",
+    "fa_lora_down", "fa_lora_up", "fa_lora_grad", "fa_lora_grad_workspace_size",
 ]
 
 
@@ -125,6 +126,31 @@ class RowsArgs(ctypes.Structure):
     ]
 
 
+class LoraDownArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("tokens", ctypes.c_int32), ("in_features", ctypes.c_int32),
+        ("rank", ctypes.c_int32), ("scale", ctypes.c_float), ("x", ctypes.c_void_p), ("ldx", ctypes.c_int64),
+        ("a", ctypes.c_void_p), ("u", ctypes.c_void_p), ("ldu", ctypes.c_int64),
+    ]
+
+
+class LoraUpArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("tokens", ctypes.c_int32), ("out_features", ctypes.c_int32),
+        ("rank", ctypes.c_int32), ("scale", ctypes.c_float), ("u", ctypes.c_void_p), ("ldu", ctypes.c_int64),
+        ("b", ctypes.c_void_p), ("y", ctypes.c_void_p), ("ldy", ctypes.c_int64),
+    ]
+
+
+class LoraGradArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("tokens", ctypes.c_int32), ("features", ctypes.c_int32),
+        ("rank", ctypes.c_int32), ("scale", ctypes.c_float), ("u", ctypes.c_void_p), ("ldu", ctypes.c_int64),
+        ("x", ctypes.c_void_p), ("ldx", ctypes.c_int64), ("grad", ctypes.c_void_p), ("transpose", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class SwigluArgs(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
@@ -182,10 +208,13 @@ def lib() -> ctypes.CDLL:
     for name, st in (("fa_ln_mod_fwd", LnModArgs), ("fa_ln_mod_bwd", LnModBwdArgs),
                      ("fa_gated_residual", RowsArgs), ("fa_gelu_fwd", RowsArgs),
                      ("fa_gelu_bwd", RowsArgs), ("fa_silu", RowsArgs), ("fa_adamw_step", AdamwArgs),
-                     ("fa_swiglu_fwd", SwigluArgs), ("fa_swiglu_bwd", SwigluBwdArgs)):
+                     ("fa_swiglu_fwd", SwigluArgs), ("fa_swiglu_bwd", SwigluBwdArgs),
+                     ("fa_lora_down", LoraDownArgs), ("fa_lora_up", LoraUpArgs), ("fa_lora_grad", LoraGradArgs)):
         fn = getattr(L, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+    L.fa_lora_grad_workspace_size.restype = ctypes.c_size_t
+    L.fa_lora_grad_workspace_size.argtypes = [ctypes.POINTER(LoraGradArgs)]
     L.fa_rope_tables_host.restype = ctypes.c_int
     L.fa_rope_tables_host.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_float, ctypes.c_int32,

@@ -35,8 +35,8 @@ import torch
 
 from . import _abi
 from ._abi import FoundryAttnError, check, lib
-from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_fwd, qk_prologue,
-                  qk_prologue_bwd, rope_tables)
+from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_down, lora_fwd, lora_grad,
+                  lora_up, qk_prologue, qk_prologue_bwd, rope_tables)
 
 
 # ---------------------------------------------------------------------------
@@ -462,6 +462,7 @@ def random_block(dim: int, heads: int, txt_tokens: int, img_rows: int, img_cols:
 # single-stream block (the real klein layout)
 # ---------------------------------------------------------------------------
 SINGLE_LORA_TARGETS = ("to_in", "to_out")
+ADAPTER_PAD = 64  # extra GEMM columns that carry a folded adapter (rank <= 64, K stays a multiple of 64)
 
 
 @dataclass
@@ -509,7 +510,7 @@ class SingleBlockLoRA:
 
     def __init__(self, weights: SingleWeights, heads: int, head_dim: int, txt_tokens: int, img_rows: int,
                  img_cols: int, axes: Sequence[int] = (32, 32, 32, 32), theta: float = 2000.0,
-                 lora_scale: float = 1.0, eps: float = 1e-6):
+                 lora_scale: float = 1.0, eps: float = 1e-6, fuse_adapters: bool = True):
         self.w = weights
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
@@ -527,6 +528,26 @@ class SingleBlockLoRA:
                                          dtype=self.dtype, device=self.device)
         self.step_count = 0
         self._buf = None
+        self.r = weights.lora_a["to_in"].shape[0]
+        # bf16: the adapters ride in the frozen GEMMs (ADAPTER_PAD extra K or N
+        # columns: r of them the adapter's, the rest zero)
+        self.fused = fuse_adapters and self.dtype == torch.bfloat16 and self.r <= ADAPTER_PAD
+        if self.fused:
+            C, M, P = self.C, self.M, ADAPTER_PAD
+            kw = dict(dtype=self.dtype, device=self.device)
+            self.w_in_ext = torch.zeros((3 * C + 2 * M, C + P), **kw)   # [W_in | B_in | 0]
+            self.w_in_ext[:, :C] = weights.w_in
+            self.w_out_ext = torch.zeros((C + P, C + M), **kw)          # [W_out; A_out; 0]
+            self.w_out_ext[:C] = weights.w_out
+            self._refresh_adapters()
+
+    def _refresh_adapters(self) -> None:
+        """Copy the trainable factors into the GEMM operands (after AdamW)."""
+        C, r, w = self.C, self.r, self.w
+        self.w_in_ext[:, C:C + r].copy_(w.lora_b["to_in"])
+        self.w_out_ext[C:C + r].copy_(w.lora_a["to_out"])
+        self.a_in_t = w.lora_a["to_in"].t().contiguous()     # [C, r]: the dx term's "B"
+        self.b_out_t = w.lora_b["to_out"].t().contiguous()   # [r, C]: du_out = s dout B_out
 
     def set_conditioning(self, c: torch.Tensor) -> None:
         """Modulation parts chunk3(silu(c) W_mod^T) (the Mod3 of throughput.rs:284-288)."""
@@ -547,6 +568,11 @@ class SingleBlockLoRA:
                 "dq": torch.empty((1, S, H, D), **kw), "dk": torch.empty((1, S, H, D), **kw),
                 "lse": torch.empty((1, H, S), dtype=torch.float32, device=self.device),
                 "ws": torch.empty(2 * ((H * S * 4 + 255) // 256) * 256, dtype=torch.uint8, device=self.device)}
+            if self.fused:
+                P = ADAPTER_PAD
+                for key in ("nh_ext", "out_ext", "dout_ext", "dnh_ext"):  # padding columns stay zero
+                    self._buf[key] = torch.zeros((S, C + P), **kw)
+                self._buf["t_in"] = torch.zeros((S, self.r), **kw)
         return self._buf
 
     def _heads(self, t: torch.Tensor) -> torch.Tensor:
@@ -573,9 +599,18 @@ class SingleBlockLoRA:
         w = self.w
         sh, sc, g = w.mod
         fused, dfused, joined, djoined = B["fused"], B["dfused"], B["joined"], B["djoined"]
-        nh, mean, rstd = ln_mod_fwd(x, sh, sc, self.eps, out=B["nh"], stats=True)
-        torch.mm(nh, w.w_in.t(), out=fused)
-        u_in = lora_fwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], fused, s)
+        F = self.fused
+        r = self.r
+        if F:
+            # [nh | s u_in | 0] [W_in | B_in | 0]^T = nh W_in^T + s u_in B_in^T
+            nh_ext = B["nh_ext"]
+            nh, mean, rstd = ln_mod_fwd(x, sh, sc, self.eps, out=nh_ext[:, :C], stats=True)
+            su_in = lora_down(nh, w.lora_a["to_in"], s, out=nh_ext[:, C:C + r])
+            torch.mm(nh_ext, self.w_in_ext.t(), out=fused)
+        else:
+            nh, mean, rstd = ln_mod_fwd(x, sh, sc, self.eps, out=B["nh"], stats=True)
+            torch.mm(nh, w.w_in.t(), out=fused)
+            u_in = lora_fwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], fused, s)
         q_raw, k_raw, v = self._heads(fused[:, :C]), self._heads(fused[:, C:2 * C]), self._heads(fused[:, 2 * C:3 * C])
         qk_prologue(q_raw, w.q_norm, self.cos, self.sin, self.axes, self.eps, out=B["q"])
         qk_prologue(k_raw, w.k_norm, self.cos, self.sin, self.axes, self.eps, out=B["k"])
@@ -588,15 +623,32 @@ class SingleBlockLoRA:
         kept = (o.clone(memory_format=torch.contiguous_format), lse.clone()) if keep_attention else None
         gate, up = fused[:, 3 * C:3 * C + M], fused[:, 3 * C + M:]
         swiglu(gate, up, out=joined[:, C:])
-        out = torch.mm(joined, w.w_out.t(), out=B["out"])
-        u_out = lora_fwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], out, s)
+        if F:
+            # joined [W_out; A_out; 0]^T = [out | u_out | 0]; then out += s u_out B_out^T
+            out_ext = B["out_ext"]
+            torch.mm(joined, self.w_out_ext.t(), out=out_ext)
+            out, u_out = out_ext[:, :C], out_ext[:, C:C + r]
+            lora_up(u_out, w.lora_b["to_out"], out, s)
+        else:
+            out = torch.mm(joined, w.w_out.t(), out=B["out"])
+            u_out = lora_fwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], out, s)
         y = gated_residual(x, g, out, out=B["y"])
         if dy is None:
             return y, kept
         # backward: y = x + g * to_out(joined)
-        dout = gated_residual(None, g, dy, out=B["dout"])
-        torch.mm(dout, w.w_out, out=djoined)
-        grads = {"to_out": lora_bwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], u_out, dout, s, dx=djoined)}
+        if F:
+            # [dout | s dout B_out | 0] [W_out; A_out; 0] = dout W_out + du_out A_out
+            dout_ext = B["dout_ext"]
+            dout = gated_residual(None, g, dy, out=dout_ext[:, :C])
+            du_out = lora_down(dout, self.b_out_t, s, out=dout_ext[:, C:C + r])
+            torch.mm(dout_ext, self.w_out_ext, out=djoined)
+            grads = {"to_out": (lora_grad(du_out, joined, 1.0, transpose=False),
+                                lora_grad(u_out, dout, s, transpose=True))}
+        else:
+            dout = gated_residual(None, g, dy, out=B["dout"])
+            torch.mm(dout, w.w_out, out=djoined)
+            grads = {"to_out": lora_bwd(joined, w.lora_a["to_out"], w.lora_b["to_out"], u_out, dout, s,
+                                        dx=djoined)}
         swiglu_bwd(djoined[:, C:], gate, up, dgate=dfused[:, 3 * C:3 * C + M], dup=dfused[:, 3 * C + M:])
         attn_bwd(B["q"], B["k"], v, o, self._heads(djoined[:, :C]), lse, self.attn_scale, None,
                  workspace=B["ws"], out=(B["dq"], B["dk"], self._heads(dfused[:, 2 * C:3 * C])))
@@ -604,8 +656,21 @@ class SingleBlockLoRA:
                         dx=self._heads(dfused[:, :C]))
         qk_prologue_bwd(k_raw, w.k_norm, self.cos, self.sin, self.axes, B["dk"], eps=self.eps,
                         dx=self._heads(dfused[:, C:2 * C]))
-        dnh = torch.mm(dfused, w.w_in, out=B["dnh"]) if want_dx else None
-        grads["to_in"] = lora_bwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], u_in, dfused, s, dx=dnh)
+        if F:
+            if want_dx:
+                # dfused [W_in | B_in | 0] = [dfused W_in | dfused B_in | 0]
+                dnh_ext = B["dnh_ext"]
+                torch.mm(dfused, self.w_in_ext, out=dnh_ext)
+                dnh, t_in = dnh_ext[:, :C], dnh_ext[:, C:C + r]
+                lora_up(t_in, self.a_in_t, dnh, s)  # + s (dfused B_in) A_in
+            else:
+                dnh = None
+                t_in = lora_down(dfused, w.lora_b["to_in"].t().contiguous(), 1.0, out=B["t_in"])
+            grads["to_in"] = (lora_grad(t_in, nh, s, transpose=False),
+                              lora_grad(su_in, dfused, 1.0, transpose=True))
+        else:
+            dnh = torch.mm(dfused, w.w_in, out=B["dnh"]) if want_dx else None
+            grads["to_in"] = lora_bwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], u_in, dfused, s, dx=dnh)
         if want_dx:
             grads["x"] = ln_mod_bwd(x, dnh, sc, mean, rstd, self.eps, dres=dy, out=B["dx"])
         return y, grads
@@ -617,6 +682,8 @@ class SingleBlockLoRA:
             da, db = grads[t]
             adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
             adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
+        if self.fused:
+            self._refresh_adapters()
 
     def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = True):
         y, grads = self.forward_backward(x, dy, want_dx=want_dx)

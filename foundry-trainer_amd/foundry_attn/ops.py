@@ -346,3 +346,54 @@ def lora_bwd(x, a, b, u, dy, scale: float, dx: Optional[torch.Tensor] = None):
     args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     check(lib().fa_lora_bwd(ctypes.byref(args), _stream(x)))
     return da, db
+
+
+# ---------------------------------------------------------------------------
+# adapter pieces around a base GEMM that carries the adapter (bf16)
+# ---------------------------------------------------------------------------
+def _rank_view(t: torch.Tensor, N: int, r: int, name: str) -> torch.Tensor:
+    if t.shape != (N, r) or t.stride(1) != 1 or t.dtype != torch.bfloat16:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be a bf16 [{N}, {r}] view with unit column stride")
+    return t
+
+
+def lora_down(x, a, scale: float, out: torch.Tensor):
+    """out = scale * x a^T, bf16, into a [N, r] view (e.g. the extra K-columns
+    of a GEMM operand)."""
+    N, K = x.shape
+    r = a.shape[0]
+    _rank_view(out, N, r, "out")
+    args = _abi.LoraDownArgs(dtype=_dtype_code(x), tokens=N, in_features=K, rank=r, scale=float(scale),
+                             x=_ptr(x), ldx=x.stride(0), a=_ptr(a.contiguous()), u=_ptr(out), ldu=out.stride(0))
+    check(lib().fa_lora_down(ctypes.byref(args), _stream(x)))
+    return out
+
+
+def lora_up(u, b, y, scale: float):
+    """y += scale * u b^T in place; u a bf16 [N, r] view, b [M, r]."""
+    N, M = y.shape
+    r = b.shape[1]
+    _rank_view(u, N, r, "u")
+    if y.stride(1) != 1:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "y must have contiguous rows")
+    args = _abi.LoraUpArgs(dtype=_dtype_code(y), tokens=N, out_features=M, rank=r, scale=float(scale),
+                           u=_ptr(u), ldu=u.stride(0), b=_ptr(b.contiguous()), y=_ptr(y), ldy=y.stride(0))
+    check(lib().fa_lora_up(ctypes.byref(args), _stream(y)))
+    return y
+
+
+def lora_grad(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor] = None):
+    """f32 scale * u^T x: [r, C] (lora_a layout) or, with transpose, [C, r]
+    (lora_b layout).  u a bf16 [N, r] view, x [N, C]."""
+    N, C = x.shape
+    r = u.shape[1]
+    _rank_view(u, N, r, "u")
+    shape = (C, r) if transpose else (r, C)
+    g = torch.empty(shape, dtype=torch.float32, device=x.device) if out is None else out
+    args = _abi.LoraGradArgs(dtype=_dtype_code(x), tokens=N, features=C, rank=r, scale=float(scale), u=_ptr(u),
+                             ldu=u.stride(0), x=_ptr(x), ldx=x.stride(0), grad=_ptr(g), transpose=int(transpose))
+    need = lib().fa_lora_grad_workspace_size(ctypes.byref(args))
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    check(lib().fa_lora_grad(ctypes.byref(args), _stream(x)))
+    return g

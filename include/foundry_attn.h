@@ -239,6 +239,70 @@ size_t fa_lora_bwd_workspace_size(const fa_lora_bwd_args *args);
  * Deterministic. */
 fa_status fa_lora_bwd(const fa_lora_bwd_args *args, void *stream);
 
+/* ---- adapter pieces for a base GEMM that carries the adapter ------------- */
+/* The adapter term s (x A^T) B^T can ride in the frozen GEMM: appending s*u
+ * (u = x A^T) as r extra K-columns of the GEMM's left operand and B as r
+ * extra columns of its weight gives x W^T + s u B^T in one product, and
+ * appending A as r extra rows of W makes the product also output u (or, in
+ * a backward, dy B).  These three calls are the pieces around such a GEMM,
+ * bf16 only, reading and writing the rank columns as row views (u + n*ldu),
+ * ldu*2 % 16 == 0 for the 16-byte paths, rank 1..32.  They restate the
+ * adapter term of linear_scaled (lib.rs:280-285) and its autograd. */
+
+typedef struct fa_lora_down_args {
+    int32_t dtype;        /* FA_DTYPE_BF16                                     */
+    int32_t tokens;       /* N                                                 */
+    int32_t in_features;  /* K (% 16 == 0)                                     */
+    int32_t rank;         /* r                                                 */
+    float scale;
+    const void *x;        /* [N, K] rows of stride ldx, 16-byte aligned        */
+    int64_t ldx;
+    const void *a;        /* [r, K] contiguous (lora_a), 16-byte aligned       */
+    void *u;              /* [N, r] output rows of stride ldu: scale * x A^T   */
+    int64_t ldu;
+} fa_lora_down_args;
+
+/* u = scale * x A^T, rounded to bf16 (the reference's bf16 matmul result). */
+fa_status fa_lora_down(const fa_lora_down_args *args, void *stream);
+
+typedef struct fa_lora_up_args {
+    int32_t dtype;        /* FA_DTYPE_BF16                                     */
+    int32_t tokens;       /* N                                                 */
+    int32_t out_features; /* M (% 16 == 0)                                     */
+    int32_t rank;         /* r                                                 */
+    float scale;
+    const void *u;        /* [N, r] rows of stride ldu                         */
+    int64_t ldu;
+    const void *b;        /* [M, r] contiguous (lora_b layout)                 */
+    void *y;              /* [N, M] rows of stride ldy, updated in place       */
+    int64_t ldy;
+} fa_lora_up_args;
+
+/* y += scale * u B^T. */
+fa_status fa_lora_up(const fa_lora_up_args *args, void *stream);
+
+typedef struct fa_lora_grad_args {
+    int32_t dtype;        /* FA_DTYPE_BF16                                     */
+    int32_t tokens;       /* N                                                 */
+    int32_t features;     /* C (% 16 == 0)                                     */
+    int32_t rank;         /* r                                                 */
+    float scale;
+    const void *u;        /* [N, r] rows of stride ldu                         */
+    int64_t ldu;
+    const void *x;        /* [N, C] rows of stride ldx, 16-byte aligned        */
+    int64_t ldx;
+    float *grad;          /* f32 output: scale * u^T x                         */
+    int32_t transpose;    /* 0: grad is [r, C] (lora_a layout, dA = du^T x);
+                             1: grad is [C, r] (lora_b layout, dB = dy^T u)    */
+    void *workspace;      /* device scratch, 256-B aligned                     */
+    size_t workspace_bytes;
+} fa_lora_grad_args;
+
+size_t fa_lora_grad_workspace_size(const fa_lora_grad_args *args);
+
+/* grad = scale * u^T x (or its transpose), deterministic split-K reduction. */
+fa_status fa_lora_grad(const fa_lora_grad_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

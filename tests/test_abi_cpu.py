@@ -51,7 +51,8 @@ def test_struct_layouts_match_header(tmp_path):
                "fa_lora_bwd_args": _abi.LoraBwdArgs, "fa_ln_mod_args": _abi.LnModArgs,
                "fa_ln_mod_bwd_args": _abi.LnModBwdArgs, "fa_rows_args": _abi.RowsArgs,
                "fa_adamw_args": _abi.AdamwArgs, "fa_swiglu_args": _abi.SwigluArgs,
-               "fa_swiglu_bwd_args": _abi.SwigluBwdArgs}
+               "fa_swiglu_bwd_args": _abi.SwigluBwdArgs, "fa_lora_down_args": _abi.LoraDownArgs,
+               "fa_lora_up_args": _abi.LoraUpArgs, "fa_lora_grad_args": _abi.LoraGradArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{BLOCK_HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -252,3 +253,30 @@ def test_swiglu_validate_before_device_work():
         bad = _abi.SwigluBwdArgs.from_buffer_copy(bw)
         setattr(bad, field, val)
         assert L.fa_swiglu_bwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+
+
+def test_lora_pieces_validate_before_device_work():
+    L = lib()
+    ok_dev = _abi.FA_OK if gpu_available() else _abi.FA_ERR_NO_DEVICE
+    dn = _abi.LoraDownArgs(dtype=0, tokens=64, in_features=3072, rank=16, scale=1.0, x=_FAKE, ldx=3136, a=_FAKE,
+                           u=_FAKE + 6144, ldu=3136)
+    if not gpu_available():
+        assert L.fa_lora_down(ctypes.byref(dn), None) == ok_dev
+    for field, val, code in (("dtype", 1, _abi.FA_ERR_UNSUPPORTED), ("rank", 33, _abi.FA_ERR_INVALID_ARG),
+                             ("in_features", 3080, _abi.FA_ERR_UNSUPPORTED), ("ldu", 8, _abi.FA_ERR_INVALID_ARG),
+                             ("x", _FAKE + 2, _abi.FA_ERR_INVALID_ARG), ("u", _FAKE + 1, _abi.FA_ERR_INVALID_ARG)):
+        bad = _abi.LoraDownArgs.from_buffer_copy(dn)
+        setattr(bad, field, val)
+        assert L.fa_lora_down(ctypes.byref(bad), None) == code, field
+    up = _abi.LoraUpArgs(dtype=0, tokens=64, out_features=3072, rank=16, scale=1.0, u=_FAKE, ldu=3136, b=_FAKE,
+                         y=_FAKE, ldy=3136)
+    if not gpu_available():
+        assert L.fa_lora_up(ctypes.byref(up), None) == ok_dev
+    bad = _abi.LoraUpArgs.from_buffer_copy(up)
+    bad.ldy = 3000
+    assert L.fa_lora_up(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    gr = _abi.LoraGradArgs(dtype=0, tokens=64, features=3072, rank=16, scale=1.0, u=_FAKE, ldu=3136, x=_FAKE,
+                           ldx=3072, grad=_FAKE, transpose=0, workspace=0, workspace_bytes=0)
+    assert L.fa_lora_grad_workspace_size(ctypes.byref(gr)) > 0
+    assert L.fa_lora_grad(ctypes.byref(gr), None) == _abi.FA_ERR_INVALID_ARG  # no workspace
+    assert b"workspace" in L.fa_last_error()

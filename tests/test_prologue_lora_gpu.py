@@ -183,3 +183,47 @@ def test_lora_bf16_ranks_ragged(r):
     want_dx = (s * (dy.astype(np.float64) @ B) @ A).astype(np.float32)
     assert rel_l2(host(dA), wA) <= 1e-2 and rel_l2(host(dB), wB) <= 1e-2
     assert rel_l2(host(dx), want_dx) <= 1e-2
+
+
+@pytest.mark.parametrize("r", [4, 16, 32])
+def test_lora_pieces_strided_views(r):
+    """fa_lora_down / fa_lora_up / fa_lora_grad on the rank-column views a
+    GEMM that carries the adapter uses: u lives in extra columns of wider
+    buffers.  Checked against f64 products of the same bf16 values, and the
+    fused product [x | s u] [W | B]^T against x W^T + s u B^T."""
+    from foundry_attn.ops import lora_down, lora_grad, lora_up
+    rng = np.random.default_rng(200 + r)
+    N, K, M, s, pad = 333, 256, 384, 0.75, 64
+    rnd = oracle.bf16_round
+    x = rnd(rng.standard_normal((N, K)).astype(np.float32))
+    A = rnd(rng.standard_normal((r, K)).astype(np.float32) / r)
+    B = rnd(0.05 * rng.standard_normal((M, r)).astype(np.float32))
+    dy = rnd(rng.standard_normal((N, M)).astype(np.float32))
+    bf = torch.bfloat16
+    xe = torch.zeros(N, K + pad, dtype=bf, device="cuda")
+    xe[:, :K] = dev(x, bf)
+    u = lora_down(xe[:, :K], dev(A, bf), s, out=xe[:, K:K + r])
+    want_u = rnd((s * (x.astype(np.float64) @ A.T.astype(np.float64))).astype(np.float32))
+    got_u = host(u)
+    assert max_abs(got_u, want_u) <= 2 ** -7 * np.abs(want_u).max() and rel_l2(got_u, want_u) <= 4e-3
+    assert float(xe[:, K + r:].abs().max()) == 0.0  # padding untouched
+    # y += s' u B^T into a strided y view
+    ye = torch.zeros(N, M + 32, dtype=bf, device="cuda")
+    y0 = rnd(rng.standard_normal((N, M)).astype(np.float32))
+    ye[:, :M] = dev(y0, bf)
+    lora_up(xe[:, K:K + r], dev(B, bf), ye[:, :M], 2.0)
+    want_y = y0 + 2.0 * (got_u.astype(np.float64) @ B.T.astype(np.float64))
+    assert rel_l2(host(ye[:, :M]), want_y) <= 1e-2 and max_abs(host(ye[:, :M]), want_y) <= 2e-2 * np.abs(want_y).max()
+    assert float(ye[:, M:].abs().max()) == 0.0
+    # grads: dA-style [r, K] and dB-style [M, r]
+    gA = lora_grad(xe[:, K:K + r], xe[:, :K], 1.5, transpose=False)
+    np.testing.assert_allclose(host(gA), 1.5 * got_u.astype(np.float64).T @ x, rtol=1e-4, atol=1e-3)
+    gB = lora_grad(xe[:, K:K + r], dev(dy, bf), 0.5, transpose=True)
+    np.testing.assert_allclose(host(gB), 0.5 * dy.astype(np.float64).T @ got_u, rtol=1e-4, atol=1e-3)
+    # the fused product carries the adapter term
+    We = torch.zeros(M, K + pad, dtype=bf, device="cuda")
+    We[:, :K] = dev(rnd(0.02 * rng.standard_normal((M, K)).astype(np.float32)), bf)
+    We[:, K:K + r] = dev(B, bf)
+    fused = host(torch.mm(xe, We.t()))
+    ref = host(torch.mm(xe[:, :K], We[:, :K].t()).float() + torch.mm(xe[:, K:K + r].float(), We[:, K:K + r].t().float()))
+    assert rel_l2(fused, ref) <= 1e-2
