@@ -260,3 +260,70 @@ def test_backward_phases_match_single_call():
     torch.cuda.synchronize()
     for a, b, c in zip(ref, seq, out):
         assert torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_one_call_backward_is_ordered_on_the_caller_stream():
+    """fa_attn_bwd runs dQ on a library side stream and joins it back: work
+    queued on the caller's stream right after the call (a copy of dq, and a
+    second call reusing the same workspace with other inputs) sees finished
+    results."""
+    torch.manual_seed(5)
+    mk = lambda: torch.randn(1, 1100, 4, 128, device="cuda").to(torch.bfloat16)
+    q1, k1, v1, do1, q2, k2, v2, do2 = (mk() for _ in range(8))
+    o1, l1 = attn_fwd(q1, k1, v1)
+    o2, l2 = attn_fwd(q2, k2, v2)
+    ref1 = attn_bwd(q1, k1, v1, o1, do1, l1)
+    ref2 = attn_bwd(q2, k2, v2, o2, do2, l2)
+    torch.cuda.synchronize()
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    out1 = tuple(torch.empty_like(q1) for _ in range(3))
+    out2 = tuple(torch.empty_like(q1) for _ in range(3))
+    s = torch.cuda.Stream()  # default priority
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        attn_bwd(q1, k1, v1, o1, do1, l1, workspace=ws, out=out1)
+        snap = out1[0].clone()
+        attn_bwd(q2, k2, v2, o2, do2, l2, workspace=ws, out=out2)
+    torch.cuda.synchronize()
+    assert torch.equal(snap, ref1[0])
+    for a, b in zip(out1, ref1):
+        assert torch.equal(a, b)
+    for a, b in zip(out2, ref2):
+        assert torch.equal(a, b)
+
+
+def test_backward_from_two_host_threads():
+    """Each host thread gets its own side stream and events: two threads
+    calling fa_attn_bwd at once give the single-threaded bits."""
+    import threading
+    torch.manual_seed(6)
+    cases = []
+    for _ in range(2):
+        q, k, v, do = (torch.randn(1, 900, 3, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
+        o, lse = attn_fwd(q, k, v)
+        cases.append((q, k, v, o, do, lse))
+    refs = [attn_bwd(*c) for c in cases]
+    torch.cuda.synchronize()
+    results, errors = {}, []
+
+    def work(i):
+        try:
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.default_stream())
+            with torch.cuda.stream(st):
+                for _ in range(3):
+                    r = attn_bwd(*cases[i])
+            st.synchronize()
+            results[i] = r
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for a, b in zip(results[i], refs[i]):
+            assert torch.equal(a, b), i
