@@ -33,7 +33,7 @@ from typing import Dict, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from . import _abi
+from . import _abi, gemm_tuning
 from ._abi import FoundryAttnError, check, lib
 from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_down, lora_fwd, lora_grad,
                   lora_up, qk_prologue, qk_prologue_bwd, rope_tables)
@@ -214,7 +214,8 @@ class DoubleBlockLoRA:
 
     def __init__(self, weights: Dict[str, StreamWeights], heads: int, head_dim: int, txt_tokens: int,
                  img_rows: int, img_cols: int, axes: Sequence[int] = (16, 56, 56), theta: float = 1e4,
-                 lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True):
+                 lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
+                 tuned_gemms: bool = True):
         self.w = weights
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
@@ -239,6 +240,8 @@ class DoubleBlockLoRA:
         self.step_count = 0
         self._buf = None
         self._side = torch.cuda.Stream(device=self.device) if overlap_streams else None
+        if tuned_gemms and self.dtype == torch.bfloat16:
+            gemm_tuning.enable()
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
@@ -510,7 +513,8 @@ class SingleBlockLoRA:
 
     def __init__(self, weights: SingleWeights, heads: int, head_dim: int, txt_tokens: int, img_rows: int,
                  img_cols: int, axes: Sequence[int] = (32, 32, 32, 32), theta: float = 2000.0,
-                 lora_scale: float = 1.0, eps: float = 1e-6, fuse_adapters: bool = True):
+                 lora_scale: float = 1.0, eps: float = 1e-6, fuse_adapters: bool = True,
+                 tuned_gemms: bool = True):
         self.w = weights
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
@@ -528,6 +532,8 @@ class SingleBlockLoRA:
                                          dtype=self.dtype, device=self.device)
         self.step_count = 0
         self._buf = None
+        if tuned_gemms and self.dtype == torch.bfloat16:
+            gemm_tuning.enable()
         self.r = weights.lora_a["to_in"].shape[0]
         # bf16: the adapters ride in the frozen GEMMs (ADAPTER_PAD extra K or N
         # columns: r of them the adapter's, the rest zero)

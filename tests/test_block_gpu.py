@@ -299,3 +299,19 @@ def test_klein_single_block_step_properties():
     for t in fb.SINGLE_LORA_TARGETS:
         for a, b in zip(g1[t], g2[t]):
             assert torch.isfinite(a).all() and float(a.abs().max()) > 0 and torch.equal(a, b), t
+
+
+def test_tuned_gemm_file_loads_and_tuned_shapes_stay_accurate():
+    """The packaged TunableOp file (solutions measured on MI355X for the block
+    GEMM shapes) loads read-only on this image, and a tuned shape (the txt
+    stream's fused qkv projection, 512 x 3072 -> 9216) still agrees with an
+    f32 product."""
+    from foundry_attn import gemm_tuning
+    assert gemm_tuning.enable(), "TunableOp refused the packaged file (library versions differ?)"
+    assert torch.cuda.tunable.is_enabled() and not torch.cuda.tunable.tuning_is_enabled()
+    g = torch.Generator(device="cuda").manual_seed(8)
+    a = torch.randn(512, 3072, device="cuda", generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(9216, 3072, device="cuda", generator=g)).to(torch.bfloat16)
+    got = torch.mm(a, w.t()).float()
+    ref = torch.mm(a.float(), w.float().t())
+    assert float((got - ref).norm() / ref.norm()) <= 1e-2
