@@ -10,7 +10,8 @@ single block's adapter-carrying K / N extensions), measured on an MI355X.
 Its Validator rows name the PyTorch, HIP, hipBLASLt and rocBLAS versions it
 was measured with.
 
-``enable()`` loads it read-only:
+``enable()`` loads it read-only, unless the process already runs TunableOp
+its own way (then it changes nothing):
 - no tuning happens at run time;
 - shapes not in the file keep the default heuristic;
 - TunableOp refuses a file whose validators do not match the running
@@ -42,6 +43,8 @@ def enable(path: str = TUNING_FILE) -> bool:
     if not torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName.startswith("gfx950"):
         return False
     t = torch.cuda.tunable
+    if t.is_enabled():  # the caller runs TunableOp its own way: leave it alone
+        return False
     t.enable(True)
     t.tuning_enable(False)
     t.record_untuned_enable(False)
