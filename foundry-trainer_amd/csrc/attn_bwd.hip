@@ -12,16 +12,18 @@
 //   dV   = P^T dO,  dK = dS^T Q,  dQ = dS K
 // Three launches, no atomics, bit-identical on repeat:
 //   1. delta:  D = rowsum(dO * O)                    (HBM-bound)
-//   2. dk/dv:  one workgroup per 128 keys (4 waves x 32 keys), looping over
-//              all queries in 64-query LDS stages.  S = Q K^T puts keys on the
+//   2. dk/dv:  one workgroup per NW*32 keys (NW = 4 or 8 waves x 32 keys),
+//              looping over all queries in 64-query LDS stages.  S = Q K^T puts keys on the
 //              accumulator's lanes, so P and dS feed the dV / dK MFMAs as A
 //              operands straight from registers.
-//   3. dq:     one workgroup per 128 queries (4 waves x 32), looping over
-//              64-key LDS stages.  S^T = K Q^T puts queries on the lanes, so
+//   3. dq:     one workgroup per NW*32 queries (NW waves x 32), looping over
+//              32-key LDS units.  S^T = K Q^T puts queries on the lanes, so
 //              dS^T feeds dQ^T = K^T dS^T as the B operand.
 // Tiles move HBM -> LDS with buffer_load ... lds (double-buffered, zero fill
 // past S); every transposed operand (dO^T, Q^T, K^T) is read from the same
-// row-major tile with ds_read_b64_tr_b16.
+// row-major tile with ds_read_b64_tr_b16.  Eight-wave workgroups share each
+// streamed tile between twice as many rows, halving the L2 -> LDS bytes per
+// FLOP; attn_waves (attn_fwd.hip) picks the shape.
 // All GEMMs run on v_mfma_f32_32x32x16_bf16 (bf16 storage) or
 // v_mfma_f32_32x32x2_f32 (f32 storage) with f32 accumulation.
 #include <math.h>
@@ -77,29 +79,31 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(AttnBwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. dK / dV (bf16): a workgroup owns 128 keys (4 waves x 32); it streams the
+// 2. dK / dV (bf16): a workgroup owns NW*32 keys (NW waves x 32); it streams the
 //    queries in 64-row stages (Q, dO, lse2, delta) straight into LDS,
 //    double-buffered.  S = Q K^T and dP = dO V^T put the wave's keys on the
 //    accumulator lanes, so P^T and dS^T are A operands from registers; dO^T
 //    and Q^T come from the row-major tiles by transpose reads.
 // ---------------------------------------------------------------------------
-constexpr int kKT = 128;  // keys per workgroup
 constexpr int kQB = 64;   // queries per LDS stage
 
-template <int D>
+template <int D, int NW>
 struct DkvTile {
     using T = LdsTile<D, kQB>;
+    static constexpr int KT = NW * 32;  // keys per workgroup
     static constexpr int Q_OFF = 0;
     static constexpr int DO_OFF = T::BYTES;
     static constexpr int LSE_OFF = 2 * T::BYTES;        // 64 f32
     static constexpr int DELTA_OFF = LSE_OFF + kQB * 4;  // 64 f32
     static constexpr int STAGE = DELTA_OFF + kQB * 4;
-    static constexpr int WI = T::WAVE_INSTS / 4;
+    static constexpr int WI = T::WAVE_INSTS / NW;
+    static_assert(WI >= 1 && WI * NW == T::WAVE_INSTS, "tile split over waves");
 };
 
-template <int D>
+template <int D, int NW>
 __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
-    using F = DkvTile<D>;
+    using F = DkvTile<D, NW>;
+    constexpr int kKT = F::KT;
     using T = typename F::T;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -132,7 +136,7 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
     const __amdgpu_buffer_rsrc_t drs = make_rsrc(p.delta + row0, (uint32_t)(S * 4));
     const uint32_t qvo = tile_src_off<D>(wave, lane, p.q_ss);
     const uint32_t ovo = tile_src_off<D>(wave, lane, p.do_ss);
-    const uint32_t qi_step = tile_inst_row_step<D>(p.q_ss), oi_step = tile_inst_row_step<D>(p.do_ss);
+    const uint32_t qi_step = tile_inst_row_step<D, NW>(p.q_ss), oi_step = tile_inst_row_step<D, NW>(p.do_ss);
     const uint32_t qstep = (uint32_t)(kQB * p.q_ss * 2), ostep = (uint32_t)(kQB * p.do_ss * 2);
     // one LDS object per stage: the compiler then keeps the prefetch DMA in
     // flight across the transpose reads of the other stage
@@ -141,10 +145,10 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
         char *st = buf ? stage1 : stage0;
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(qrs, st + F::Q_OFF + (i * 4 + wave) * 1024, qvo, qb * qstep + i * qi_step);
+            buffer_to_lds_16(qrs, st + F::Q_OFF + (i * NW + wave) * 1024, qvo, qb * qstep + i * qi_step);
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(ors, st + F::DO_OFF + (i * 4 + wave) * 1024, ovo, qb * ostep + i * oi_step);
+            buffer_to_lds_16(ors, st + F::DO_OFF + (i * NW + wave) * 1024, ovo, qb * ostep + i * oi_step);
         if (wave == 0)
             buffer_to_lds_4(lrs, st + F::LSE_OFF, lane * 4, qb * kQB * 4);
         else if (wave == 1)
@@ -224,7 +228,7 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
         if (qb + 1 < nqb) stage(std::integral_constant<int, 1>{}, qb + 1);
     }
 
-    // accumulators: element r of lane = (key kt*128 + wave*32 + acc_row(r), d = dt*32 + n).
+    // accumulators: element r of lane = (key kt*KT + wave*32 + acc_row(r), d = dt*32 + n).
     // A lane's P / dS values feed only its own key's rows of dV / dK (the A
     // operand row), so an excluded key is handled here: its rows are zero
     // (selected, not multiplied: its unmasked P may have overflowed).
@@ -245,7 +249,7 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. dQ (bf16): a workgroup owns 128 queries (4 waves x 32) and streams K/V in
+// 3. dQ (bf16): a workgroup owns NW*32 queries (NW waves x 32) and streams K/V in
 //    32-key units straight into LDS, four buffers deep.  S^T = K Q^T and
 //    dP^T = V dO^T put the wave's queries on the lanes; dQ^T = K^T dS^T takes
 //    K^T from the row-major K tile by transpose reads.  Software pipeline per
@@ -253,20 +257,22 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
 //    dS^T VALU work and dQ^T MFMAs, unit u+2 is in flight and unit u+3 is
 //    issued into the buffer unit u-1 just released.
 // ---------------------------------------------------------------------------
-constexpr int kQT = 128;  // queries per workgroup
 constexpr int kKU = 32;   // keys per unit
 
-template <int D>
+template <int D, int NW>
 struct DqTile {
     using T = LdsTile<D, kKU>;
-    static constexpr int WI = T::WAVE_INSTS / 4;  // wave-instructions per wave per tile
+    static constexpr int QT = NW * 32;              // queries per workgroup
+    static constexpr int WI = T::WAVE_INSTS / NW;  // wave-instructions per wave per tile
+    static_assert(WI >= 1 && WI * NW == T::WAVE_INSTS, "tile split over waves");
 };
 
 // KEEP: a key mask is given (p.keep != nullptr).  The unmasked instance has
 // no per-unit loads besides the tile DMA.
-template <int D, bool KEEP>
+template <int D, bool KEEP, int NW>
 __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
-    using F = DqTile<D>;
+    using F = DqTile<D, NW>;
+    constexpr int kQT = F::QT;
     using T = typename F::T;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -294,15 +300,15 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(((S - 1) * p.v_ss + D) * 2));
     const uint32_t kvo = tile_src_off<D>(wave, lane, p.k_ss);
     const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
-    const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
+    const uint32_t ki_step = tile_inst_row_step<D, NW>(p.k_ss), vi_step = tile_inst_row_step<D, NW>(p.v_ss);
     const uint32_t kstep = (uint32_t)(kKU * p.k_ss * 2), vstep = (uint32_t)(kKU * p.v_ss * 2);
     auto issue = [&](int u, char *kd, char *vd) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(krs, kd + (i * 4 + wave) * 1024, kvo, u * kstep + i * ki_step);
+            buffer_to_lds_16(krs, kd + (i * NW + wave) * 1024, kvo, u * kstep + i * ki_step);
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(vrs, vd + (i * 4 + wave) * 1024, vvo, u * vstep + i * vi_step);
+            buffer_to_lds_16(vrs, vd + (i * NW + wave) * 1024, vvo, u * vstep + i * vi_step);
     };
 
     // loop-invariant LDS operand offsets
@@ -442,14 +448,15 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
-    dkdv_block<D>(p, xcd_remap(blockIdx.x, gridDim.x));
+// 2 waves per SIMD (<= 256 VGPRs) for either workgroup size.
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
+    dkdv_block<D, NW>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
-template <int D, bool KEEP>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
-    dq_block<D, KEEP>(p, xcd_remap(blockIdx.x, gridDim.x));
+template <int D, bool KEEP, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
+    dq_block<D, KEEP, NW>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
 // ---------------------------------------------------------------------------
@@ -630,26 +637,39 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStr
         e = D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
         if (e != hipSuccess) return e;
     }
-    const dim3 block(256);
-    const int n_kv = p.B * p.H * ((p.S + kKT - 1) / kKT);
-    const int n_q = p.B * p.H * ((p.S + kQT - 1) / kQT);
+    // workgroup shape as for the forward (attn_waves); dQ at D = 64 streams
+    // 4 KiB units, too small to split over 8 waves.
+    const int nw = attn_waves(p.B, p.H, p.S);
+    const int nw_q = D == 128 ? nw : 4;
     if (phase == 0 || phase == 2) {
-        if (D == 128)
-            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<128>, dim3(n_kv), block, 0, s, p);
+        const dim3 grid(p.B * p.H * ((p.S + nw * 32 - 1) / (nw * 32))), block(nw * 64);
+        if (D == 128 && nw == 8)
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 8>), grid, block, 0, s, p);
+        else if (D == 128)
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 4>), grid, block, 0, s, p);
+        else if (nw == 8)
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 8>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL(attn_bwd_dkdv_bf16_kernel<64>, dim3(n_kv), block, 0, s, p);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 4>), grid, block, 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (phase == 0 || phase == 3) {
-        const dim3 grid(n_q);
-        if (D == 128 && p.keep)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, true>), grid, block, 0, s, p);
-        else if (D == 128)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, false>), grid, block, 0, s, p);
-        else if (p.keep)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, true>), grid, block, 0, s, p);
-        else
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, false>), grid, block, 0, s, p);
+        const dim3 grid(p.B * p.H * ((p.S + nw_q * 32 - 1) / (nw_q * 32))), block(nw_q * 64);
+        if (D == 128 && nw_q == 8) {
+            if (p.keep)
+                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, true, 8>), grid, block, 0, s, p);
+            else
+                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, false, 8>), grid, block, 0, s, p);
+        } else if (D == 128) {
+            if (p.keep)
+                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, true, 4>), grid, block, 0, s, p);
+            else
+                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, false, 4>), grid, block, 0, s, p);
+        } else if (p.keep) {
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, true, 4>), grid, block, 0, s, p);
+        } else {
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, false, 4>), grid, block, 0, s, p);
+        }
         e = hipGetLastError();
     }
     return e;

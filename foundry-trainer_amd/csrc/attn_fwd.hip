@@ -7,7 +7,9 @@
 // reference materialises never exists; the natural-log row logsumexp is
 // written for the backward.
 //
-// bf16 kernel layout (one workgroup = 4 waves = 128 queries of one (b, h)):
+// bf16 kernel layout (one workgroup = NW = 8 waves = 256 queries of one
+// (b, h), or 4 waves = 128 queries for short sequences; all waves share each
+// K/V tile, so 8 waves halve the L2 -> LDS bytes per FLOP):
 //   - Each wave owns 32 queries.  It computes S^T = K Q^T for a 64-key block
 //     on v_mfma_f32_32x32x16_bf16: K (A operand) is read from LDS, Q (B
 //     operand) stays in registers for the whole kernel.  In the S^T
@@ -20,8 +22,11 @@
 //     register staging), double-buffered: the next block's loads are in
 //     flight while the current block computes (one barrier per block).  V^T
 //     operands come from the row-major V tile through ds_read_b64_tr_b16.
-//   - The running max is rescaled lazily (only when it grows by > 2^8), so
-//     the O rescale leaves the inner loop.
+//   - The exp2 reference (a past row max) moves only when a block's P could
+//     grow large (its row sum exceeds 2^12), so the common block runs no
+//     max reduction and no O rescale.
+//   - Each 64-key block interleaves three independent streams: the next
+//     block's scores, this block's P, and O += P V of the previous block.
 //   - Workgroups are remapped so the 8 XCDs each take contiguous runs of
 //     (b, h) query tiles and share K/V in their own L2.
 #include <math.h>
@@ -35,20 +40,25 @@
 namespace fa {
 namespace {
 
-constexpr int kBM = 128;  // queries per workgroup (4 waves x 32)
+// A workgroup is NW waves x 32 queries (NW = 4 or 8) sharing each K/V tile:
+// 8 waves halve the K/V bytes streamed into LDS per FLOP.
 constexpr int kBN = 64;   // keys per block
-constexpr int kThreads = 256;
-// Lazy rescaling: the running max used as the exp2 reference only moves when
-// a row's max grows by more than 2^8 in the exp2 domain, so P <= 256 and the
-// O / l rescale (64 + 1 multiplies per lane) runs in a handful of blocks.
-constexpr float kRescaleLog2 = 8.f;
+// Lazy rescaling: P = exp2(s*c - m_sc) against a reference m_sc that is a
+// past row max.  A block whose per-lane P sum (32 values) stays <= 2^12 has
+// every P <= 2^12, far from bf16/f32 overflow, and is used as is; otherwise
+// (or while a row has seen no kept key) the wave moves the reference to the
+// block's row max, rescales O and l, and recomputes that block's P.  The
+// common block runs no max reduction at all.
+constexpr float kRescaleSum = 4096.f;
 
-// LDS: K0, K1, V0, V1, each a row-major 64-row tile.  K runs one block
-// ahead of V: iteration j reads K_{j+1} (for the next scores) and V_j.
-template <int D>
+// LDS: K0, K1, V0, V1, each a row-major 64-row tile.  Iteration j reads
+// K_{j+1} (for the next scores) and V_{j-1} (for the previous block's P V).
+template <int D, int NW>
 struct FwdTile {
     using T = LdsTile<D, kBN>;
-    static constexpr int WI = T::WAVE_INSTS / 4;  // wave-instructions per wave per tile
+    static constexpr int BM = NW * 32;              // queries per workgroup
+    static constexpr int WI = T::WAVE_INSTS / NW;  // wave-instructions per wave per tile
+    static_assert(WI >= 1 && WI * NW == T::WAVE_INSTS, "tile split over waves");
 };
 
 // Per-lane state of one query tile after a range of key blocks: the O^T
@@ -61,9 +71,10 @@ struct FwdState {
 };
 
 // Key blocks [kb0, kb1) of query tile t (t = (b*H + h)*nq + qt).
-template <int D>
+template <int D, int NW>
 __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0, int kb1, FwdState<D> &st) {
-    using F = FwdTile<D>;
+    using F = FwdTile<D, NW>;
+    constexpr int kBM = F::BM;
     using T = typename F::T;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -84,7 +95,7 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, (uint32_t)(((S - 1) * p.v_ss + D) * 2));
     const uint32_t kvo = tile_src_off<D>(wave, lane, p.k_ss);
     const uint32_t vvo = tile_src_off<D>(wave, lane, p.v_ss);
-    const uint32_t ki_step = tile_inst_row_step<D>(p.k_ss), vi_step = tile_inst_row_step<D>(p.v_ss);
+    const uint32_t ki_step = tile_inst_row_step<D, NW>(p.k_ss), vi_step = tile_inst_row_step<D, NW>(p.v_ss);
     const uint32_t kstep = (uint32_t)(kBN * p.k_ss * 2), vstep = (uint32_t)(kBN * p.v_ss * 2);
     // The four stage buffers are distinct LDS objects: the compiler can then
     // tell a read of one stage from the DMA still filling another and emits no
@@ -94,12 +105,12 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
     auto issue_k = [&](int kb, char *dst) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(krs, dst + (i * 4 + wave) * 1024, kvo, kb * kstep + i * ki_step);
+            buffer_to_lds_16(krs, dst + (i * NW + wave) * 1024, kvo, kb * kstep + i * ki_step);
     };
     auto issue_v = [&](int kb, char *dst) {
 #pragma unroll
         for (int i = 0; i < F::WI; ++i)
-            buffer_to_lds_16(vrs, dst + (i * 4 + wave) * 1024, vvo, kb * vstep + i * vi_step);
+            buffer_to_lds_16(vrs, dst + (i * NW + wave) * 1024, vvo, kb * vstep + i * vi_step);
     };
 
     // loop-invariant LDS operand offsets
@@ -137,18 +148,67 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         }
     };
 
-    // One key block, software-pipelined: the scores of block kb (cur, computed
-    // one iteration earlier) go through the softmax and P V while the MFMAs of
-    // block kb+1's scores (nxt) are interleaved with that VALU work.  PAR is
-    // kb % 2, so every LDS stage offset is an immediate.
-    auto block = [&](auto par, int kb, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1) {
+    // P of block kb against the current reference m_sc: 32 scores per lane
+    // -> 16 packed bf16 words, and the lane's row sum of the bf16 P actually
+    // multiplied into O.  Slice ks (16 keys) is pw[ks].
+    auto make_p = [&](const f32x16 &c0, const f32x16 &c1, u32x4 (&pw)[4], float &lp, int ks) {
+        const f32x16 &sv = (ks >> 1) ? c1 : c0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = (ks & 1) * 8 + 2 * e;
+            const uint32_t word = pack_bf16x2(exp2_fast(sv[r] * c - m_sc), exp2_fast(sv[r + 1] * c - m_sc));
+            pw[ks][e] = word;
+            lp = __builtin_amdgcn_fdot2_f32_bf16(u32_as_bf16x2(word), ones, lp, false);
+        }
+    };
+    // Move the reference to the row max of block kb's scores (rare path):
+    // O and l, accumulated under the old reference, are rescaled to it.
+    auto move_reference = [&](const f32x16 &c0, const f32x16 &c1) {
+        float mx = fmaxf(c0[0], c1[0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(c0[r], c1[r]));
+        mx = max_xor32(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const float m_sc_new = m_new == -INFINITY ? 0.f : m_new * c;
+        const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_sc - m_sc_new);
+        m_run = m_new;
+        m_sc = m_sc_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    };
+    // O^T += V^T P^T for one 16-key slice of a block's P (V^T fragments by
+    // transpose reads of the row-major V tile).
+    auto pv_slice = [&](const char *vt, const u32x4 &w, int ks) {
+        const bf16x8 pf = as_bf16x8(w);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+            const bf16x8 a = lds_read_col_frag(vt, voff[dt] + ks * 16 * T::ROWB,
+                                               col_frag_hi8<D>(voff, dt) + ks * 16 * T::ROWB);
+            o[dt] = mfma_32x32x16(a, pf, o[dt]);
+        }
+    };
+
+    // One key block kb, a three-stage software pipeline with no dependency
+    // inside the block: the scores of block kb+1 (MFMA), P of block kb (VALU,
+    // from scores computed one block earlier) and O += P V for block kb-1
+    // (MFMA, with P kept in registers from the previous block) are
+    // interleaved slice by slice.  The reference check closes the block, so
+    // its body is one straight-line region.  K_j sits in ks[j%2] and V_j in
+    // vs[j%2] (relative to kb0); PAR = (kb - kb0) % 2 makes every LDS stage
+    // offset an immediate.  FIRST (kb == kb0) has no block kb-1.
+    auto block = [&](auto par, auto first, int kb, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1,
+                     u32x4 (&pw)[4]) {
         constexpr int P = decltype(par)::value;
+        constexpr bool FIRST = decltype(first)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // K_{kb+1}, V_kb landed; K_kb and V_{kb-1} fully consumed
+        __syncthreads();  // K_{kb+1}, V_{kb-1} landed; K_kb and V_{kb-2} fully consumed
         if (kb + 2 < kb1) issue_k(kb + 2, P ? ks1 : ks0);
-        if (kb + 1 < kb1) issue_v(kb + 1, P ? vs0 : vs1);
+        issue_v(kb, P ? vs1 : vs0);
         const char *kn = P ? ks0 : ks1;  // K_{kb+1}
-        const char *vt = P ? vs1 : vs0;  // V_kb
+        const char *vp = P ? vs0 : vs1;  // V_{kb-1}
 
         // key-keep bits of block kb (uniform over the workgroup)
         uint64_t km = ~0ull;
@@ -158,9 +218,6 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) n0[r] = n1[r] = 0.f;
-        // The last block computes scores of a stale K tile that are never
-        // used: keeping the MFMAs unconditional keeps them interleavable.
-        qk_part(kn, n0, n1, 0, 2);
         if (km != ~0ull) {
             // acc_row(r, lane) = (r/4)*8 + 4*g + r%4: one lane-dependent shift,
             // then constant bit positions
@@ -172,63 +229,54 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
                 if (!((k1 >> kk) & 1)) c1[r] = -INFINITY;
             }
         }
-
-        // online softmax, exp2 domain, lazily rescaled
-        float mx = fmaxf(c0[0], c1[0]);
+        if (FIRST) move_reference(c0, c1);
+        u32x4 prev[4];
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(c0[r], c1[r]));
-        mx = max_xor32(mx);
-        const float m_new = fmaxf(m_run, mx);
-        if (__any((m_new - m_run) * c > kRescaleLog2)) {
-            const float m_sc_new = m_new == -INFINITY ? 0.f : m_new * c;
-            const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_sc - m_sc_new);
-            m_run = m_new;
-            m_sc = m_sc_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-        }
+        for (int ks = 0; ks < 4; ++ks) prev[ks] = pw[ks];
+        float lp = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const f32x16 &sv = (ks >> 1) ? c1 : c0;
-            u32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = (ks & 1) * 8 + 2 * e;
-                const uint32_t word =
-                    pack_bf16x2(exp2_fast(sv[r] * c - m_sc), exp2_fast(sv[r + 1] * c - m_sc));
-                w[e] = word;
-                // row sum of the bf16 P actually multiplied into O
-                l_run = __builtin_amdgcn_fdot2_f32_bf16(u32_as_bf16x2(word), ones, l_run, false);
-            }
-            const bf16x8 pf = as_bf16x8(w);
-            // next block's scores, a slice per k-step
-            qk_part(kn, n0, n1, 2 + ks * (D / 16 - 2) / 4, 2 + (ks + 1) * (D / 16 - 2) / 4);
-            // O^T += V^T P^T  (V^T fragments by transpose reads of the row-major V tile)
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const bf16x8 a = lds_read_col_frag(vt, voff[dt] + ks * 16 * T::ROWB,
-                                                   col_frag_hi8<D>(voff, dt) + ks * 16 * T::ROWB);
-                o[dt] = mfma_32x32x16(a, pf, o[dt]);
-            }
+            make_p(c0, c1, pw, lp, ks);
+            // The last block computes scores of a stale K tile that are never
+            // used: keeping the MFMAs unconditional keeps them interleavable.
+            qk_part(kn, n0, n1, ks * (D / 16) / 4, (ks + 1) * (D / 16) / 4);
+            if (!FIRST) pv_slice(vp, prev[ks], ks);
         }
+        // Every P <= 2^12 when the lane's block sum is (P >= 0); a row with
+        // no kept key so far (m_run = -inf) has no reference yet.
+        if (!FIRST && __any(m_run == -INFINITY || !(lp <= kRescaleSum))) {
+            move_reference(c0, c1);
+            lp = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) make_p(c0, c1, pw, lp, ks);
+        }
+        l_run += lp;
     };
 
-    // prologue: K_kb0 -> scores of block kb0; K_kb0+1 and V_kb0 in flight
+    // prologue: K_kb0 -> scores of block kb0; K_kb0+1 in flight
     f32x16 sa0, sa1, sb0, sb1;
+    u32x4 pw[4];
     issue_k(kb0, ks0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (kb0 + 1 < kb1) issue_k(kb0 + 1, ks1);
-    issue_v(kb0, vs0);
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa0[r] = sa1[r] = 0.f;
     qk_part(ks0, sa0, sa1, 0, D / 16);
-    for (int kb = kb0; kb < kb1; kb += 2) {
-        block(std::integral_constant<int, 0>{}, kb, sa0, sa1, sb0, sb1);
-        if (kb + 1 < kb1) block(std::integral_constant<int, 1>{}, kb + 1, sb0, sb1, sa0, sa1);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    block(I0{}, std::true_type{}, kb0, sa0, sa1, sb0, sb1, pw);
+    for (int kb = kb0 + 1; kb < kb1; kb += 2) {
+        block(I1{}, std::false_type{}, kb, sb0, sb1, sa0, sa1, pw);
+        if (kb + 1 < kb1) block(I0{}, std::false_type{}, kb + 1, sa0, sa1, sb0, sb1, pw);
+    }
+    // epilogue: O += P V for the last block, V_{kb1-1} issued by that block
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    {
+        const char *vl = ((kb1 - 1 - kb0) & 1) ? vs1 : vs0;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) pv_slice(vl, pw[ks], ks);
     }
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) st.o[dt] = o[dt];
@@ -239,8 +287,9 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
 }
 
 // O = O / l and LSE = (m_sc + log2 l) * ln 2 for query tile t.
-template <int D>
+template <int D, int NW>
 __device__ __forceinline__ void fwd_store(const AttnFwdParams &p, int t, const FwdState<D> &st) {
+    constexpr int kBM = FwdTile<D, NW>::BM;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n = lane & 31, g = lane >> 5;
@@ -269,14 +318,14 @@ __device__ __forceinline__ void fwd_store(const AttnFwdParams &p, int t, const F
     }
 }
 
-// One workgroup per 128-query tile.
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
+// One workgroup per NW*32-query tile; 2 waves per SIMD (<= 256 VGPRs).
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
     const int nkb = (p.S + kBN - 1) / kBN;
     const int t = xcd_remap(blockIdx.x, gridDim.x);
     FwdState<D> st;
-    fwd_tile<D>(p, t, 0, nkb, st);
-    fwd_store<D>(p, t, st);
+    fwd_tile<D, NW>(p, t, 0, nkb, st);
+    fwd_store<D, NW>(p, t, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -379,13 +428,43 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(AttnFwdParams p) {
 
 }  // namespace
 
+// Workgroup shape, shared by the forward and backward bf16 kernels.  An
+// 8-wave workgroup fills a CU's registers alone (2 waves per SIMD), so its
+// grid runs in whole-CU rounds; 4-wave workgroups pair up per CU, and in a
+// sparse last round run alone at higher speed.  8 waves halve the streamed
+// L2 -> LDS bytes per FLOP but only pay when the 8-wave grid's last round is
+// at least half full: measured on MI355X, c2 (B1 H24 S4608: last round 69%
+// full) +3.6% and c5 (B2 S6656: 88%) +3% fwd+bwd, c3 (B4 S1536: 25%) -13%.
+int attn_waves(int B, int H, int S) {
+    if (S < 512) return 4;  // fewer than two 256-row tiles per (b, h)
+    static int cus[64];
+    int dev = 0;
+    int n = 256;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+        int c = __atomic_load_n(&cus[dev], __ATOMIC_RELAXED);
+        if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            c > 0)
+            __atomic_store_n(&cus[dev], c, __ATOMIC_RELAXED);
+        if (c > 0) n = c;
+    }
+    const int64_t wg = (int64_t)B * H * ((S + 255) / 256);
+    const int64_t last = wg % n == 0 ? n : wg % n;
+    return 2 * last >= n ? 8 : 4;
+}
+
 hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s) {
-    const int nq = (p.S + kBM - 1) / kBM;
-    const dim3 grid(p.B * p.H * nq), block(kThreads);
-    if (D == 128)
-        hipLaunchKernelGGL(attn_fwd_bf16_kernel<128>, grid, block, 0, s, p);
+    const int nw = attn_waves(p.B, p.H, p.S);
+    const int bm = nw * 32;
+    const int nq = (p.S + bm - 1) / bm;
+    const dim3 grid(p.B * p.H * nq), block(nw * 64);
+    if (D == 128 && nw == 8)
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8>), grid, block, 0, s, p);
+    else if (D == 128)
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 4>), grid, block, 0, s, p);
+    else if (nw == 8)
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL(attn_fwd_bf16_kernel<64>, grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 4>), grid, block, 0, s, p);
     return hipGetLastError();
 }
 

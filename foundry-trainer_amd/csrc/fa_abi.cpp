@@ -205,12 +205,16 @@ fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
 }  // extern "C"
 
 namespace {
-// The whole bf16 backward runs dQ beside dK/dV: the two kernels are
-// independent after the pre-pass, and together they fill the partial last
-// wave each leaves on its own (measured 2.4% off the c2 backward, results
-// bit-identical).  Per host thread and device: one side stream (default
-// priority) and two events, made on first use and kept for the thread's
-// life, so concurrent callers on other threads never share them.
+// With the 4-wave kernels (fa::attn_waves) the whole bf16 backward runs dQ beside
+// dK/dV: the two kernels are independent after the pre-pass, and two
+// 4-wave workgroups per CU let them fill the partial last wave each leaves
+// on its own (measured 2.4% off a 4-wave c2 backward, results
+// bit-identical).  The 8-wave kernels each fill a CU's registers alone, and
+// there running them side by side measured 4% slower than in order, so they
+// run in order on the caller's stream.  Per host thread and device: one side
+// stream (default priority) and two events, made on first use and kept for
+// the thread's life, so concurrent callers on other threads never share
+// them.
 struct BwdFork {
     hipStream_t side = nullptr;
     hipEvent_t pre = nullptr, done = nullptr;
@@ -242,6 +246,7 @@ hipError_t fork_for_current(BwdFork **out) {
 // waits for dQ, so everything the caller queues on s afterwards sees all
 // three results (and may reuse the workspace).
 hipError_t launch_bwd_forked(const fa::AttnBwdParams &p, int D, hipStream_t s) {
+    if (fa::attn_waves(p.B, p.H, p.S) == 8) return fa::launch_attn_bwd_bf16(p, D, FA_BWD_ALL, s);
     BwdFork *f = nullptr;
     if (fork_for_current(&f) != hipSuccess) return fa::launch_attn_bwd_bf16(p, D, FA_BWD_ALL, s);
     hipError_t e = fa::launch_attn_bwd_bf16(p, D, FA_BWD_PREPASS, s);

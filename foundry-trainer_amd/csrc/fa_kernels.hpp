@@ -45,6 +45,10 @@ hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s);
 hipError_t launch_attn_fwd_f32(const AttnFwdParams &p, int D, hipStream_t s);
 // phase: 0 all, 1 pre-pass, 2 dK/dV, 3 dQ
 hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStream_t s);
+// Waves per workgroup (4 or 8, i.e. 128- or 256-row tiles) of the bf16
+// forward, dK/dV and D = 128 dQ kernels for B x H sequences of S tokens on
+// the current device (see attn_fwd.hip).
+int attn_waves(int B, int H, int S);
 hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStream_t s);
 
 // One-time per-process kernel attribute setup (dynamic LDS limits).

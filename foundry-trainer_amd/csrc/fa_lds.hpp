@@ -124,13 +124,14 @@ __device__ __forceinline__ uint32_t tile_src_off(int inst, int lane, int64_t row
     return (uint32_t)((row * row_stride_elems + logical * 8) * 2);
 }
 
-// Wave-instruction `inst` of a tile covers rows inst*(1024/ROWB) ..; for a
-// 64-row tile the 4 instructions of one wave are 16 rows apart, where the
-// chunk swizzle repeats, so they share one per-lane offset and differ only by
-// the uniform row step (added to the scalar offset).
-template <int D>
+// Wave-instruction `inst` of a tile covers rows inst*(1024/ROWB) ..; with
+// NW waves sharing a tile, wave w issues instructions w, w+NW, ...  For a
+// D=128 tile those are 4*NW rows apart (16 or 32), a multiple of the chunk
+// swizzle's 16-row period, so they share one per-lane offset and differ only
+// by the uniform row step (added to the scalar offset).
+template <int D, int NW = 4>
 __device__ __forceinline__ uint32_t tile_inst_row_step(int64_t row_stride_elems) {
-    return (uint32_t)(4 * (1024 / (2 * D)) * row_stride_elems * 2);
+    return (uint32_t)(NW * (1024 / (2 * D)) * row_stride_elems * 2);
 }
 
 // Row-fragment addressing split into a per-lane base and an XOR key:

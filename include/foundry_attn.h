@@ -122,11 +122,12 @@ size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
 
 /* dQ, dK, dV of the forward above: P is recomputed from Q, K and the saved
  * LSE; dS = P * (dP - rowsum(dO * O)) * scale; dQ = dS K, dK = dS^T Q,
- * dV = P^T dO, f32 accumulation, deterministic (no atomics).  For bf16 the
- * dQ kernel runs on a library-owned side stream (one per host thread and
- * device, default priority) beside dK/dV, joined back to `stream` by events
- * before the call returns; everything queued on `stream` afterwards sees the
- * results.  Replaces AttnBwd::bwd (lib.rs:216-263). */
+ * dV = P^T dO, f32 accumulation, deterministic (no atomics).  For bf16 with
+ * seq < 512 the dQ kernel runs on a library-owned side stream (one per host
+ * thread and device, default priority) beside dK/dV, joined back to `stream`
+ * by events before the call returns; longer sequences run the three launches
+ * in order on `stream`.  Either way everything queued on `stream` afterwards
+ * sees the results.  Replaces AttnBwd::bwd (lib.rs:216-263). */
 fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
 
 /* The backward in its three launches, for callers that time them or run the

@@ -182,6 +182,78 @@ def test_fully_masked_batch_item(dtype):
     compare(g, q, k, v, do, 0.125, keep, dtype == torch.bfloat16, (0, 2))
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("masked", [False, True])
+def test_wide_tiles_partial_last_tile(D, masked):
+    """B=1, H=40, S=1400 runs the 8-wave (256-row) forward and dK/dV kernels
+    (and dQ at D = 128): 240 workgroups fill most of the chip, so the
+    workgroup-shape rule picks them, and 1400 = 5*256 + 120 leaves a partial
+    last tile of queries and of keys.  The backward then runs its three
+    launches in order.  Checked against the oracle on three heads."""
+    rng = np.random.default_rng(40 + D + masked)
+    B, S, H = 1, 1400, 40
+    q, k, v, do = (oracle.bf16_round(rng.standard_normal((B, S, H, D)).astype(np.float32)) for _ in range(4))
+    keep = None
+    if masked:
+        keep = (rng.random((B, S)) > 0.2).astype(np.uint8)
+        keep[:, :8] = 1
+    g = run_gpu(q, k, v, do, torch.bfloat16, D ** -0.5, keep)
+    compare(g, q, k, v, do, D ** -0.5, keep, True, (0, 2))
+    compare(g, q, k, v, do, D ** -0.5, keep, True, (39, 40))
+
+
+@pytest.mark.parametrize("shape", [(2, 2), (1, 44)], ids=["4wave", "8wave"])
+@pytest.mark.parametrize("case", ["growing", "overflow", "masked_prefix"])
+def test_softmax_reference_moves(case, shape):
+    """Scores that make the bf16 forward move its lazy exp2 reference:
+    - growing: key scales rise along the sequence, so later blocks' P would
+      exceed the stale reference by many orders of magnitude;
+    - overflow: the same with logits of magnitude ~200, so P against a stale
+      reference is inf and must be caught;
+    - masked_prefix: rows whose first key blocks are all masked have no
+      reference until a kept key appears, and every kept score is below -99
+      (P against a zero reference would underflow to 0).
+    S = 640 with B x H = 2 x 2 runs the 4-wave kernels, 1 x 44 the 8-wave
+    ones (132 workgroups), both with a partial last tile.
+    Near one-hot rows give |O| up to ~4.5, where one bf16 ulp (2^-5) exceeds
+    the 2e-2 max-abs gate: O is held to rel-L2 <= 1e-2 and, element-wise, to
+    max(2e-2, one bf16 ulp of the oracle's value).  The backward (unchanged
+    kernels fed this LSE) is held to rel-L2, as its magnitudes scale with the
+    keys.  Two heads are compared."""
+    rng = np.random.default_rng({"growing": 31, "overflow": 32, "masked_prefix": 33}[case])
+    (B, H), S, D = shape, 640, 128
+    q, k, v, do = (rng.standard_normal((B, S, H, D)).astype(np.float32) for _ in range(4))
+    scale, keep = D ** -0.5, None
+    if case in ("growing", "overflow"):
+        k *= (1.0 + np.arange(S, dtype=np.float32) / 16.0)[None, :, None, None]
+        if case == "overflow":
+            q *= 3.0
+    else:
+        q, k, scale = np.abs(q), -np.abs(k), 24.0 * D ** -0.5
+        keep = np.ones((B, S), np.uint8)
+        keep[0, :320] = 0
+        if B > 1:
+            keep[1, :130] = 0
+    q, k, v, do = (oracle.bf16_round(a) for a in (q, k, v, do))
+    g = run_gpu(q, k, v, do, torch.bfloat16, scale, keep)
+    hs = (0, 2)
+    sl = (slice(None), slice(None), slice(*hs))
+    o, lse = oracle.attn_fwd(q, k, v, scale=scale, key_keep=keep, bf16=True, heads=hs)
+    o, go = o[sl], g["o"][sl]
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(o), 2.0 ** -126))) - 7)
+    err = np.abs(go.astype(np.float64) - o)
+    print(f"  O: max_abs={err.max():.3e} max_ulps={(err / ulp).max():.2f} rel_l2={rel_l2(go, o):.3e}",
+          flush=True)
+    assert np.all(err <= np.maximum(BF16_MAX_ABS, ulp)) and rel_l2(go, o) <= BF16_REL_L2
+    gl, wl = g["lse"][:, hs[0]:hs[1]], lse[:, hs[0]:hs[1]]
+    assert max_abs(gl, wl) <= 2e-3 * max(1.0, float(np.abs(wl).max()) / 64.0)
+    dq, dk, dv = oracle.attn_bwd(q, k, v, do, scale=scale, key_keep=keep, bf16=True, heads=hs)
+    for name, got, want in (("dQ", g["dq"], dq), ("dK", g["dk"], dk), ("dV", g["dv"], dv)):
+        rl = rel_l2(got[sl], want[sl])
+        print(f"  {name}: rel_l2={rl:.3e}", flush=True)
+        assert rl <= BF16_REL_L2, (name, rl)
+
+
 def test_bitwise_repeatable():
     """The reference's determinism gate (docs/TESTING.md:19) as a kernel
     property: three runs give identical bits."""
@@ -262,13 +334,15 @@ def test_backward_phases_match_single_call():
         assert torch.equal(a, b) and torch.equal(a, c)
 
 
-def test_one_call_backward_is_ordered_on_the_caller_stream():
-    """fa_attn_bwd runs dQ on a library side stream and joins it back: work
-    queued on the caller's stream right after the call (a copy of dq, and a
-    second call reusing the same workspace with other inputs) sees finished
-    results."""
+@pytest.mark.parametrize("S,H", [(1100, 4), (1100, 44)], ids=["forked", "in_order"])
+def test_one_call_backward_is_ordered_on_the_caller_stream(S, H):
+    """fa_attn_bwd runs dQ on a library side stream and joins it back (H = 4:
+    20 workgroups, the 4-wave kernels) or runs the three phases in order
+    (H = 44: 220 workgroups, 8-wave): either way, work queued on the caller's
+    stream right after the call (a copy of dq, and a second call reusing the
+    same workspace with other inputs) sees finished results."""
     torch.manual_seed(5)
-    mk = lambda: torch.randn(1, 1100, 4, 128, device="cuda").to(torch.bfloat16)
+    mk = lambda: torch.randn(1, S, H, 128, device="cuda").to(torch.bfloat16)
     q1, k1, v1, do1, q2, k2, v2, do2 = (mk() for _ in range(8))
     o1, l1 = attn_fwd(q1, k1, v1)
     o2, l2 = attn_fwd(q2, k2, v2)
@@ -292,14 +366,16 @@ def test_one_call_backward_is_ordered_on_the_caller_stream():
         assert torch.equal(a, b)
 
 
-def test_backward_from_two_host_threads():
-    """Each host thread gets its own side stream and events: two threads
+@pytest.mark.parametrize("H", [3, 40], ids=["forked", "in_order"])
+def test_backward_from_two_host_threads(H):
+    """Each host thread gets its own side stream and events (H = 3 forks dQ;
+    H = 40, 160 workgroups of the 8-wave kernels, runs in order): two threads
     calling fa_attn_bwd at once give the single-threaded bits."""
     import threading
     torch.manual_seed(6)
     cases = []
     for _ in range(2):
-        q, k, v, do = (torch.randn(1, 900, 3, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
+        q, k, v, do = (torch.randn(1, 900, H, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
         o, lse = attn_fwd(q, k, v)
         cases.append((q, k, v, o, do, lse))
     refs = [attn_bwd(*c) for c in cases]
