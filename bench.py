@@ -38,10 +38,10 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # for that 256 MiB copy (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, KiB).  Kept in
 # profiles/attn_c2_pmc.md; None for a kernel or workload not measured.
 TRAFFIC = {
-    ("c2", "attn_fwd"): int((2.0 * 53939.1 + 28911.8) * 1024),
-    ("c2", "attn_bwd_prepass"): int((2.0 * 29408.6 + 5760.2) * 1024),
-    ("c2", "attn_bwd_dkdv"): int((2.0 * 65962.7 + 56160.0) * 1024),
-    ("c2", "attn_bwd_dq"): int((2.0 * 70812.6 + 28386.0) * 1024),
+    ("c2", "attn_fwd"): int((2.0 * 50776.0 + 28711.8) * 1024),
+    ("c2", "attn_bwd_prepass"): int((2.0 * 29408.6 + 5760.5) * 1024),
+    ("c2", "attn_bwd_dkdv"): int((2.0 * 65622.5 + 56160.0) * 1024),
+    ("c2", "attn_bwd_dq"): int((2.0 * 65026.4 + 28366.4) * 1024),
 }
 
 
