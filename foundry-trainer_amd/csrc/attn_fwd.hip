@@ -191,6 +191,12 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         }
     };
 
+    // Keep byte of this lane's key in block kb, loaded one block ahead so its
+    // latency hides behind a block of work: with one 8-wave workgroup per CU,
+    // a load right after the barrier would stall every wave of the CU at once.
+    auto keep_byte = [&](int kb) -> uint32_t { return keep ? keep[min(kb * kBN + lane, S - 1)] : 1u; };
+    uint32_t kbyte = keep_byte(kb0);
+
     // One key block kb, a three-stage software pipeline with no dependency
     // inside the block: the scores of block kb+1 (MFMA), P of block kb (VALU,
     // from scores computed one block earlier) and O += P V for block kb-1
@@ -210,12 +216,17 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         const char *kn = P ? ks0 : ks1;  // K_{kb+1}
         const char *vp = P ? vs0 : vs1;  // V_{kb-1}
 
-        // key-keep bits of block kb (uniform over the workgroup)
+        // key-keep bits of block kb (uniform over the workgroup).  The byte
+        // was loaded one block ago and has landed under the wait above; the
+        // empty asm keeps its use here (hoisted into the previous block, its
+        // wait would also drain the DMA issued after the load).
         uint64_t km = ~0ull;
         if (keep || (kb + 1) * kBN > S) {
+            if (keep) asm volatile("" : "+v"(kbyte));
             const int key = kb * kBN + lane;
-            km = __ballot(key < S && (!keep || keep[key]));
+            km = __ballot(key < S && kbyte != 0);
         }
+        if (keep && kb + 1 < kb1) kbyte = keep_byte(kb + 1);
 #pragma unroll
         for (int r = 0; r < 16; ++r) n0[r] = n1[r] = 0.f;
         if (km != ~0ull) {
