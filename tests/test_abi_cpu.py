@@ -280,3 +280,15 @@ def test_lora_pieces_validate_before_device_work():
     assert L.fa_lora_grad_workspace_size(ctypes.byref(gr)) > 0
     assert L.fa_lora_grad(ctypes.byref(gr), None) == _abi.FA_ERR_INVALID_ARG  # no workspace
     assert b"workspace" in L.fa_last_error()
+
+
+def test_public_headers_are_plain_c():
+    """include/*.h compile as C99 on their own (no C++ or HIP types cross the
+    boundary), as a Rust bindgen or cgo consumer would read them."""
+    import subprocess
+    inc = os.path.join(ROOT, "include")
+    for h in ("foundry_attn.h", "foundry_block.h"):
+        src = f'#include "{h}"\nint main(void) {{ return 0; }}\n'
+        r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-fsyntax-only",
+                            "-I", inc, "-x", "c", "-"], input=src, capture_output=True, text=True)
+        assert r.returncode == 0, (h, r.stderr)
