@@ -10,7 +10,8 @@
 //                                           lib.rs:246-247 form)
 //   dS   = P * (dP - D_i) * scale
 //   dV   = P^T dO,  dK = dS^T Q,  dQ = dS K
-// Three launches, no atomics, bit-identical on repeat:
+// Three launches (two when dQ does the pre-pass, see dq_block), no atomics,
+// bit-identical on repeat:
 //   1. delta:  D = rowsum(dO * O)                    (HBM-bound)
 //   2. dk/dv:  one workgroup per NW*32 keys (NW = 4 or 8 waves x 32 keys),
 //              looping over all queries in 64-query LDS stages.  S = Q K^T puts keys on the
@@ -269,7 +270,12 @@ struct DqTile {
 
 // KEEP: a key mask is given (p.keep != nullptr).  The unmasked instance has
 // no per-unit loads besides the tile DMA.
-template <int D, bool KEEP, int NW>
+// DELTA: the kernel also does the pre-pass for its own queries (delta =
+// rowsum(dO * O) and lse2 from LSE, written to the workspace for dK/dV, which
+// then runs after it), so the whole backward is two launches.  The row sum
+// follows the pre-pass's order exactly -- sequential sums over 8-element
+// parts, then an xor butterfly over the parts -- so both give the same bits.
+template <int D, bool KEEP, int NW, bool DELTA>
 __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     using F = DqTile<D, NW>;
     constexpr int kQT = F::QT;
@@ -327,9 +333,43 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
         of[kd] = as_bf16x8(in ? ld_global_16(dobase + qi * p.do_ss + kd * 16 + g * 8) : u32x4{0, 0, 0, 0});
     }
     float lse2 = INFINITY, dlt = 0.f;
-    if (qi < S) {
-        lse2 = p.lse2[((int64_t)b * H + h) * S + qi];
-        dlt = p.delta[((int64_t)b * H + h) * S + qi];
+    const int64_t qrow = ((int64_t)b * H + h) * S + qi;
+    if constexpr (DELTA) {
+        // part 2*kd + g = features [16 kd + 8 g, +8): this lane holds the
+        // parts of one parity, its lane ^ 32 partner the others
+        const bf16 *obase = static_cast<const bf16 *>(p.o) + b * p.o_sb + h * p.o_sh;
+        float part[D / 16];
+#pragma unroll
+        for (int kd = 0; kd < D / 16; ++kd) {
+            const bf16x8 ov =
+                as_bf16x8(qi < S ? ld_global_16(obase + qi * p.o_ss + kd * 16 + g * 8) : u32x4{0, 0, 0, 0});
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)of[kd][e];
+            part[kd] = acc;
+        }
+        // butterfly: part offsets D/16 .. 2 pair parts of one lane (kd ^ m),
+        // offset 1 pairs the lane with its partner
+#pragma unroll
+        for (int m = D / 32; m >= 1; m >>= 1) {
+            float nxt[D / 16];
+#pragma unroll
+            for (int kd = 0; kd < D / 16; ++kd) nxt[kd] = part[kd] + part[kd ^ m];
+#pragma unroll
+            for (int kd = 0; kd < D / 16; ++kd) part[kd] = nxt[kd];
+        }
+        dlt = sum_xor32(part[0]);
+        if (qi < S) {
+            const float l = p.lse[qrow];
+            lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
+            if (g == 0) {
+                p.delta[qrow] = dlt;
+                p.lse2[qrow] = lse2;
+            }
+        }
+    } else if (qi < S) {
+        lse2 = p.lse2[qrow];
+        dlt = p.delta[qrow];
     }
     f32x16 dq[D / 32];
 #pragma unroll
@@ -454,9 +494,17 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdP
     dkdv_block<D, NW>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
-template <int D, bool KEEP, int NW>
+template <int D, bool KEEP, int NW, bool DELTA>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
-    dq_block<D, KEEP, NW>(p, xcd_remap(blockIdx.x, gridDim.x));
+    dq_block<D, KEEP, NW, DELTA>(p, xcd_remap(blockIdx.x, gridDim.x));
+}
+
+template <int D, int NW, bool DELTA>
+void launch_dq(const AttnBwdParams &p, dim3 grid, dim3 block, hipStream_t s) {
+    if (p.keep)
+        hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, true, NW, DELTA>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, false, NW, DELTA>), grid, block, 0, s, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -632,15 +680,29 @@ hipError_t launch_delta(const AttnBwdParams &p, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
-    hipError_t e = hipSuccess;
-    if (phase == 0 || phase == 1) {
-        e = D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
-        if (e != hipSuccess) return e;
-    }
     // workgroup shape as for the forward (attn_waves); dQ at D = 64 streams
     // 4 KiB units, too small to split over 8 waves.
     const int nw = attn_waves(p.B, p.H, p.S);
     const int nw_q = D == 128 ? nw : 4;
+    // The whole backward with 8-wave kernels runs in order on one stream:
+    // dQ first, doing the pre-pass for its own queries, then dK/dV.
+    const bool fused = phase == 0 && nw == 8;
+    hipError_t e = hipSuccess;
+    if (!fused && (phase == 0 || phase == 1)) {
+        e = D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
+        if (e != hipSuccess) return e;
+    }
+    auto dq = [&](bool delta) {
+        const dim3 grid(p.B * p.H * ((p.S + nw_q * 32 - 1) / (nw_q * 32))), block(nw_q * 64);
+        if (D == 128 && nw_q == 8)
+            delta ? launch_dq<128, 8, true>(p, grid, block, s) : launch_dq<128, 8, false>(p, grid, block, s);
+        else if (D == 128)
+            delta ? launch_dq<128, 4, true>(p, grid, block, s) : launch_dq<128, 4, false>(p, grid, block, s);
+        else
+            delta ? launch_dq<64, 4, true>(p, grid, block, s) : launch_dq<64, 4, false>(p, grid, block, s);
+        return hipGetLastError();
+    };
+    if (fused && (e = dq(true)) != hipSuccess) return e;
     if (phase == 0 || phase == 2) {
         const dim3 grid(p.B * p.H * ((p.S + nw * 32 - 1) / (nw * 32))), block(nw * 64);
         if (D == 128 && nw == 8)
@@ -653,25 +715,7 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStr
             hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 4>), grid, block, 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if (phase == 0 || phase == 3) {
-        const dim3 grid(p.B * p.H * ((p.S + nw_q * 32 - 1) / (nw_q * 32))), block(nw_q * 64);
-        if (D == 128 && nw_q == 8) {
-            if (p.keep)
-                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, true, 8>), grid, block, 0, s, p);
-            else
-                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, false, 8>), grid, block, 0, s, p);
-        } else if (D == 128) {
-            if (p.keep)
-                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, true, 4>), grid, block, 0, s, p);
-            else
-                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, false, 4>), grid, block, 0, s, p);
-        } else if (p.keep) {
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, true, 4>), grid, block, 0, s, p);
-        } else {
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, false, 4>), grid, block, 0, s, p);
-        }
-        e = hipGetLastError();
-    }
+    if (!fused && (phase == 0 || phase == 3)) e = dq(false);
     return e;
 }
 

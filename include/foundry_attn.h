@@ -125,8 +125,8 @@ size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
  * dV = P^T dO, f32 accumulation, deterministic (no atomics).  For bf16 with
  * seq < 512 the dQ kernel runs on a library-owned side stream (one per host
  * thread and device, default priority) beside dK/dV, joined back to `stream`
- * by events before the call returns; longer sequences run the three launches
- * in order on `stream`.  Either way everything queued on `stream` afterwards
+ * by events before the call returns; longer sequences run in order on
+ * `stream` (dQ, which also forms the pre-pass for its queries, then dK/dV).  Either way everything queued on `stream` afterwards
  * sees the results.  Replaces AttnBwd::bwd (lib.rs:216-263). */
 fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
 

@@ -302,13 +302,17 @@ def test_custom_op_surface_and_autograd():
     assert torch.equal(qa.grad, dq) and torch.equal(ka.grad, dk) and torch.equal(va.grad, dv)
 
 
-def test_backward_phases_match_single_call():
+@pytest.mark.parametrize("B,S,H,D", [(2, 700, 3, 128), (1, 1100, 44, 128), (1, 1100, 44, 64)],
+                         ids=["4wave", "8wave", "8wave_d64"])
+def test_backward_phases_match_single_call(B, S, H, D):
     """fa_attn_bwd_phase: pre-pass, dK/dV and dQ issued separately (one
-    stream, then dK/dV and dQ on two streams) give the one-call bits."""
+    stream, then dK/dV and dQ on two streams) give the one-call bits.  With
+    8-wave kernels the one call is two launches (dQ doing the pre-pass for
+    its own queries, then dK/dV), whose row sums follow the pre-pass's order."""
     from foundry_attn import _abi
     torch.manual_seed(3)
-    q, k, v, do = (torch.randn(2, 700, 3, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
-    keep = torch.ones(2, 700, dtype=torch.uint8, device="cuda")
+    q, k, v, do = (torch.randn(B, S, H, D, device="cuda").to(torch.bfloat16) for _ in range(4))
+    keep = torch.ones(B, S, dtype=torch.uint8, device="cuda")
     keep[0, 100:300] = 0
     o, lse = attn_fwd(q, k, v, key_keep=keep)
     ref = attn_bwd(q, k, v, o, do, lse, key_keep=keep)
