@@ -231,9 +231,18 @@ hipError_t fork_for_current(BwdFork **out) {
     if (!f.side) {
         hipStream_t st = nullptr;
         hipEvent_t e0 = nullptr, e1 = nullptr;
+        // a partial failure releases what was made (the caller then runs the
+        // backward in order on its own stream)
         if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&e0, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&e1, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&e0, hipEventDisableTiming)) != hipSuccess) {
+            (void)hipStreamDestroy(st);
+            return e;
+        }
+        if ((e = hipEventCreateWithFlags(&e1, hipEventDisableTiming)) != hipSuccess) {
+            (void)hipEventDestroy(e0);
+            (void)hipStreamDestroy(st);
+            return e;
+        }
         f.side = st;
         f.pre = e0;
         f.done = e1;
