@@ -517,7 +517,7 @@ fa_status fa_lora_bwd(const fa_lora_bwd_args *a, void *stream) {
 static fa_status check_lora_part(int32_t dtype, int32_t tokens, int32_t features, int32_t rank, float scale,
                                  const char *fname) {
     if (dtype != FA_DTYPE_BF16) return fail(FA_ERR_UNSUPPORTED, "adapter pieces are bf16 only");
-    if (tokens < 1 || rank < 1 || rank > 32) return fail(FA_ERR_INVALID_ARG, "tokens >= 1 and rank 1..32");
+    if (tokens < 1 || rank < 1 || rank > 64) return fail(FA_ERR_INVALID_ARG, "tokens >= 1 and rank 1..64");
     if (features < 16 || features % 16) return fail(FA_ERR_UNSUPPORTED, "%s must be a multiple of 16", fname);
     if (!isfinite(scale)) return fail(FA_ERR_INVALID_ARG, "scale must be finite");
     return FA_OK;

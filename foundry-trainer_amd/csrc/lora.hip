@@ -585,10 +585,16 @@ hipError_t launch_lora_down_bf16(const void *x, int64_t ldx, const void *a, int 
     const dim3 grid((unsigned)((N + 15) / 16)), block(512);
     const bf16 *X = static_cast<const bf16 *>(x), *A = static_cast<const bf16 *>(a);
     bf16 *U = static_cast<bf16 *>(u);
+    // R <= 64: up to four 16-column tiles per workgroup (a stack of adapters
+    // that share x, e.g. q/k/v, runs as one product)
     if (R <= 16)
         hipLaunchKernelGGL((lora_rowdot16_kernel<1, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
-    else
+    else if (R <= 32)
         hipLaunchKernelGGL((lora_rowdot16_kernel<2, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+    else if (R <= 48)
+        hipLaunchKernelGGL((lora_rowdot16_kernel<3, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+    else
+        hipLaunchKernelGGL((lora_rowdot16_kernel<4, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
     return hipGetLastError();
 }
 
@@ -607,9 +613,16 @@ hipError_t launch_lora_grad_bf16(const void *u, int64_t ldu, const void *x, int6
     char *ws = static_cast<char *>(work);
     bf16 *ut = reinterpret_cast<bf16 *>(ws);
     float *part = reinterpret_cast<float *>(ws + al256((size_t)32 * colsum_npad(N) * 2));
-    // grad [R, C] (lora_a layout): element (j, c) at j * C + c; transposed [C, R]: c * R + j
-    return colsum_bf16<bf16>(static_cast<const bf16 *>(u), ldu, static_cast<const bf16 *>(x), ldx, grad,
-                             transpose ? 1 : C, transpose ? R : 1, N, C, R, scale, ut, part, st);
+    // grad [R, C] (lora_a layout): element (j, c) at j * C + c; transposed [C, R]: c * R + j.
+    // The MFMA colsum covers 32 rank columns; R <= 64 runs as two passes over
+    // the same workspace, in stream order.
+    const bf16 *U = static_cast<const bf16 *>(u);
+    const int64_t os_j = transpose ? 1 : C, os_c = transpose ? R : 1;
+    hipError_t e = colsum_bf16<bf16>(U, ldu, static_cast<const bf16 *>(x), ldx, grad, os_j, os_c, N, C,
+                                     R < 32 ? R : 32, scale, ut, part, st);
+    if (e != hipSuccess || R <= 32) return e;
+    return colsum_bf16<bf16>(U + 32, ldu, static_cast<const bf16 *>(x), ldx, grad + 32 * os_j, os_j, os_c, N, C,
+                             R - 32, scale, ut, part, st);
 }
 
 }  // namespace fa

@@ -183,6 +183,7 @@ def adamw_step(param, grad, m, v, step: int, lr: float = 1e-3, betas=(0.9, 0.999
 # the block
 # ---------------------------------------------------------------------------
 LORA_TARGETS = ("q", "k", "v", "out")
+QKV = ("q", "k", "v")
 STREAMS = ("txt", "img")  # joint order: txt first (throughput.rs:545-547)
 
 
@@ -210,12 +211,22 @@ class DoubleBlockLoRA:
     heads * head_dim = dim; img tokens lie on an (img_rows, img_cols) grid,
     txt tokens get positions (l, 0, 0), img tokens (0, r, c)
     (throughput.rs:724-748).
+
+    batch_qkv_adapters (bf16, 3r <= 64): the q, k and v adapters of a stream
+    read the same h, so their A factors are stacked into one [3r, C] tensor
+    (lora_a[t] become row views of it) and every product that contracts or
+    expands over h runs once at rank 3r -- s u = s h A^T, dh += s t A_qkv
+    and dA = s t^T h -- while the block-diagonal ones (the three up
+    projections, t_j = dy_j B_j and dB_j) stay per adapter.  Same arithmetic
+    as the adapter pieces of the single block (u and t rounded to bf16 as the
+    reference's bf16 matmuls round them); a third of the launches and one
+    pass over h and dh instead of three.
     """
 
     def __init__(self, weights: Dict[str, StreamWeights], heads: int, head_dim: int, txt_tokens: int,
                  img_rows: int, img_cols: int, axes: Sequence[int] = (16, 56, 56), theta: float = 1e4,
                  lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
-                 tuned_gemms: bool = True):
+                 tuned_gemms: bool = True, batch_qkv_adapters: bool = True):
         self.w = weights
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
@@ -242,6 +253,29 @@ class DoubleBlockLoRA:
         self._side = torch.cuda.Stream(device=self.device) if overlap_streams else None
         if tuned_gemms and self.dtype == torch.bfloat16:
             gemm_tuning.enable()
+        self.rank = int(weights["img"].lora_a["q"].shape[0])
+        self._batched = batch_qkv_adapters and self.dtype == torch.bfloat16 and 3 * self.rank <= 64
+        if self._batched:
+            r = self.rank
+            self._a_qkv, self._a_qkv_t, self._b_t = {}, {}, {}
+            for name in STREAMS:
+                w = weights[name]
+                a = torch.cat([w.lora_a[t] for t in QKV]).contiguous()
+                for j, t in enumerate(QKV):
+                    w.lora_a[t] = a[j * r:(j + 1) * r]  # AdamW updates the stack in place
+                self._a_qkv[name] = a
+                self._a_qkv_t[name] = torch.empty((a.shape[1], 3 * r), dtype=a.dtype, device=a.device)
+                self._b_t[name] = {t: torch.empty((r, w.lora_b[t].shape[0]), dtype=a.dtype, device=a.device)
+                                   for t in QKV}
+            self._refresh_adapters()
+
+    def _refresh_adapters(self) -> None:
+        """The transposed factors the batched adapters read (A_qkv^T for
+        dh += s t A_qkv, B_j^T for t_j = dy_j B_j), after each AdamW step."""
+        for name in STREAMS:
+            self._a_qkv_t[name].copy_(self._a_qkv[name].t())
+            for t in QKV:
+                self._b_t[name][t].copy_(self.w[name].lora_b[t].t())
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
@@ -267,7 +301,7 @@ class DoubleBlockLoRA:
                 n = self.rows[name]
                 for key, width in (("h", C), ("out", C), ("x1", C), ("h2", C), ("y", C), ("t1", C),
                                    ("t2", C), ("dx1", C), ("dx", C), ("pre", F), ("act", F), ("dact", F),
-                                   ("mlp", C)):
+                                   ("mlp", C), ("su", 3 * self.rank), ("tq", 3 * self.rank)):
                     b[f"{key}.{name}"] = torch.empty((n, width), **kw)
             self._buf = b
         return self._buf
@@ -318,8 +352,14 @@ class DoubleBlockLoRA:
         saved[(name, "ln1")] = (mean1, rstd1)
         rows = B["qkv"][off:off + n]
         torch.mm(h, w.w_qkv.t(), out=rows)
-        for j, t in enumerate(("q", "k", "v")):
-            saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
+        if self._batched:
+            r = self.rank
+            su = lora_down(h, self._a_qkv[name], s, out=B[f"su.{name}"])  # [n, 3r] = s h A_qkv^T
+            for j, t in enumerate(QKV):
+                lora_up(su[:, j * r:(j + 1) * r], w.lora_b[t], rows[:, j * C:(j + 1) * C], 1.0)
+        else:
+            for j, t in enumerate(QKV):
+                saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
         cos, sin = self.rope[name]
         qk_prologue(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, self.eps,
                     out=B["q"], seq_offset=off)
@@ -366,9 +406,21 @@ class DoubleBlockLoRA:
                         seq_offset=off, eps=self.eps, dx=drows[:, C:2 * C].view(1, n, H, D))
         h = B[f"h.{name}"]
         dh = torch.mm(drows, w.w_qkv, out=B[f"t2.{name}"]) if want_dx else None
-        for j, t in enumerate(("q", "k", "v")):
-            grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
-                                        drows[:, j * C:(j + 1) * C], s, dx=dh)
+        if self._batched:
+            r = self.rank
+            su, tq = B[f"su.{name}"], B[f"tq.{name}"]
+            for j, t in enumerate(QKV):  # t_j = dy_j B_j
+                lora_down(drows[:, j * C:(j + 1) * C], self._b_t[name][t], 1.0, out=tq[:, j * r:(j + 1) * r])
+            if dh is not None:
+                lora_up(tq, self._a_qkv_t[name], dh, s)  # dh += s t A_qkv
+            da = lora_grad(tq, h, s, transpose=False)  # [3r, C] = s t^T h
+            for j, t in enumerate(QKV):  # dB_j = dy_j^T (s u_j)
+                db = lora_grad(su[:, j * r:(j + 1) * r], drows[:, j * C:(j + 1) * C], 1.0, transpose=True)
+                grads[(name, t)] = (da[j * r:(j + 1) * r], db)
+        else:
+            for j, t in enumerate(QKV):
+                grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
+                                            drows[:, j * C:(j + 1) * C], s, dx=dh)
         grads[(name, "out")] = saved[(name, "out", "grad")]
         if want_dx:
             mean1, rstd1 = saved[(name, "ln1")]
@@ -423,6 +475,8 @@ class DoubleBlockLoRA:
             w = self.w[name]
             adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
             adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
+        if self._batched:
+            self._refresh_adapters()
 
     def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = False):
         """One LoRA block step: forward, backward, AdamW (the unit of the

@@ -250,8 +250,10 @@ fa_status fa_lora_bwd(const fa_lora_bwd_args *args, void *stream);
  * appending A as r extra rows of W makes the product also output u (or, in
  * a backward, dy B).  These three calls are the pieces around such a GEMM,
  * bf16 only, reading and writing the rank columns as row views (u + n*ldu),
- * ldu*2 % 16 == 0 for the 16-byte paths, rank 1..32.  They restate the
- * adapter term of linear_scaled (lib.rs:280-285) and its autograd. */
+ * ldu*2 % 16 == 0 for the 16-byte paths, rank 1..64 (so the adapters of
+ * several projections that share x -- q, k, v -- can run as one stacked
+ * rank).  They restate the adapter term of linear_scaled (lib.rs:280-285)
+ * and its autograd. */
 
 typedef struct fa_lora_down_args {
     int32_t dtype;        /* FA_DTYPE_BF16                                     */

@@ -262,7 +262,7 @@ def test_lora_pieces_validate_before_device_work():
                            u=_FAKE + 6144, ldu=3136)
     if not gpu_available():
         assert L.fa_lora_down(ctypes.byref(dn), None) == ok_dev
-    for field, val, code in (("dtype", 1, _abi.FA_ERR_UNSUPPORTED), ("rank", 33, _abi.FA_ERR_INVALID_ARG),
+    for field, val, code in (("dtype", 1, _abi.FA_ERR_UNSUPPORTED), ("rank", 65, _abi.FA_ERR_INVALID_ARG),
                              ("in_features", 3080, _abi.FA_ERR_UNSUPPORTED), ("ldu", 8, _abi.FA_ERR_INVALID_ARG),
                              ("x", _FAKE + 2, _abi.FA_ERR_INVALID_ARG), ("u", _FAKE + 1, _abi.FA_ERR_INVALID_ARG)):
         bad = _abi.LoraDownArgs.from_buffer_copy(dn)

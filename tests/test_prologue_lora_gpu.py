@@ -185,7 +185,7 @@ def test_lora_bf16_ranks_ragged(r):
     assert rel_l2(host(dx), want_dx) <= 1e-2
 
 
-@pytest.mark.parametrize("r", [4, 16, 32])
+@pytest.mark.parametrize("r", [4, 16, 32, 40, 48, 64])
 def test_lora_pieces_strided_views(r):
     """fa_lora_down / fa_lora_up / fa_lora_grad on the rank-column views a
     GEMM that carries the adapter uses: u lives in extra columns of wider
@@ -193,7 +193,7 @@ def test_lora_pieces_strided_views(r):
     fused product [x | s u] [W | B]^T against x W^T + s u B^T."""
     from foundry_attn.ops import lora_down, lora_grad, lora_up
     rng = np.random.default_rng(200 + r)
-    N, K, M, s, pad = 333, 256, 384, 0.75, 64
+    N, K, M, s, pad = 333, 256, 384, 0.75, 80
     rnd = oracle.bf16_round
     x = rnd(rng.standard_normal((N, K)).astype(np.float32))
     A = rnd(rng.standard_normal((r, K)).astype(np.float32) / r)
