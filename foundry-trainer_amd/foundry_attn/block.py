@@ -267,15 +267,27 @@ class DoubleBlockLoRA:
                 self._a_qkv_t[name] = torch.empty((a.shape[1], 3 * r), dtype=a.dtype, device=a.device)
                 self._b_t[name] = {t: torch.empty((r, w.lora_b[t].shape[0]), dtype=a.dtype, device=a.device)
                                    for t in QKV}
-            self._refresh_adapters()
+            self.refresh_adapters()
 
-    def _refresh_adapters(self) -> None:
-        """The transposed factors the batched adapters read (A_qkv^T for
-        dh += s t A_qkv, B_j^T for t_j = dy_j B_j), after each AdamW step."""
+    def refresh_adapters(self) -> None:
+        """Re-derive what the batched adapter products read from the LoRA
+        factors: the stacked A_qkv, A_qkv^T (for dh += s t A_qkv) and B_j^T
+        (for t_j = dy_j B_j).  apply_adamw calls it; call it after changing
+        lora_a / lora_b any other way (loading a LoRA file: a tensor assigned
+        to lora_a[t] is copied into the stack and replaced by its view)."""
+        if not self._batched:
+            return
+        r = self.rank
         for name in STREAMS:
-            self._a_qkv_t[name].copy_(self._a_qkv[name].t())
+            w, a = self.w[name], self._a_qkv[name]
+            for j, t in enumerate(QKV):
+                view = a[j * r:(j + 1) * r]
+                if w.lora_a[t].data_ptr() != view.data_ptr():
+                    view.copy_(w.lora_a[t])
+                    w.lora_a[t] = view
+            self._a_qkv_t[name].copy_(a.t())
             for t in QKV:
-                self._b_t[name][t].copy_(self.w[name].lora_b[t].t())
+                self._b_t[name][t].copy_(w.lora_b[t].t())
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
@@ -475,8 +487,7 @@ class DoubleBlockLoRA:
             w = self.w[name]
             adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
             adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
-        if self._batched:
-            self._refresh_adapters()
+        self.refresh_adapters()
 
     def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = False):
         """One LoRA block step: forward, backward, AdamW (the unit of the
@@ -599,10 +610,14 @@ class SingleBlockLoRA:
             self.w_in_ext[:, :C] = weights.w_in
             self.w_out_ext = torch.zeros((C + P, C + M), **kw)          # [W_out; A_out; 0]
             self.w_out_ext[:C] = weights.w_out
-            self._refresh_adapters()
+            self.refresh_adapters()
 
-    def _refresh_adapters(self) -> None:
-        """Copy the trainable factors into the GEMM operands (after AdamW)."""
+    def refresh_adapters(self) -> None:
+        """Copy the trainable factors into the GEMM operands that carry them.
+        apply_adamw calls it; call it after changing lora_a / lora_b any other
+        way (loading a LoRA file)."""
+        if not self.fused:
+            return
         C, r, w = self.C, self.r, self.w
         self.w_in_ext[:, C:C + r].copy_(w.lora_b["to_in"])
         self.w_out_ext[C:C + r].copy_(w.lora_a["to_out"])
@@ -742,8 +757,7 @@ class SingleBlockLoRA:
             da, db = grads[t]
             adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
             adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
-        if self.fused:
-            self._refresh_adapters()
+        self.refresh_adapters()
 
     def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = True):
         y, grads = self.forward_backward(x, dy, want_dx=want_dx)

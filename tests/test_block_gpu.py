@@ -190,6 +190,60 @@ def test_block_step_matches_oracle(dtype, want_dx):
         assert min(agree) >= (0.97 if bf else 0.999), key
 
 
+def test_refresh_adapters_after_changing_factors():
+    """LoRA factors changed outside apply_adamw -- a new tensor assigned to
+    lora_a[t] (as a LoRA-file loader would), an in-place copy into
+    lora_b[t] -- followed by refresh_adapters() give the bits of blocks built
+    from the changed factors: the double block (q/k/v adapters stacked, their
+    transposes cached) and the single block (adapters carried by its GEMMs)."""
+    import copy
+    bf = torch.bfloat16
+    rng = np.random.default_rng(77)
+    rnd = oracle.bf16_round
+    case = oracle_mods(make_case(C=256, H=2, T=16, rows=4, cols=8, r=4, bf16=True, seed=7))
+    case2 = copy.deepcopy(case)
+    blk = device_block(case, bf)
+    for name in ("txt", "img"):
+        W2 = case2["W"][name]
+        W2["lora_a"]["q"] = rnd(rng.standard_normal(W2["lora_a"]["q"].shape).astype(np.float32) / 4)
+        W2["lora_b"]["k"] = rnd(0.05 * rng.standard_normal(W2["lora_b"]["k"].shape).astype(np.float32))
+        blk.w[name].lora_a["q"] = dev(W2["lora_a"]["q"], bf)
+        blk.w[name].lora_b["k"].copy_(dev(W2["lora_b"]["k"], bf))
+    blk.refresh_adapters()
+    ref = device_block(case2, bf)
+    x = {k: dev(v, bf) for k, v in case["x"].items()}
+    dy = {k: dev(v, bf) for k, v in case["dy"].items()}
+    (y1, g1), (y2, g2) = (b.forward_backward(x, dy, want_dx=True) for b in (blk, ref))
+    torch.cuda.synchronize()
+    for name in ("txt", "img"):
+        assert torch.equal(y1[name], y2[name]), name
+    assert g1.keys() == g2.keys()
+    for key in g1:
+        parts = (g1[key],) if key[1] == "x" else g1[key]
+        want = (g2[key],) if key[1] == "x" else g2[key]
+        for a, b in zip(parts, want):
+            assert torch.equal(a, b), key
+
+    sc = single_oracle_mods(make_single_case(C=256, H=2, T=40, rows=8, cols=12, r=4, bf16=True, seed=9))
+    sc2 = copy.deepcopy(sc)
+    sblk = device_single_block(sc, bf)
+    sc2["W"]["lora_a"]["to_out"] = rnd(rng.standard_normal(sc["W"]["lora_a"]["to_out"].shape).astype(np.float32) / 4)
+    sc2["W"]["lora_b"]["to_in"] = rnd(0.05 * rng.standard_normal(sc["W"]["lora_b"]["to_in"].shape).astype(np.float32))
+    sblk.w.lora_a["to_out"].copy_(dev(sc2["W"]["lora_a"]["to_out"], bf))
+    sblk.w.lora_b["to_in"].copy_(dev(sc2["W"]["lora_b"]["to_in"], bf))
+    sblk.refresh_adapters()
+    sref = device_single_block(sc2, bf)
+    (y1, g1), (y2, g2) = (b.forward_backward(dev(sc["x"], bf), dev(sc["dy"], bf), want_dx=True) for b in (sblk, sref))
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert g1.keys() == g2.keys()
+    for key in g1:
+        parts = (g1[key],) if key == "x" else g1[key]
+        want = (g2[key],) if key == "x" else g2[key]
+        for a, b in zip(parts, want):
+            assert torch.equal(a, b), key
+
+
 def test_c4_block_step_properties():
     """The full c4 block (4096 img + 512 txt tokens, dim 3072): one step gives
     finite outputs, nonzero finite LoRA gradients that repeat bit for bit, and
