@@ -211,8 +211,6 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         constexpr bool FIRST = decltype(first)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // K_{kb+1}, V_{kb-1} landed; K_kb and V_{kb-2} fully consumed
-        if (kb + 2 < kb1) issue_k(kb + 2, P ? ks1 : ks0);
-        issue_v(kb, P ? vs1 : vs0);
         const char *kn = P ? ks0 : ks1;  // K_{kb+1}
         const char *vp = P ? vs0 : vs1;  // V_{kb-1}
 
@@ -247,6 +245,12 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         float lp = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
+            // The DMA for K_{kb+2} and V_kb goes out after the first and the
+            // second slice rather than in one burst at the barrier, where it
+            // met every wave's first LDS reads (1% off the forward); both
+            // buffers are free from the barrier on, and are read next block.
+            if (ks == 1 && kb + 2 < kb1) issue_k(kb + 2, P ? ks1 : ks0);
+            if (ks == 2) issue_v(kb, P ? vs1 : vs0);
             make_p(c0, c1, pw, lp, ks);
             // The last block computes scores of a stale K tile that are never
             // used: keeping the MFMAs unconditional keeps them interleavable.
