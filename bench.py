@@ -98,6 +98,62 @@ def _time_steps(torch, step, steps: int, warmup: int):
     return (time.perf_counter() - t0) / steps, e0.elapsed_time(e1) * 1e-3 / steps
 
 
+def _event_ms(torch, fn, n: int = 20) -> float:
+    """Mean HIP-event time (ms) of fn() on torch's current stream, the stream
+    the ABI launches on, after warm-up."""
+    for _ in range(3):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def memory_bound_bench(torch, fa, cfg):
+    """Achieved HBM rates of the memory-bound kernels around the attention,
+    from algorithmic bytes (each tensor read or written once) over HIP-event
+    time: the QK-RMSNorm + RoPE prologue at the attention config's Q shape
+    (forward reads x, writes the joint buffer; backward reads x and dy,
+    writes dx; both read the per-token cos/sin rows and the weight) and the
+    LoRA down / up pieces at the c4 img stream's shape (x [4096, 3072],
+    r = 16: down reads x and A, writes u; up reads u and B and updates y in
+    place)."""
+    from foundry_attn.configs import C4
+    g = torch.Generator(device="cuda").manual_seed(7)
+    bf = torch.bfloat16
+    B, S, H, D = cfg.batch, cfg.seq, cfg.heads, cfg.head_dim
+    x = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
+    dy = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
+    w = (1 + 0.02 * torch.randn(D, device="cuda", generator=g)).to(bf)
+    cos, sin = fa.rope_tables(cfg.positions(), cfg.axes, cfg.theta, dtype=bf)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    row = B * S * H * D * 2
+    tables = 2 * S * D * 2 + D * 2
+    N, C, r = C4.img_tokens, C4.hidden, C4.lora_rank
+    lx = torch.randn((N, C), device="cuda", generator=g).to(bf)
+    la = (torch.randn((r, C), device="cuda", generator=g) / r).to(bf)
+    lb = (1e-3 * torch.randn((C, r), device="cuda", generator=g)).to(bf)
+    lu = torch.empty((N, r), device="cuda", dtype=bf)
+    ly = torch.randn((N, C), device="cuda", generator=g).to(bf)
+    cases = {
+        "qk_prologue_fwd": (lambda: fa.qk_prologue(x, w, cos, sin, cfg.axes, out=y), 2 * row + tables),
+        "qk_prologue_bwd": (lambda: fa.qk_prologue_bwd(x, w, cos, sin, cfg.axes, dy, dx=dx), 3 * row + tables),
+        "lora_down": (lambda: fa.lora_down(lx, la, 1.0, out=lu), N * C * 2 + r * C * 2 + N * r * 2),
+        "lora_up": (lambda: fa.lora_up(lu, lb, ly, 1.0), 2 * N * C * 2 + N * r * 2 + C * r * 2),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        ms = _event_ms(torch, fn)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
+    out["shapes"] = (f"prologue: B={B} S={S} H={H} D={D} bf16; lora: N={N} C={C} r={r} bf16")
+    return out
+
+
 def _lora_flops(N, r, fin, fout):
     """x A^T, u B^T forward; dB, du, dA, dx backward: 6 skinny GEMMs of 2 N r (in or out)."""
     return 6 * N * r * (fin + fout)
@@ -350,6 +406,7 @@ def main():
                      "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
                      "traffic": TRAFFIC.get((cfg.name, dominant))},
         "kernels": kernels,
+        "memory_bound": memory_bound_bench(torch, fa, cfg),
     }
     if args.block_steps > 0:
         rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
