@@ -162,19 +162,33 @@ class AttnBwd:
     slot is missing (a `res` this instance did not produce) the forward is
     rerun to regenerate it, as the reference's backward recomputes its
     probabilities.
+
+    Host (CPU) tensors take the `cpu_fwd` route as the Rust shim does: they
+    are staged to the current GPU, the HIP kernels run there, and the results
+    come back as host tensors (no CPU computation path exists).
     """
 
     def __init__(self, scale: Optional[float] = None, key_keep=None):
         self.scale = scale
         self.key_keep = key_keep
-        self._saved = None  # (data_ptr of res, version, lse)
+        self._saved = None  # (data_ptr of res, version, lse on the device)
 
     @staticmethod
     def name() -> str:
         return lib().fa_op_name().decode()
 
+    @staticmethod
+    def _staged(*ts):
+        dev = torch.device("cuda", torch.cuda.current_device())
+        return tuple(t.to(dev) for t in ts)
+
     def fwd(self, q, k, v):
+        host = not q.is_cuda
+        if host:
+            q, k, v = self._staged(q, k, v)
         o, lse = attn_fwd(q, k, v, self.scale, self.key_keep)
+        if host:
+            o = o.cpu()
         self._saved = (o.data_ptr(), o._version, lse)
         return o
 
@@ -182,9 +196,13 @@ class AttnBwd:
         lse = None
         if self._saved is not None and self._saved[0] == res.data_ptr() and self._saved[1] == res._version:
             lse = self._saved[2]
+        host = not q.is_cuda
+        if host:
+            q, k, v, res, grad_res = self._staged(q, k, v, res, grad_res)
         if lse is None:
             _, lse = attn_fwd(q, k, v, self.scale, self.key_keep)
-        return attn_bwd(q, k, v, res, grad_res, lse, self.scale, self.key_keep)
+        grads = attn_bwd(q, k, v, res, grad_res, lse, self.scale, self.key_keep)
+        return tuple(g.cpu() for g in grads) if host else grads
 
 
 class _AttentionFn(torch.autograd.Function):

@@ -302,6 +302,32 @@ def test_custom_op_surface_and_autograd():
     assert torch.equal(qa.grad, dq) and torch.equal(ka.grad, dk) and torch.equal(va.grad, dv)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_custom_op_host_tensors_take_the_cpu_fwd_route(dtype):
+    """Host (CPU) tensors through AttnBwd -- the reference's cpu_fwd path
+    (lib.rs:158-187) -- are staged to the GPU, run by the same kernels and
+    returned as host tensors: bit-identical to the device call (the reference
+    f32 CPU case c1's shape)."""
+    torch.manual_seed(2)
+    q, k, v, g = (torch.randn(256, 4, 64).to(dtype) for _ in range(4))
+    op = AttnBwd()
+    res = op.fwd(q, k, v)
+    assert res.device.type == "cpu" and res.dtype == dtype
+    grads = op.bwd(q, k, v, res, g)
+    assert all(t.device.type == "cpu" for t in grads)
+    dev_op = AttnBwd()
+    dres = dev_op.fwd(q.cuda(), k.cuda(), v.cuda())
+    dgrads = dev_op.bwd(q.cuda(), k.cuda(), v.cuda(), dres, g.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(res, dres.cpu())
+    for a, b in zip(grads, dgrads):
+        assert torch.equal(a, b.cpu())
+    # a fresh instance regenerates the LSE from the host inputs: same bits
+    fresh = AttnBwd().bwd(q, k, v, res, g)
+    for a, b in zip(grads, fresh):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("B,S,H,D", [(2, 700, 3, 128), (1, 1100, 44, 128), (1, 1100, 44, 64)],
                          ids=["4wave", "8wave", "8wave_d64"])
 def test_backward_phases_match_single_call(B, S, H, D):
