@@ -101,7 +101,9 @@ struct DkvTile {
     static_assert(WI >= 1 && WI * NW == T::WAVE_INSTS, "tile split over waves");
 };
 
-template <int D, int NW>
+// SPLIT: the workgroup streams only its partition's query blocks and leaves
+// unscaled f32 partial dK, dV (the reduce pass applies the mask and scale).
+template <int D, int NW, bool SPLIT>
 __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
     using F = DkvTile<D, NW>;
     constexpr int kKT = F::KT;
@@ -111,7 +113,20 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nk = (S + kKT - 1) / kKT;
-    const int kt = work % nk, bh = work / nk;
+    const int nqb = (S + kQB - 1) / kQB;
+    const int kt = work % nk;
+    int bh, qpart = 0, qb0 = 0, qb1 = nqb;  // qpart: this workgroup's query range
+    if constexpr (SPLIT) {
+        qpart = (work / nk) % p.split;
+        bh = work / (nk * p.split);
+        int c0, c1;
+        split_chunks(S, p.split, qpart, c0, c1);
+        constexpr int kBPC = kSplitChunk / kQB;
+        qb0 = c0 * kBPC;
+        qb1 = min(c1 * kBPC, nqb);
+    } else {
+        bh = work / nk;
+    }
     const int h = bh % H, b = bh / H;
 
     const bf16 *qbase = static_cast<const bf16 *>(p.q) + b * p.q_sb + h * p.q_sh;
@@ -167,13 +182,12 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
         for (int r = 0; r < 16; ++r) dk[dt][r] = dv[dt][r] = 0.f;
     const float c = p.scale_log2;
 
-    const int nqb = (S + kQB - 1) / kQB;
-    issue(0, 0);
+    issue(qb0, 0);
     auto stage = [&](auto par, int qb) {
-        constexpr int P = decltype(par)::value;  // qb % 2
+        constexpr int P = decltype(par)::value;  // (qb - qb0) % 2
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (qb + 1 < nqb) issue(qb + 1, P ^ 1);
+        if (qb + 1 < qb1) issue(qb + 1, P ^ 1);
         const char *st = P ? stage1 : stage0;
         const char *qs_t = st + F::Q_OFF, *os_t = st + F::DO_OFF;
         const float *lse_s = reinterpret_cast<const float *>(st + F::LSE_OFF);
@@ -224,9 +238,28 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
                 }
         }
     };
-    for (int qb = 0; qb < nqb; qb += 2) {
+    for (int qb = qb0; qb < qb1; qb += 2) {
         stage(std::integral_constant<int, 0>{}, qb);
-        if (qb + 1 < nqb) stage(std::integral_constant<int, 1>{}, qb + 1);
+        if (qb + 1 < qb1) stage(std::integral_constant<int, 1>{}, qb + 1);
+    }
+
+    if constexpr (SPLIT) {
+        // element r of lane: key kt*KT + wave*32 + acc_row(r), d = dt*32 + n
+        const int64_t rows = (int64_t)p.B * H * S;
+        float *pk = p.part_dk + (qpart * rows + (int64_t)bh * S) * D;
+        float *pv = p.part_dv + (qpart * rows + (int64_t)bh * S) * D;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kt * kKT + wave * 32 + acc_row(r, lane);
+            if (key < S) {
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt) {
+                    pk[(int64_t)key * D + dt * 32 + n] = dk[dt][r];
+                    pv[(int64_t)key * D + dt * 32 + n] = dv[dt][r];
+                }
+            }
+        }
+        return;
     }
 
     // accumulators: element r of lane = (key kt*KT + wave*32 + acc_row(r), d = dt*32 + n).
@@ -275,7 +308,9 @@ struct DqTile {
 // then runs after it), so the whole backward is two launches.  The row sum
 // follows the pre-pass's order exactly -- sequential sums over 8-element
 // parts, then an xor butterfly over the parts -- so both give the same bits.
-template <int D, bool KEEP, int NW, bool DELTA>
+// SPLIT: the workgroup streams only its partition's key units and leaves an
+// unscaled f32 partial dQ; with DELTA, key range 0 stores the pre-pass rows.
+template <int D, bool KEEP, int NW, bool DELTA, bool SPLIT>
 __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     using F = DqTile<D, NW>;
     constexpr int kQT = F::QT;
@@ -285,7 +320,20 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     const int n = lane & 31, g = lane >> 5;
     const int S = p.S, H = p.H;
     const int nq = (S + kQT - 1) / kQT;
-    const int qt = work % nq, bh = work / nq;
+    const int qt = work % nq;
+    const int nku4 = (((S + kKU - 1) / kKU) + 3) & ~3;
+    int bh, kpart = 0, u0 = 0, u1 = nku4;  // kpart: this workgroup's key range
+    if constexpr (SPLIT) {
+        kpart = (work / nq) % p.split;
+        bh = work / (nq * p.split);
+        int c0, c1;
+        split_chunks(S, p.split, kpart, c0, c1);
+        constexpr int kUPC = kSplitChunk / kKU;  // 4 units per chunk
+        u0 = c0 * kUPC;
+        u1 = c1 * kUPC;  // the last part ends at nku4
+    } else {
+        bh = work / nq;
+    }
     const int h = bh % H, b = bh / H;
 
     const bf16 *qbase = static_cast<const bf16 *>(p.q) + b * p.q_sb + h * p.q_sh;
@@ -362,7 +410,7 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
         if (qi < S) {
             const float l = p.lse[qrow];
             lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
-            if (g == 0) {
+            if (g == 0 && kpart == 0) {
                 p.delta[qrow] = dlt;
                 p.lse2[qrow] = lse2;
             }
@@ -391,13 +439,11 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     // and are fully masked).  Every unit issues its prefetch and its next
     // keep-byte load unconditionally, so each unit sees the same loads in
     // flight and the only waits are the explicit ones at the barriers.
-    const int nku = (S + kKU - 1) / kKU;
-    const int nku4 = (nku + 3) & ~3;
     // keep byte of this lane's key in unit u (clamped address; KEEP only)
     auto keep_byte = [&](int u) -> uint32_t { return KEEP ? keep[min(u * kKU + n, S - 1)] : 1u; };
-    uint32_t kbyte = keep_byte(0);
+    uint32_t kbyte = keep_byte(u0);
     auto unit = [&](auto par, int u, f32x16 &sc, f32x16 &dc, f32x16 &sn, f32x16 &dn) {
-        constexpr int P = decltype(par)::value;  // u % 4
+        constexpr int P = decltype(par)::value;  // u % 4 (u0 is a multiple of 4)
         // unit u+1 landed (unit u+2, 2*WI loads per wave, may still be in
         // flight, as may the keep byte issued after it); unit u-1 consumed
         barrier_keep_dma<2 * F::WI>();
@@ -454,16 +500,16 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
         }
     };
 
-    // prologue: units 0..2 issued, unit 0's scores computed
-    issue(0, k0, v0);
-    issue(1, k1, v1);
-    issue(2, k2, v2);
+    // prologue: units u0..u0+2 issued, unit u0's scores computed
+    issue(u0, k0, v0);
+    issue(u0 + 1, k1, v1);
+    issue(u0 + 2, k2, v2);
     barrier_keep_dma<0>();
     f32x16 sa0, da0, sa1, da1;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa0[r] = da0[r] = 0.f;
     sdp(k0, v0, sa0, da0, 0, D / 16);
-    for (int u = 0; u < nku4; u += 4) {
+    for (int u = u0; u < u1; u += 4) {
         unit(std::integral_constant<int, 0>{}, u, sa0, da0, sa1, da1);
         unit(std::integral_constant<int, 1>{}, u + 1, sa1, da1, sa0, da0);
         unit(std::integral_constant<int, 2>{}, u + 2, sa0, da0, sa1, da1);
@@ -473,6 +519,21 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     // workgroup can end
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+    if constexpr (SPLIT) {
+        if (qi < S) {
+            float *row = p.part_dq + ((int64_t)kpart * p.B * H * S + (int64_t)bh * S + qi) * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp) {
+                    f32x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = dq[dt][grp * 4 + e];
+                    *reinterpret_cast<f32x4 *>(row + dt * 32 + grp * 8 + g * 4) = w;
+                }
+        }
+        return;
+    }
     if (qi < S) {
         bf16 *row = static_cast<bf16 *>(p.dq) + b * p.dq_sb + h * p.dq_sh + qi * p.dq_ss;
 #pragma unroll
@@ -489,22 +550,74 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
 }
 
 // 2 waves per SIMD (<= 256 VGPRs) for either workgroup size.
-template <int D, int NW>
+template <int D, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
-    dkdv_block<D, NW>(p, xcd_remap(blockIdx.x, gridDim.x));
+    dkdv_block<D, NW, SPLIT>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
-template <int D, bool KEEP, int NW, bool DELTA>
+template <int D, bool KEEP, int NW, bool DELTA, bool SPLIT>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq_bf16_kernel(AttnBwdParams p) {
-    dq_block<D, KEEP, NW, DELTA>(p, xcd_remap(blockIdx.x, gridDim.x));
+    dq_block<D, KEEP, NW, DELTA, SPLIT>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
-template <int D, int NW, bool DELTA>
+template <int D, int NW, bool DELTA, bool SPLIT>
 void launch_dq(const AttnBwdParams &p, dim3 grid, dim3 block, hipStream_t s) {
     if (p.keep)
-        hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, true, NW, DELTA>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, true, NW, DELTA, SPLIT>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, false, NW, DELTA>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<D, false, NW, DELTA, SPLIT>), grid, block, 0, s, p);
+}
+
+// Sums the split partials of gradients [z0, z0 + nz) (0 dQ, 1 dK, 2 dV) in
+// partition order and stores them as the unsplit kernels do: dQ and dK times
+// the scale, dK and dV rows of an excluded key zero (selected: a masked key's
+// partials may hold overflowed values).  One thread per 8 features of a row.
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(AttnBwdParams p, int z0) {
+    constexpr int kCPR = D / 8;
+    const int64_t rows = (int64_t)p.B * p.H * p.S;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * kCPR) return;
+    const int z = z0 + (int)blockIdx.y;
+    const int64_t row = idx / kCPR;
+    const int c = (int)(idx % kCPR);
+    const int S = p.S, H = p.H;
+    const int s = (int)(row % S), h = (int)((row / S) % H), b = (int)(row / ((int64_t)S * H));
+    const float *src = z == 0 ? p.part_dq : z == 1 ? p.part_dk : p.part_dv;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < p.split; ++q) {
+        const f32x4 *v = reinterpret_cast<const f32x4 *>(src + (q * rows + row) * D + c * 8);
+        const f32x4 lo = v[0], hi = v[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[e] += lo[e];
+            acc[4 + e] += hi[e];
+        }
+    }
+    const bool kept = z == 0 || !p.keep || p.keep[(int64_t)b * S + s];
+    const float f = z == 2 ? 1.f : p.scale;
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf16x2(kept ? acc[2 * e] * f : 0.f, kept ? acc[2 * e + 1] * f : 0.f);
+    bf16 *dst;
+    if (z == 0)
+        dst = static_cast<bf16 *>(p.dq) + b * p.dq_sb + h * p.dq_sh + s * p.dq_ss;
+    else if (z == 1)
+        dst = static_cast<bf16 *>(p.dk) + b * p.dk_sb + h * p.dk_sh + s * p.dk_ss;
+    else
+        dst = static_cast<bf16 *>(p.dv) + b * p.dv_sb + h * p.dv_sh + s * p.dv_ss;
+    *reinterpret_cast<u32x4 *>(dst + c * 8) = w;
+}
+
+hipError_t launch_reduce(const AttnBwdParams &p, int D, int z0, int nz, hipStream_t s) {
+    const int64_t threads = (int64_t)p.B * p.H * p.S * (D / 8);
+    const dim3 grid((unsigned)((threads + 255) / 256), nz), block(256);
+    if (D == 128)
+        hipLaunchKernelGGL(attn_bwd_reduce_kernel<128>, grid, block, 0, s, p, z0);
+    else
+        hipLaunchKernelGGL(attn_bwd_reduce_kernel<64>, grid, block, 0, s, p, z0);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -679,7 +792,36 @@ hipError_t launch_delta(const AttnBwdParams &p, hipStream_t s) {
 
 }  // namespace
 
+// Split backward (p.split > 1, 8-wave dK/dV; dQ with 8 waves at D = 128, 4
+// at D = 64), in order on one stream.  All phases: dQ partials (partition 0
+// also writing the pre-pass rows), dK/dV partials, one reduce of all three.
+// Phase 2 / 3 alone: the partials, then their own reduce (dK/dV and dQ use
+// separate partial buffers, so they may run concurrently after the pre-pass).
+hipError_t launch_attn_bwd_split(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
+    hipError_t e = hipSuccess;
+    if (phase == 1) return D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
+    if (phase == 0 || phase == 3) {
+        const int nw_q = D == 128 ? 8 : 4;
+        const dim3 grid(p.B * p.H * ((p.S + nw_q * 32 - 1) / (nw_q * 32)) * p.split), block(nw_q * 64);
+        const bool delta = phase == 0;
+        if (D == 128)
+            delta ? launch_dq<128, 8, true, true>(p, grid, block, s) : launch_dq<128, 8, false, true>(p, grid, block, s);
+        else
+            delta ? launch_dq<64, 4, true, true>(p, grid, block, s) : launch_dq<64, 4, false, true>(p, grid, block, s);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (phase == 3) return launch_reduce(p, D, 0, 1, s);
+    }
+    const dim3 grid(p.B * p.H * ((p.S + 255) / 256) * p.split), block(512);
+    if (D == 128)
+        hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 8, true>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 8, true>), grid, block, 0, s, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return phase == 0 ? launch_reduce(p, D, 0, 3, s) : launch_reduce(p, D, 1, 2, s);
+}
+
 hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
+    if (p.split > 1) return launch_attn_bwd_split(p, D, phase, s);
     // workgroup shape as for the forward (attn_waves); dQ at D = 64 streams
     // 4 KiB units, too small to split over 8 waves.
     const int nw = attn_waves(p.B, p.H, p.S);
@@ -695,24 +837,26 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStr
     auto dq = [&](bool delta) {
         const dim3 grid(p.B * p.H * ((p.S + nw_q * 32 - 1) / (nw_q * 32))), block(nw_q * 64);
         if (D == 128 && nw_q == 8)
-            delta ? launch_dq<128, 8, true>(p, grid, block, s) : launch_dq<128, 8, false>(p, grid, block, s);
+            delta ? launch_dq<128, 8, true, false>(p, grid, block, s)
+                  : launch_dq<128, 8, false, false>(p, grid, block, s);
         else if (D == 128)
-            delta ? launch_dq<128, 4, true>(p, grid, block, s) : launch_dq<128, 4, false>(p, grid, block, s);
+            delta ? launch_dq<128, 4, true, false>(p, grid, block, s)
+                  : launch_dq<128, 4, false, false>(p, grid, block, s);
         else
-            delta ? launch_dq<64, 4, true>(p, grid, block, s) : launch_dq<64, 4, false>(p, grid, block, s);
+            delta ? launch_dq<64, 4, true, false>(p, grid, block, s) : launch_dq<64, 4, false, false>(p, grid, block, s);
         return hipGetLastError();
     };
     if (fused && (e = dq(true)) != hipSuccess) return e;
     if (phase == 0 || phase == 2) {
         const dim3 grid(p.B * p.H * ((p.S + nw * 32 - 1) / (nw * 32))), block(nw * 64);
         if (D == 128 && nw == 8)
-            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 8>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 8, false>), grid, block, 0, s, p);
         else if (D == 128)
-            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 4>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 4, false>), grid, block, 0, s, p);
         else if (nw == 8)
-            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 8>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 8, false>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 4>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 4, false>), grid, block, 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (!fused && (phase == 0 || phase == 3)) e = dq(false);

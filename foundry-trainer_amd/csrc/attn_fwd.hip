@@ -333,14 +333,101 @@ __device__ __forceinline__ void fwd_store(const AttnFwdParams &p, int t, const F
     }
 }
 
-// One workgroup per NW*32-query tile; 2 waves per SIMD (<= 256 VGPRs).
+// Split partial of query tile t over one key range: O / l in f32 and the
+// range's natural-log LSE (-inf when none of its keys is kept).
 template <int D, int NW>
+__device__ __forceinline__ void fwd_store_part(const AttnFwdParams &p, int t, int part, const FwdState<D> &st) {
+    constexpr int kBM = FwdTile<D, NW>::BM;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int S = p.S;
+    const int nq = (S + kBM - 1) / kBM;
+    const int qt = t % nq, bh = t / nq;
+    const int qi = qt * kBM + wave * 32 + n;
+    const float l_tot = sum_xor32(st.l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (qi < S) {
+        const int64_t row = ((int64_t)part * p.B * p.H + bh) * S + qi;
+        float *orow = p.part_o + row * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                f32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = st.o[dt][grp * 4 + e] * inv;
+                *reinterpret_cast<f32x4 *>(orow + dt * 32 + grp * 8 + g * 4) = w;
+            }
+        if (g == 0)
+            p.part_lse[row] = l_tot > 0.f ? (st.m_sc + log2_fast(l_tot)) * 0.6931471805599453f : -INFINITY;
+    }
+}
+
+// One workgroup per NW*32-query tile; 2 waves per SIMD (<= 256 VGPRs).
+// SPLIT: p.split workgroups per tile, each over one key range.
+template <int D, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
     const int nkb = (p.S + kBN - 1) / kBN;
-    const int t = xcd_remap(blockIdx.x, gridDim.x);
+    const int w = xcd_remap(blockIdx.x, gridDim.x);
     FwdState<D> st;
-    fwd_tile<D, NW>(p, t, 0, nkb, st);
-    fwd_store<D, NW>(p, t, st);
+    if constexpr (SPLIT) {
+        constexpr int kBM = FwdTile<D, NW>::BM;
+        const int nq = (p.S + kBM - 1) / kBM;
+        const int qt = w % nq, part = (w / nq) % p.split, bh = w / (nq * p.split);
+        int c0, c1;
+        split_chunks(p.S, p.split, part, c0, c1);
+        constexpr int kBPC = kSplitChunk / kBN;  // key blocks per chunk
+        const int t = bh * nq + qt;
+        fwd_tile<D, NW>(p, t, c0 * kBPC, min(c1 * kBPC, nkb), st);
+        fwd_store_part<D, NW>(p, t, part, st);
+    } else {
+        fwd_tile<D, NW>(p, w, 0, nkb, st);
+        fwd_store<D, NW>(p, w, st);
+    }
+}
+
+// Combines the split partials of each query row through their LSEs:
+// LSE = log sum_p exp(LSE_p), O = sum_p exp(LSE_p - LSE) O_p, summed in
+// partition order.  One thread per 8 features of a row.
+template <int D>
+__global__ __launch_bounds__(256) void attn_fwd_combine_kernel(AttnFwdParams p) {
+    constexpr int kCPR = D / 8;  // threads per row
+    const int64_t rows = (int64_t)p.B * p.H * p.S;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * kCPR) return;
+    const int64_t row = idx / kCPR;
+    const int c = (int)(idx % kCPR);
+    const int S = p.S, H = p.H;
+    const int s = (int)(row % S), h = (int)((row / S) % H), b = (int)(row / ((int64_t)S * H));
+    float m = -INFINITY;
+    for (int q = 0; q < p.split; ++q) m = fmaxf(m, p.part_lse[q * rows + row]);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lse = -INFINITY;
+    if (m != -INFINITY) {
+        float den = 0.f;
+        for (int q = 0; q < p.split; ++q) {
+            const float wq = expf(p.part_lse[q * rows + row] - m);
+            den += wq;
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(p.part_o + (q * rows + row) * D + c * 8);
+            const f32x4 lo = src[0], hi = src[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[e] += wq * lo[e];
+                acc[4 + e] += wq * hi[e];
+            }
+        }
+        const float inv = 1.f / den;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= inv;
+        lse = m + logf(den);
+    }
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(acc[2 * e], acc[2 * e + 1]);
+    bf16 *orow = static_cast<bf16 *>(p.o) + b * p.o_sb + h * p.o_sh + s * p.o_ss;
+    *reinterpret_cast<u32x4 *>(orow + c * 8) = w;
+    if (c == 0) p.lse[row] = lse;
 }
 
 // ---------------------------------------------------------------------------
@@ -450,8 +537,9 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(AttnFwdParams p) {
 // L2 -> LDS bytes per FLOP but only pay when the 8-wave grid's last round is
 // at least half full: measured on MI355X, c2 (B1 H24 S4608: last round 69%
 // full) +3.6% and c5 (B2 S6656: 88%) +3% fwd+bwd, c3 (B4 S1536: 25%) -13%.
-int attn_waves(int B, int H, int S) {
-    if (S < 512) return 4;  // fewer than two 256-row tiles per (b, h)
+namespace {
+// CU count of the current device (cached per device; 256 if unknown).
+int device_cus() {
     static int cus[64];
     int dev = 0;
     int n = 256;
@@ -462,24 +550,73 @@ int attn_waves(int B, int H, int S) {
             __atomic_store_n(&cus[dev], c, __ATOMIC_RELAXED);
         if (c > 0) n = c;
     }
+    return n;
+}
+}  // namespace
+
+int attn_waves(int B, int H, int S) {
+    if (S < 512) return 4;  // fewer than two 256-row tiles per (b, h)
+    if (attn_split(B, H, S) > 1) return 8;
+    const int n = device_cus();
     const int64_t wg = (int64_t)B * H * ((S + 255) / 256);
     const int64_t last = wg % n == 0 ? n : wg % n;
     return 2 * last >= n ? 8 : 4;
 }
 
+// Range split for grids that leave most CUs idle: with at most half the CUs
+// busy even at 8 waves (B*H*ceil(S/256) <= CUs/2, e.g. 3 or 6 heads at
+// S = 4608, one GPU's share of 24 heads over 8 or 4 GPUs), each tile's key
+// range (forward, dQ) or query range (dK/dV) is cut into `split` parts of at
+// least 512 rows, so the grid grows to about one workgroup per CU.  The
+// partials cost an f32 write and read of split x O (or of each gradient).
+int attn_split(int B, int H, int S) {
+    if (S < 1024) return 1;
+    const int n = device_cus();
+    const int64_t wg = (int64_t)B * H * ((S + 255) / 256);
+    if (2 * wg > n) return 1;
+    const int nc = (S + kSplitChunk - 1) / kSplitChunk;
+    int64_t split = n / wg;
+    split = split < nc / 4 ? split : nc / 4;  // >= 4 chunks (512 rows) per part
+    split = split < 16 ? split : 16;
+    return split > 1 ? (int)split : 1;
+}
+
+size_t attn_split_elems(int B, int H, int S, int D, int split) {
+    return split > 1 ? (size_t)split * B * H * S * D : 0;
+}
+
+// p.split > 1 (set by the caller from attn_split, with the partial buffers):
+// 8-wave split grid, then the combine pass.
 hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s) {
+    if (p.split > 1) {
+        const int nq = (p.S + 255) / 256;
+        const dim3 grid(p.B * p.H * nq * p.split), block(512);
+        if (D == 128)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, true>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, true>), grid, block, 0, s, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t threads = (int64_t)p.B * p.H * p.S * (D / 8);
+        const dim3 cgrid((unsigned)((threads + 255) / 256)), cblock(256);
+        if (D == 128)
+            hipLaunchKernelGGL(attn_fwd_combine_kernel<128>, cgrid, cblock, 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_fwd_combine_kernel<64>, cgrid, cblock, 0, s, p);
+        return hipGetLastError();
+    }
     const int nw = attn_waves(p.B, p.H, p.S);
     const int bm = nw * 32;
     const int nq = (p.S + bm - 1) / bm;
     const dim3 grid(p.B * p.H * nq), block(nw * 64);
     if (D == 128 && nw == 8)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, false>), grid, block, 0, s, p);
     else if (D == 128)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 4>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 4, false>), grid, block, 0, s, p);
     else if (nw == 8)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, false>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 4>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 4, false>), grid, block, 0, s, p);
     return hipGetLastError();
 }
 

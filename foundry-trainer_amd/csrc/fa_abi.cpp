@@ -127,9 +127,26 @@ fa_status check_buffer_view(const char *name, const fa_strides &st, int32_t S, i
 
 size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// backward workspace: delta [B,H,S] f32, then lse2 [B,H,S] f32
-size_t bwd_workspace(int32_t B, int32_t S, int32_t H) {
-    return 2 * round256((size_t)B * H * S * sizeof(float));
+// Range split factor of a bf16 call (1 for f32 or unsplit shapes).
+int split_for(int32_t dtype, int32_t B, int32_t S, int32_t H) {
+    return dtype == FA_DTYPE_BF16 ? fa::attn_split(B, H, S) : 1;
+}
+
+// backward workspace: delta [B,H,S] f32, lse2 [B,H,S] f32, then for a split
+// call the f32 partials of dQ, dK and dV ([split][B,H,S][D] each)
+size_t bwd_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D) {
+    const int split = split_for(dtype, B, S, H);
+    return 2 * round256((size_t)B * H * S * sizeof(float)) +
+           3 * round256(fa::attn_split_elems(B, H, S, D, split) * sizeof(float));
+}
+
+// forward workspace of a split call: O partials [split][B,H,S][D] f32, then
+// the partial LSEs [split][B,H,S] f32; 0 when the call does not split
+size_t fwd_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D) {
+    const int split = split_for(dtype, B, S, H);
+    if (split <= 1) return 0;
+    return round256(fa::attn_split_elems(B, H, S, D, split) * sizeof(float)) +
+           round256((size_t)split * B * H * S * sizeof(float));
 }
 
 #define FA_TRY(expr)                      \
@@ -186,6 +203,22 @@ fa_status fa_attn_fwd(const fa_attn_fwd_args *a, void *stream) {
     p.B = a->batch; p.S = a->seq; p.H = a->heads;
     p.scale = a->scale;
     p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.split = 1;
+    if (a->workspace) {
+        const size_t need = fwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+        if (!aligned(a->workspace, 256)) return fail(FA_ERR_INVALID_ARG, "workspace is not 256-byte aligned");
+        if (a->workspace_bytes < need)
+            return fail(FA_ERR_INVALID_ARG,
+                        "workspace of %zu bytes is smaller than the %zu a split forward needs (NULL runs unsplit)",
+                        a->workspace_bytes, need);
+        if (need > 0) {
+            p.split = split_for(a->dtype, a->batch, a->seq, a->heads);
+            p.part_o = static_cast<float *>(a->workspace);
+            p.part_lse = reinterpret_cast<float *>(
+                static_cast<char *>(a->workspace) +
+                round256(fa::attn_split_elems(a->batch, a->heads, a->seq, a->head_dim, p.split) * sizeof(float)));
+        }
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t e = a->dtype == FA_DTYPE_BF16 ? fa::launch_attn_fwd_bf16(p, a->head_dim, s)
                                                    : fa::launch_attn_fwd_f32(p, a->head_dim, s);
@@ -193,9 +226,14 @@ fa_status fa_attn_fwd(const fa_attn_fwd_args *a, void *stream) {
     return ok();
 }
 
+size_t fa_attn_fwd_workspace_size(const fa_attn_fwd_args *a) {
+    if (!a || a->batch < 1 || a->seq < 1 || a->heads < 1 || (a->head_dim != 64 && a->head_dim != 128)) return 0;
+    return fwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+}
+
 size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *a) {
-    if (!a || a->batch < 1 || a->seq < 1 || a->heads < 1) return 0;
-    return bwd_workspace(a->batch, a->seq, a->heads);
+    if (!a || a->batch < 1 || a->seq < 1 || a->heads < 1 || (a->head_dim != 64 && a->head_dim != 128)) return 0;
+    return bwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
 }
 
 fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
@@ -291,7 +329,7 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stre
         FA_TRY(check_buffer_view("v", a->v_stride, a->seq, a->head_dim));
         FA_TRY(check_buffer_view("dout", a->do_stride, a->seq, a->head_dim));
     }
-    const size_t need = bwd_workspace(a->batch, a->seq, a->heads);
+    const size_t need = bwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
     if (!a->workspace || !aligned(a->workspace, 256))
         return fail(FA_ERR_INVALID_ARG, "workspace is NULL or not 256-byte aligned");
     if (a->workspace_bytes < need)
@@ -316,6 +354,16 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stre
     p.B = a->batch; p.S = a->seq; p.H = a->heads;
     p.scale = a->scale;
     p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.split = split_for(a->dtype, a->batch, a->seq, a->heads);
+    if (p.split > 1) {
+        const size_t rows = round256((size_t)a->batch * a->heads * a->seq * sizeof(float));
+        const size_t part = round256(
+            fa::attn_split_elems(a->batch, a->heads, a->seq, a->head_dim, p.split) * sizeof(float));
+        char *base = static_cast<char *>(a->workspace) + 2 * rows;
+        p.part_dq = reinterpret_cast<float *>(base);
+        p.part_dk = reinterpret_cast<float *>(base + part);
+        p.part_dv = reinterpret_cast<float *>(base + 2 * part);
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t e = a->dtype != FA_DTYPE_BF16 ? fa::launch_attn_bwd_f32(p, a->head_dim, phase, s)
                          : phase == FA_BWD_ALL     ? launch_bwd_forked(p, a->head_dim, s)

@@ -102,4 +102,15 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
+// Range split: a sequence of S rows (queries or keys) is cut into 128-row
+// chunks, and partition `part` of `split` covers chunks [c0, c1).  Work ids
+// of a split grid run (b*H + h, part, tile), so the tiles that stream the
+// same range are neighbours and share an XCD's L2.
+constexpr int kSplitChunk = 128;
+__host__ __device__ __forceinline__ void split_chunks(int S, int split, int part, int &c0, int &c1) {
+    const int nc = (S + kSplitChunk - 1) / kSplitChunk;
+    c0 = part * nc / split;
+    c1 = (part + 1) * nc / split;
+}
+
 }  // namespace fa

@@ -19,6 +19,11 @@ struct AttnFwdParams {
     int B, S, H;
     float scale;       // softmax scale
     float scale_log2;  // scale * log2(e)
+    // Key-range split (split > 1, bf16 only): `split` workgroups per query
+    // tile each cover a range of keys and leave O / l (f32, [split][B*H*S][D])
+    // and the range's LSE ([split][B*H*S]) here; a combine pass writes o, lse.
+    int split;
+    float *part_o, *part_lse;
 };
 
 struct AttnBwdParams {
@@ -38,6 +43,11 @@ struct AttnBwdParams {
     int64_t dv_sb, dv_ss, dv_sh;
     int B, S, H;
     float scale, scale_log2;
+    // Split (split > 1, bf16 only): dQ workgroups cover a range of keys, dK/dV
+    // workgroups a range of queries; each leaves unscaled f32 partial sums
+    // ([split][B*H*S][D] per gradient) here and a reduce pass writes dq, dk, dv.
+    int split;
+    float *part_dq, *part_dk, *part_dv;
 };
 
 // Returns hipSuccess or the launch error.  `D` is 64 or 128.
@@ -49,6 +59,12 @@ hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStr
 // forward, dK/dV and D = 128 dQ kernels for B x H sequences of S tokens on
 // the current device (see attn_fwd.hip).
 int attn_waves(int B, int H, int S);
+// Range split factor (1 = none) of the bf16 kernels for B x H sequences of S
+// tokens on the current device: > 1 when even 8-wave workgroups would leave
+// most CUs idle (e.g. one GPU's share of heads under sequence parallelism).
+int attn_split(int B, int H, int S);
+// f32 elements of the split partials per gradient or O (split * B*H*S*D).
+size_t attn_split_elems(int B, int H, int S, int D, int split);
 hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStream_t s);
 
 // One-time per-process kernel attribute setup (dynamic LDS limits).

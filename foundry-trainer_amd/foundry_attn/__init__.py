@@ -5,9 +5,10 @@ ops.py.  Importing this package loads nothing; the first op call loads the
 library and fails loudly if it is missing.
 """
 from ._abi import FoundryAttnError, LIB_PATH, lib
-from .ops import (AttnBwd, attention, attn_bwd, attn_fwd, lora_bwd, lora_down, lora_fwd, lora_grad, lora_up,
+from .ops import (AttnBwd, attention, attn_bwd, attn_fwd, attn_workspace_bytes, lora_bwd, lora_down, lora_fwd,
+                  lora_grad, lora_up,
                   qk_prologue, qk_prologue_bwd, rope_tables)
 
-__all__ = ["AttnBwd", "attention", "attn_fwd", "attn_bwd", "qk_prologue", "qk_prologue_bwd",
+__all__ = ["AttnBwd", "attention", "attn_fwd", "attn_bwd", "attn_workspace_bytes", "qk_prologue", "qk_prologue_bwd",
            "rope_tables", "lora_fwd", "lora_bwd", "lora_down", "lora_up", "lora_grad", "FoundryAttnError",
            "LIB_PATH", "lib"]

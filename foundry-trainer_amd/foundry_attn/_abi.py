@@ -21,7 +21,8 @@ FA_MAX_ROPE_AXES = 8
 
 EXPORTED = [
     "fa_version", "fa_last_error", "fa_op_name", "fa_init",
-    "fa_attn_fwd", "fa_attn_bwd_workspace_size", "fa_attn_bwd", "fa_attn_bwd_phase",
+    "fa_attn_fwd", "fa_attn_fwd_workspace_size", "fa_attn_bwd_workspace_size", "fa_attn_bwd",
+    "fa_attn_bwd_phase",
     "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
     # include/foundry_block.h
@@ -50,6 +51,7 @@ class AttnFwdArgs(ctypes.Structure):
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
         ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p), ("key_keep", ctypes.c_void_p),
         ("q_stride", Strides), ("k_stride", Strides), ("v_stride", Strides), ("o_stride", Strides),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -201,6 +203,8 @@ def lib() -> ctypes.CDLL:
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
     L.fa_attn_bwd_phase.restype = ctypes.c_int
     L.fa_attn_bwd_phase.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_int32, ctypes.c_void_p]
+    L.fa_attn_fwd_workspace_size.restype = ctypes.c_size_t
+    L.fa_attn_fwd_workspace_size.argtypes = [ctypes.POINTER(AttnFwdArgs)]
     L.fa_attn_bwd_workspace_size.restype = ctypes.c_size_t
     L.fa_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnBwdArgs)]
     L.fa_lora_bwd_workspace_size.restype = ctypes.c_size_t

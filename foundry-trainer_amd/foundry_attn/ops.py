@@ -69,12 +69,17 @@ def _keep(key_keep: Optional[torch.Tensor], B: int, S: int, dev) -> Optional[tor
     return kk
 
 
-def attn_fwd(q, k, v, scale: Optional[float] = None, key_keep=None, out=None, lse=None):
+def attn_fwd(q, k, v, scale: Optional[float] = None, key_keep=None, out=None, lse=None,
+             workspace: Optional[torch.Tensor] = None, split: bool = True):
     """O, LSE of softmax(q k^T * scale) v via fa_attn_fwd.
 
     q, k, v: (B,S,H,D) or (S,H,D) device tensors, bf16 or f32.  scale defaults
     to 1/sqrt(D) (the reference hard-codes 1/sqrt(128), lib.rs:138).
     key_keep: optional (B,S) bool/uint8 mask, False = key excluded.
+    split: pass a workspace so that a grid too small for the GPU (few heads,
+    fa_attn_fwd_workspace_size > 0) splits each tile's keys; `workspace` is
+    used when large enough, else one is allocated.  split=False runs the
+    unsplit kernel.
     Returns o (same shape as q) and lse (B,H,S) float32.
     """
     squeeze = q.dim() == 3
@@ -97,8 +102,27 @@ def attn_fwd(q, k, v, scale: Optional[float] = None, key_keep=None, out=None, ls
                          q=_ptr(q4), k=_ptr(k4), v=_ptr(v4), o=_ptr(o4), lse=_ptr(lse_t),
                          key_keep=_ptr(kk), q_stride=_strides(q4), k_stride=_strides(k4),
                          v_stride=_strides(v4), o_stride=_strides(o4))
+    need = lib().fa_attn_fwd_workspace_size(ctypes.byref(a)) if split else 0
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q4.device)
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
     check(lib().fa_attn_fwd(ctypes.byref(a), _stream(q4)))
     return (o4[0] if squeeze else o4), lse_t
+
+
+def attn_workspace_bytes(q) -> Tuple[int, int]:
+    """(forward, backward) workspace bytes the library asks for q's shape
+    (B,S,H,D) or (S,H,D) and dtype on its device: the forward's is 0 unless
+    the shape splits (fa_attn_fwd_workspace_size)."""
+    q4 = _as4(q, "q")
+    B, S, H, D = q4.shape
+    with torch.cuda.device(q4.device):
+        fa = _abi.AttnFwdArgs(dtype=_dtype_code(q4), batch=B, seq=S, heads=H, head_dim=D)
+        ba = _abi.AttnBwdArgs(dtype=_dtype_code(q4), batch=B, seq=S, heads=H, head_dim=D)
+        return (int(lib().fa_attn_fwd_workspace_size(ctypes.byref(fa))),
+                int(lib().fa_attn_bwd_workspace_size(ctypes.byref(ba))))
 
 
 def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None,
@@ -138,6 +162,11 @@ def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None
                          dq_stride=_strides(dq), dk_stride=_strides(dk), dv_stride=_strides(dv))
     need = lib().fa_attn_bwd_workspace_size(ctypes.byref(a))
     if workspace is None or workspace.numel() * workspace.element_size() < need:
+        if workspace is not None and phases is not None:
+            # separate phase calls share the pre-pass rows through it
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
+                                   f"workspace of {workspace.numel() * workspace.element_size()} bytes is "
+                                   f"smaller than the {need} these shapes need")
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q4.device)
     a.workspace = workspace.data_ptr()
     a.workspace_bytes = workspace.numel() * workspace.element_size()

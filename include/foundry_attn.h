@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 typedef enum fa_status {
     FA_OK = 0,
@@ -93,13 +93,29 @@ typedef struct fa_attn_fwd_args {
     const uint8_t *key_keep; /* NULL (no mask) or [B,S] contiguous: 0 = key is
                                 excluded from every row's softmax                 */
     fa_strides q_stride, k_stride, v_stride, o_stride;
+    void *workspace;         /* NULL, or device scratch (256-B aligned) of at
+                                least fa_attn_fwd_workspace_size bytes: lets a
+                                small bf16 grid split each tile's keys         */
+    size_t workspace_bytes;
 } fa_attn_fwd_args;
+
+/* Bytes of workspace a split forward needs for these shapes: nonzero for bf16
+ * when B x H x ceil(S/256) workgroups would leave at least half of the
+ * current device's CUs idle and S >= 1024 (for example 3 or 6 heads at
+ * S = 4608: one GPU's share of 24 heads over 8 or 4 GPUs).  Each query tile's
+ * keys are then cut into up to 16 ranges of >= 512 keys on separate
+ * workgroups, whose f32 partials are merged through their LSEs.  0 means
+ * the forward never splits these shapes.  No reference counterpart. */
+size_t fa_attn_fwd_workspace_size(const fa_attn_fwd_args *args);
 
 /* O = softmax(Q K^T * scale) V per (b, h), scores and softmax in f32, P cast to
  * the storage dtype before P V (lib.rs:131-149), plus the per-row LSE that the
  * backward uses to recompute P.  A fully masked row gives O = 0, LSE = -inf.
- * Replaces AttnBwd::cuda_fwd (lib.rs:189-214) and AttnBwd::cpu_fwd
- * (lib.rs:158-187). */
+ * With workspace NULL the call never splits; with a workspace of at least
+ * fa_attn_fwd_workspace_size bytes it splits the shapes that size covers (a
+ * smaller non-NULL workspace is FA_ERR_INVALID_ARG).  Results are
+ * deterministic either way.  Replaces AttnBwd::cuda_fwd (lib.rs:189-214) and
+ * AttnBwd::cpu_fwd (lib.rs:158-187). */
 fa_status fa_attn_fwd(const fa_attn_fwd_args *args, void *stream);
 
 typedef struct fa_attn_bwd_args {
@@ -117,17 +133,23 @@ typedef struct fa_attn_bwd_args {
     fa_strides dq_stride, dk_stride, dv_stride;
 } fa_attn_bwd_args;
 
-/* Bytes of workspace fa_attn_bwd needs for these shapes (0 on bad args). */
+/* Bytes of workspace fa_attn_bwd needs for these shapes (0 on bad args): the
+ * pre-pass rows, plus, for the shapes fa_attn_fwd_workspace_size splits, f32
+ * partial sums of dQ, dK and dV (dQ's key range and dK/dV's query range are
+ * split the same way, and a reduce pass adds the partials in a fixed order). */
 size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
 
 /* dQ, dK, dV of the forward above: P is recomputed from Q, K and the saved
  * LSE; dS = P * (dP - rowsum(dO * O)) * scale; dQ = dS K, dK = dS^T Q,
  * dV = P^T dO, f32 accumulation, deterministic (no atomics).  For bf16 with
- * seq < 512 the dQ kernel runs on a library-owned side stream (one per host
- * thread and device, default priority) beside dK/dV, joined back to `stream`
- * by events before the call returns; longer sequences run in order on
- * `stream` (dQ, which also forms the pre-pass for its queries, then dK/dV).  Either way everything queued on `stream` afterwards
- * sees the results.  Replaces AttnBwd::bwd (lib.rs:216-263). */
+ * 4-wave (128-row) workgroups -- seq < 512, or an 8-wave grid whose last
+ * round would be under half full -- the dQ kernel runs on a library-owned
+ * side stream (one per host thread and device, default priority) beside
+ * dK/dV, joined back to `stream` by events before the call returns.  With
+ * 8-wave workgroups the launches run in order on `stream`: dQ (which also
+ * forms the pre-pass for its queries), then dK/dV; a split call adds one
+ * reduce of the partials.  Either way everything queued on `stream`
+ * afterwards sees the results.  Replaces AttnBwd::bwd (lib.rs:216-263). */
 fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
 
 /* The backward in its three launches, for callers that time them or run the

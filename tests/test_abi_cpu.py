@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_name():
-    assert lib().fa_version() == 1
+    assert lib().fa_version() == 2
     # CustomOp3::name of the reference op (lib.rs:154-156)
     assert lib().fa_op_name() == b"foundry-attn-bwd"
 

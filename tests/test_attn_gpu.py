@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle
-from foundry_attn import attention, attn_bwd, attn_fwd, AttnBwd
+from foundry_attn import attention, attn_bwd, attn_fwd, attn_workspace_bytes, AttnBwd
 from foundry_attn.configs import C1, C2, C3, C5
 from helpers import (BF16_MAX_ABS, BF16_REL_L2, F32_REL_L2, attn_inputs, load_golden, max_abs,
                      rel_l2)
@@ -328,13 +328,15 @@ def test_custom_op_host_tensors_take_the_cpu_fwd_route(dtype):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("B,S,H,D", [(2, 700, 3, 128), (1, 1100, 44, 128), (1, 1100, 44, 64)],
-                         ids=["4wave", "8wave", "8wave_d64"])
+@pytest.mark.parametrize("B,S,H,D", [(2, 700, 3, 128), (1, 1100, 44, 128), (1, 1100, 44, 64),
+                                     (1, 2048, 2, 128), (1, 1400, 2, 64)],
+                         ids=["4wave", "8wave", "8wave_d64", "split", "split_d64"])
 def test_backward_phases_match_single_call(B, S, H, D):
     """fa_attn_bwd_phase: pre-pass, dK/dV and dQ issued separately (one
     stream, then dK/dV and dQ on two streams) give the one-call bits.  With
     8-wave kernels the one call is two launches (dQ doing the pre-pass for
-    its own queries, then dK/dV), whose row sums follow the pre-pass's order."""
+    its own queries, then dK/dV), whose row sums follow the pre-pass's order;
+    a split call adds the reduce, and its phases reduce their own partials."""
     from foundry_attn import _abi
     torch.manual_seed(3)
     q, k, v, do = (torch.randn(B, S, H, D, device="cuda").to(torch.bfloat16) for _ in range(4))
@@ -347,7 +349,7 @@ def test_backward_phases_match_single_call(B, S, H, D):
                            (_abi.FA_BWD_DQ, None)])
     cur = torch.cuda.current_stream()
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()  # default priority
-    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    ws = torch.empty(attn_workspace_bytes(q)[1], dtype=torch.uint8, device="cuda")
     out = tuple(torch.empty_like(q) for _ in range(3))
     attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=ws, out=out,
              phases=[(_abi.FA_BWD_PREPASS, None)])
@@ -364,13 +366,14 @@ def test_backward_phases_match_single_call(B, S, H, D):
         assert torch.equal(a, b) and torch.equal(a, c)
 
 
-@pytest.mark.parametrize("S,H", [(1100, 4), (1100, 44)], ids=["forked", "in_order"])
+@pytest.mark.parametrize("S,H", [(700, 4), (1100, 44), (1100, 4)], ids=["forked", "in_order", "split"])
 def test_one_call_backward_is_ordered_on_the_caller_stream(S, H):
-    """fa_attn_bwd runs dQ on a library side stream and joins it back (H = 4:
-    20 workgroups, the 4-wave kernels) or runs the three phases in order
-    (H = 44: 220 workgroups, 8-wave): either way, work queued on the caller's
-    stream right after the call (a copy of dq, and a second call reusing the
-    same workspace with other inputs) sees finished results."""
+    """fa_attn_bwd runs dQ on a library side stream and joins it back (S =
+    700, H = 4: the 4-wave kernels), runs its launches in order (H = 44: 220
+    workgroups, 8-wave), or splits and reduces in order (S = 1100, H = 4: 20
+    8-wave workgroups): either way, work queued on the caller's stream right
+    after the call (a copy of dq, and a second call reusing the same
+    workspace with other inputs) sees finished results."""
     torch.manual_seed(5)
     mk = lambda: torch.randn(1, S, H, 128, device="cuda").to(torch.bfloat16)
     q1, k1, v1, do1, q2, k2, v2, do2 = (mk() for _ in range(8))
@@ -379,7 +382,7 @@ def test_one_call_backward_is_ordered_on_the_caller_stream(S, H):
     ref1 = attn_bwd(q1, k1, v1, o1, do1, l1)
     ref2 = attn_bwd(q2, k2, v2, o2, do2, l2)
     torch.cuda.synchronize()
-    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    ws = torch.empty(attn_workspace_bytes(q1)[1], dtype=torch.uint8, device="cuda")
     out1 = tuple(torch.empty_like(q1) for _ in range(3))
     out2 = tuple(torch.empty_like(q1) for _ in range(3))
     s = torch.cuda.Stream()  # default priority
