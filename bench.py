@@ -17,6 +17,9 @@ Prints ONE JSON line.  Besides the contract fields it carries:
                 materialised f32 scores, 5-GEMM backward) timed on this host
                 on a bounded sample of the same workload
   kernels       per-kernel times and rates
+  ulysses_shards  fwd+bwd at one GPU's share of the heads (H/2, H/4, H/8) at
+                the full sequence, the per-GPU attention of 2-, 4- and 8-way
+                sequence parallelism
 """
 from __future__ import annotations
 
@@ -151,6 +154,43 @@ def memory_bound_bench(torch, fa, cfg):
         out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
                      "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
     out["shapes"] = (f"prologue: B={B} S={S} H={H} D={D} bf16; lora: N={N} C={C} r={r} bf16")
+    return out
+
+
+def shard_bench(torch, fa, cfg):
+    """Attention fwd+bwd at one GPU's share of cfg's heads under P-way
+    sequence (Ulysses) parallelism, P = 2, 4, 8: the same kernels at
+    H = heads / P and the full sequence (what one GPU runs between the two
+    all-to-alls).  Small grids take the range-split kernels; `split` is the
+    number of key/query ranges per tile (1 = unsplit)."""
+    import dataclasses
+    out = {}
+    for p in (2, 4, 8):
+        if cfg.heads % p:
+            continue
+        c = dataclasses.replace(cfg, heads=cfg.heads // p)
+        q, k, v, do, keep = make_inputs(c, torch, fa)
+        o = torch.empty_like(q)
+        lse = torch.empty((c.batch, c.heads, c.seq), dtype=torch.float32, device="cuda")
+        fws, bws = fa.attn_workspace_bytes(q)
+        wf = torch.empty(max(fws, 256), dtype=torch.uint8, device="cuda")
+        wb = torch.empty(bws, dtype=torch.uint8, device="cuda")
+        grads = tuple(torch.empty_like(q) for _ in range(3))
+        fwd = lambda: fa.attn_fwd(q, k, v, c.scale, keep, out=o, lse=lse, workspace=wf)
+        bwd = lambda: fa.attn_bwd(q, k, v, o, do, lse, c.scale, keep, workspace=wb, out=grads)
+        for _ in range(20):
+            fwd()
+            bwd()
+        f_ms, b_ms = _event_ms(torch, fwd), _event_ms(torch, bwd)
+        tf = lambda fl, ms: round(fl / (ms * 1e-3) / 1e12, 2)
+        out[f"{p}_gpus"] = {
+            # the forward workspace holds split x (O rows in f32 + their LSEs)
+            "heads": c.heads, "split": round(fws / (c.batch * c.heads * c.seq * (c.head_dim + 1) * 4)) or 1,
+            "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+            "fwd_tflops": tf(c.fwd_flops(), f_ms), "bwd_tflops": tf(c.bwd_flops(), b_ms),
+            "tflops": tf(c.fwd_flops() + c.bwd_flops(), f_ms + b_ms),
+            "pct_of_peak": round(100 * tf(c.fwd_flops() + c.bwd_flops(), f_ms + b_ms) / PEAK_BF16_TFLOPS, 2)}
+        del q, k, v, do, o, lse, wf, wb, grads
     return out
 
 
@@ -407,6 +447,7 @@ def main():
                      "traffic": TRAFFIC.get((cfg.name, dominant))},
         "kernels": kernels,
         "memory_bound": memory_bound_bench(torch, fa, cfg),
+        "ulysses_shards": shard_bench(torch, fa, cfg),
     }
     if args.block_steps > 0:
         rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
