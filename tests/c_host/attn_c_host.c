@@ -140,6 +140,17 @@ static void run_case(const char *name, int dtype, int B, int S, int H, int D, in
     fa.lse = dlse;
     fa.key_keep = dkeep;
     fa.q_stride = fa.k_stride = fa.v_stride = fa.o_stride = st;
+    /* a grid too small for the GPU splits its keys when given the workspace
+       the library asks for (0 = these shapes never split) */
+    const size_t fws = fa_attn_fwd_workspace_size(&fa);
+    if (fws > 0) {
+        printf("  split forward: %zu workspace bytes\n", fws);
+        HIP_OK(hipMalloc(&fa.workspace, fws));
+        fa.workspace_bytes = fws - 256;
+        expect(fa_attn_fwd(&fa, NULL) == FA_ERR_INVALID_ARG && fa_last_error()[0] != 0,
+               "a forward workspace 256 bytes short is refused with a message");
+        fa.workspace_bytes = fws;
+    }
     expect(fa_attn_fwd(&fa, NULL) == FA_OK, "fa_attn_fwd returns FA_OK");
 
     fa_attn_bwd_args ba;
@@ -215,6 +226,7 @@ static void run_case(const char *name, int dtype, int B, int S, int H, int D, in
     for (int t = 0; t < 8; ++t) HIP_OK(hipFree(dev[t]));
     HIP_OK(hipFree(dlse));
     HIP_OK(hipFree(ba.workspace));
+    if (fa.workspace) HIP_OK(hipFree(fa.workspace));
     if (dkeep) HIP_OK(hipFree(dkeep));
     for (int t = 0; t < 4; ++t) {
         free(host[t]);
@@ -249,6 +261,7 @@ int main(void) {
     run_case("bf16, D=64", FA_DTYPE_BF16, 1, 200, 2, 64, 0, 0, 2);
     run_case("f32, config c1 shape", FA_DTYPE_F32, 1, 256, 4, 64, 0, 0, 4);
     run_case("bf16, 8-wave workgroups", FA_DTYPE_BF16, 1, 1400, 40, 128, 0, 38, 40);
+    run_case("bf16, range split (few heads), masked", FA_DTYPE_BF16, 1, 2048, 2, 128, 1, 0, 2);
 
     printf("%s (%d failure%s)\n", failures ? "FAILED" : "PASSED", failures, failures == 1 ? "" : "s");
     return failures ? 1 : 0;

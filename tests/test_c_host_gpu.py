@@ -2,7 +2,8 @@
 __graft_entry__.build()) allocates device buffers with the HIP runtime, runs
 fa_attn_fwd / fa_attn_bwd through include/foundry_attn.h alone, and checks
 the results against the C oracle at the parity gates (bf16 ragged + masked,
-D = 64, the f32 c1 shape, an 8-wave shape) plus the ABI's error reporting.
+D = 64, the f32 c1 shape, an 8-wave shape, a masked range-split shape with
+its forward workspace) plus the ABI's error reporting.
 It runs as a child process of this test."""
 import os
 import subprocess
