@@ -461,12 +461,15 @@ hipError_t expand(const float *U, int64_t ldu, const T *Wt, T *Y, int64_t ldy, i
     return hipGetLastError();
 }
 
-// Token splits of the bf16 colsum: enough workgroups to fill the GPU, each
-// split a multiple of 64 tokens.
+// Token splits of the bf16 colsum: about 256 workgroups (one per CU), each
+// split a multiple of 64 tokens.  At the c4 shapes (N = 4096, C = 3072: 24
+// column tiles) that is 11 splits of 384 tokens; targeting 512 workgroups
+// (shorter splits, twice the partials) measured ~1% slower over the whole
+// double-block step, 1024 slower still.
 inline int colsum_splits(int N, int C) {
     const int tiles = (C + kCsCols - 1) / kCsCols;
     const int stages = (N + kCsRows - 1) / kCsRows;
-    int sp = (512 + tiles - 1) / tiles;
+    int sp = (256 + tiles - 1) / tiles;
     if (sp > stages) sp = stages;
     return sp < 1 ? 1 : sp;
 }
