@@ -254,22 +254,39 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams p) {
 //   p' = p - ((m' * ibc1) / (sqrt(v' * ibc2) + eps)) * lr
 // each product / sum rounded separately (contraction off for the
 // expressions written here), IEEE sqrt and division, p' rounded to T.
+template <typename T, typename H>
+__device__ __forceinline__ void adamw_elem(T *w, const float *grad, float *mm, float *vv, int64_t i, const H &h) {
+#pragma clang fp contract(off)
+    const float g = grad[i];
+    const float m = mm[i] * h.b1 + g * h.one_m_b1;
+    const float gg = g * g;
+    const float v = vv[i] * h.b2 + gg * h.one_m_b2;
+    const float mhat = m * h.ibc1;
+    const float den = sqrtf(v * h.ibc2) + h.eps;
+    const float delta = (mhat / den) * h.lr;
+    w[i] = (T)((float)w[i] - delta);
+    mm[i] = m;
+    vv[i] = v;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void adamw_kernel(AdamwParams p) {
-#pragma clang fp contract(off)
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < p.n; i += (int64_t)gridDim.x * 256) {
-        const float g = p.grad[i];
-        const float m = p.m[i] * p.b1 + g * p.one_m_b1;
-        const float gg = g * g;
-        const float v = p.v[i] * p.b2 + gg * p.one_m_b2;
-        const float mhat = m * p.ibc1;
-        const float den = sqrtf(v * p.ibc2) + p.eps;
-        const float delta = (mhat / den) * p.lr;
-        T *w = static_cast<T *>(p.param);
-        w[i] = (T)((float)w[i] - delta);
-        p.m[i] = m;
-        p.v[i] = v;
-    }
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < p.n; i += (int64_t)gridDim.x * 256)
+        adamw_elem(static_cast<T *>(p.param), p.grad, p.m, p.v, i, p);
+}
+
+// Several tensors of one AdamW step in one launch: tensor k owns blocks
+// [block0[k], block0[k + 1]) and strides over its elements with them.  Same
+// per-element arithmetic as adamw_kernel, so the same bits.
+template <typename T>
+__global__ __launch_bounds__(256) void adamw_many_kernel(AdamwMany p) {
+    const int b = blockIdx.x;
+    int k = 0;
+    while (k + 1 < p.count && p.block0[k + 1] <= b) ++k;
+    const int nb = p.block0[k + 1] - p.block0[k];
+    T *w = static_cast<T *>(p.param[k]);
+    for (int64_t i = (int64_t)(b - p.block0[k]) * 256 + threadIdx.x; i < p.n[k]; i += (int64_t)nb * 256)
+        adamw_elem(w, p.grad[k], p.m[k], p.v[k], i, p);
 }
 
 inline int elt_grid(int64_t n8) {
@@ -331,6 +348,22 @@ static hipError_t swiglu_t(const SwigluParams &p, bool bwd, hipStream_t s) {
 }
 hipError_t launch_swiglu(const SwigluParams &p, bool bwd, int dtype, hipStream_t s) {
     return dtype == 0 ? swiglu_t<bf16>(p, bwd, s) : swiglu_t<float>(p, bwd, s);
+}
+
+hipError_t launch_adamw_many(AdamwMany p, int dtype, hipStream_t s) {
+    int blocks = 0;
+    for (int k = 0; k < p.count; ++k) {
+        p.block0[k] = blocks;
+        const int64_t nb = (p.n[k] + 255) / 256;
+        blocks += (int)(nb < 1024 ? nb : 1024);
+    }
+    p.block0[p.count] = blocks;
+    const dim3 grid(blocks), block(256);
+    if (dtype == 0)
+        hipLaunchKernelGGL((adamw_many_kernel<bf16>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((adamw_many_kernel<float>), grid, block, 0, s, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_adamw(const AdamwParams &p, int dtype, hipStream_t s) {

@@ -800,7 +800,10 @@ fa_status fa_swiglu_bwd(const fa_swiglu_bwd_args *a, void *stream) {
     return ok();
 }
 
-fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
+}  // extern "C"
+
+namespace {
+fa_status check_adamw(const fa_adamw_args *a) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
     if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)
         return fail(FA_ERR_INVALID_ARG, "unknown dtype %d", a->dtype);
@@ -812,13 +815,13 @@ fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
     if (!(a->lr >= 0.0) || !(a->beta1 >= 0.0 && a->beta1 < 1.0) || !(a->beta2 >= 0.0 && a->beta2 < 1.0) ||
         !(a->eps > 0.0))
         return fail(FA_ERR_INVALID_ARG, "need lr >= 0, 0 <= beta < 1, eps > 0");
-    FA_TRY(init_current());
-    fa::AdamwParams p{};
-    p.param = a->param;
-    p.grad = a->grad;
-    p.m = a->m;
-    p.v = a->v;
-    p.n = a->n;
+    return FA_OK;
+}
+
+// The step's f32 scalars, formed as the reference does (1 - beta and the
+// bias corrections in f64, then rounded).
+template <typename P>
+void adamw_scalars(const fa_adamw_args *a, P &p) {
     const double b1 = a->beta1, b2 = a->beta2;
     p.lr = (float)a->lr;
     p.b1 = (float)b1;
@@ -828,8 +831,51 @@ fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
     p.eps = (float)a->eps;
     p.ibc1 = (float)(1.0 / (1.0 - pow(b1, a->step)));
     p.ibc2 = (float)(1.0 / (1.0 - pow(b2, a->step)));
+}
+}  // namespace
+
+extern "C" {
+
+fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
+    FA_TRY(check_adamw(a));
+    FA_TRY(init_current());
+    fa::AdamwParams p{};
+    p.param = a->param;
+    p.grad = a->grad;
+    p.m = a->m;
+    p.v = a->v;
+    p.n = a->n;
+    adamw_scalars(a, p);
     const hipError_t e = fa::launch_adamw(p, a->dtype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "adamw launch");
+    return ok();
+}
+
+fa_status fa_adamw_step_many(const fa_adamw_args *args, int32_t count, void *stream) {
+    if (!args || count < 1) return fail(FA_ERR_INVALID_ARG, "args is NULL or count < 1");
+    for (int32_t i = 0; i < count; ++i) {
+        FA_TRY(check_adamw(&args[i]));
+        const fa_adamw_args &a = args[i], &z = args[0];
+        if (a.dtype != z.dtype || a.lr != z.lr || a.beta1 != z.beta1 || a.beta2 != z.beta2 || a.eps != z.eps ||
+            a.step != z.step)
+            return fail(FA_ERR_INVALID_ARG, "tensor %d: dtype, lr, betas, eps and step must match tensor 0", i);
+    }
+    FA_TRY(init_current());
+    for (int32_t k0 = 0; k0 < count; k0 += fa::kAdamwMany) {
+        fa::AdamwMany p{};
+        p.count = count - k0 < fa::kAdamwMany ? count - k0 : fa::kAdamwMany;
+        for (int k = 0; k < p.count; ++k) {
+            const fa_adamw_args &a = args[k0 + k];
+            p.param[k] = a.param;
+            p.grad[k] = a.grad;
+            p.m[k] = a.m;
+            p.v[k] = a.v;
+            p.n[k] = a.n;
+        }
+        adamw_scalars(&args[0], p);
+        const hipError_t e = fa::launch_adamw_many(p, args[0].dtype, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail(e, "adamw launch");
+    }
     return ok();
 }
 

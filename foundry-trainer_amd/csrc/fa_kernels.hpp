@@ -175,4 +175,18 @@ struct AdamwParams {
 };
 hipError_t launch_adamw(const AdamwParams &p, int dtype, hipStream_t s);
 
+// Up to kAdamwMany tensors of one step (shared hyperparameters); block0 is
+// filled by the launcher.
+constexpr int kAdamwMany = 32;
+struct AdamwMany {
+    void *param[kAdamwMany];
+    const float *grad[kAdamwMany];
+    float *m[kAdamwMany], *v[kAdamwMany];
+    int64_t n[kAdamwMany];
+    int block0[kAdamwMany + 1];
+    int count;
+    float lr, b1, b2, one_m_b1, one_m_b2, eps, ibc1, ibc2;
+};
+hipError_t launch_adamw_many(AdamwMany p, int dtype, hipStream_t s);
+
 }  // namespace fa

@@ -27,7 +27,7 @@ EXPORTED = [
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
     # include/foundry_block.h
     "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
-    "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step",
+    "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step", "fa_adamw_step_many",
     "fa_lora_down", "fa_lora_up", "fa_lora_grad", "fa_lora_grad_workspace_size",
 ]
 
@@ -201,6 +201,8 @@ def lib() -> ctypes.CDLL:
         fn = getattr(L, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+    L.fa_adamw_step_many.restype = ctypes.c_int
+    L.fa_adamw_step_many.argtypes = [ctypes.POINTER(AdamwArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_attn_bwd_phase.restype = ctypes.c_int
     L.fa_attn_bwd_phase.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_attn_fwd_workspace_size.restype = ctypes.c_size_t

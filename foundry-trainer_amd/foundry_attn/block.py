@@ -179,6 +179,27 @@ def adamw_step(param, grad, m, v, step: int, lr: float = 1e-3, betas=(0.9, 0.999
     check(lib().fa_adamw_step(ctypes.byref(a), _stream(param)))
 
 
+def adamw_step_many(items, step: int, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8):
+    """adamw_step over several (param, grad, m, v) of one step in one call
+    (fa_adamw_step_many: up to 32 tensors per launch, the bits of separate
+    adamw_step calls).  The params share a dtype and a device."""
+    items = list(items)
+    if not items:
+        return
+    arr = (_abi.AdamwArgs * len(items))()
+    for i, (param, grad, m, v) in enumerate(items):
+        n = param.numel()
+        for name, t in (("grad", grad), ("m", m), ("v", v)):
+            if t.numel() != n or t.dtype != torch.float32 or not t.is_contiguous() or t.device != param.device:
+                raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be contiguous float32 like param")
+        if not param.is_contiguous() or param.device != items[0][0].device:
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "params must be contiguous on one device")
+        arr[i] = _abi.AdamwArgs(dtype=_dtype_code(param), n=n, param=_ptr(param), grad=_ptr(grad), m=_ptr(m),
+                                v=_ptr(v), lr=float(lr), beta1=float(betas[0]), beta2=float(betas[1]),
+                                eps=float(eps), step=int(step))
+    check(lib().fa_adamw_step_many(arr, len(items), _stream(items[0][0])))
+
+
 # ---------------------------------------------------------------------------
 # the block
 # ---------------------------------------------------------------------------
@@ -479,14 +500,18 @@ class DoubleBlockLoRA:
         return y, grads
 
     def apply_adamw(self, grads, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8) -> None:
+        """One AdamW step of every LoRA factor (adamw_step, lib.rs:477-510),
+        all factors in one fa_adamw_step_many call."""
         self.step_count += 1
+        items = []
         for (name, t), g in grads.items():
             if t == "x":
                 continue
             da, db = g
             w = self.w[name]
-            adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
-            adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
+            items.append((w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"]))
+            items.append((w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"]))
+        adamw_step_many(items, self.step_count, lr, betas, eps)
         self.refresh_adapters()
 
     def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = False):
@@ -753,10 +778,12 @@ class SingleBlockLoRA:
     def apply_adamw(self, grads, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8) -> None:
         self.step_count += 1
         w = self.w
+        items = []
         for t in SINGLE_LORA_TARGETS:
             da, db = grads[t]
-            adamw_step(w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"], self.step_count, lr, betas, eps)
-            adamw_step(w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"], self.step_count, lr, betas, eps)
+            items.append((w.lora_a[t], da, w.m[f"{t}.a"], w.v[f"{t}.a"]))
+            items.append((w.lora_b[t], db, w.m[f"{t}.b"], w.v[f"{t}.b"]))
+        adamw_step_many(items, self.step_count, lr, betas, eps)
         self.refresh_adapters()
 
     def train_step(self, x, dy, lr: float = 1e-3, want_dx: bool = True):

@@ -14,7 +14,7 @@
  *                    single block throughput.rs:620)
  *                                        fa_swiglu_fwd / fa_swiglu_bwd
  *   modulation input silu(temb)  throughput.rs:297-324     fa_silu
- *   adamw_step       lib.rs:477-510      fa_adamw_step
+ *   adamw_step       lib.rs:477-510      fa_adamw_step, fa_adamw_step_many
  *
  * Row views: `rows` x `cols` elements, row r starting at base + r * ld
  * elements; cols % 8 == 0, ld >= cols, and base and ld keep every row
@@ -143,6 +143,14 @@ typedef struct fa_adamw_args {
  * p' = p - ((m'/bc1) / (sqrt(v'/bc2) + eps)) * lr, every f32 product or sum
  * rounded separately. */
 fa_status fa_adamw_step(const fa_adamw_args *args, void *stream);
+
+/* fa_adamw_step over `count` tensors of one optimiser step (one adapter
+ * stack's LoRA factors) in as few launches as possible (up to 32 tensors
+ * each): every tensor gets the same bits as its own fa_adamw_step call.
+ * dtype, lr, betas, eps and step must be equal across the array.  The
+ * reference steps each parameter in turn (lib.rs:477-510 inside the loop of
+ * throughput.rs:787-803). */
+fa_status fa_adamw_step_many(const fa_adamw_args *args, int32_t count, void *stream);
 
 #ifdef __cplusplus
 }

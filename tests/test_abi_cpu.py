@@ -230,6 +230,17 @@ def test_block_ops_validate_before_device_work():
         bad = _abi.AdamwArgs.from_buffer_copy(ad)
         setattr(bad, field, val)
         assert L.fa_adamw_step(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+    # several tensors of one step: the hyperparameters and dtype must agree
+    arr = (_abi.AdamwArgs * 3)(ad, ad, ad)
+    if not gpu_available():
+        assert L.fa_adamw_step_many(arr, 3, None) == ok_dev
+    assert L.fa_adamw_step_many(arr, 0, None) == _abi.FA_ERR_INVALID_ARG
+    assert L.fa_adamw_step_many(None, 3, None) == _abi.FA_ERR_INVALID_ARG
+    for field, val in (("step", 2), ("lr", 2e-3), ("beta2", 0.99), ("eps", 1e-6), ("dtype", 1), ("n", 0)):
+        bad = (_abi.AdamwArgs * 3)(ad, ad, ad)
+        setattr(bad[2], field, val)
+        assert L.fa_adamw_step_many(bad, 3, None) == _abi.FA_ERR_INVALID_ARG, field
+        assert b"tensor 2" in L.fa_last_error() or field == "n", field
 
 
 

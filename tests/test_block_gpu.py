@@ -125,6 +125,28 @@ def test_adamw_matches_oracle_over_steps(dtype):
         np.testing.assert_allclose(host(tp), p, rtol=1e-6, atol=1e-9)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_adamw_many_matches_separate_steps(dtype):
+    """fa_adamw_step_many over 40 tensors (two launches of up to 32; sizes
+    from 7 elements to more than 1024 x 256, which strides) gives the bits of
+    40 separate fa_adamw_step calls, over two steps."""
+    torch.manual_seed(9)
+    sizes = [7, 256, 257, 49152, 300000] + [1000 + 97 * i for i in range(35)]
+    mk = lambda n: (torch.randn(n, device="cuda").to(dtype), torch.randn(n, device="cuda"),
+                    torch.zeros(n, device="cuda"), torch.zeros(n, device="cuda"))
+    many = [mk(n) for n in sizes]
+    one = [tuple(t.clone() for t in item) for item in many]
+    for step in (1, 2):
+        grads = [torch.randn(n, device="cuda") for n in sizes]
+        fb.adamw_step_many([(p, g, m, v) for (p, _, m, v), g in zip(many, grads)], step, lr=3e-3)
+        for (p, _, m, v), g in zip(one, grads):
+            fb.adamw_step(p, g, m, v, step, lr=3e-3)
+    torch.cuda.synchronize()
+    for a, b in zip(many, one):
+        for x, y in zip(a[::2] + a[3:], b[::2] + b[3:]):
+            assert torch.equal(x, y)
+
+
 def device_block(case, dtype):
     ws = {}
     for name in ("txt", "img"):
