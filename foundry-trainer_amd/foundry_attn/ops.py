@@ -55,6 +55,15 @@ def _strides(t: torch.Tensor) -> _abi.Strides:
 
 
 def _stream(t: torch.Tensor) -> int:
+    """torch's current stream on t's device, which must be the current
+    device: the library launches on the current HIP device (and sizes split
+    workspaces for it), so a tensor elsewhere is refused rather than read
+    from the wrong GPU."""
+    cur = torch.cuda.current_device()
+    if t.device.index != cur:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
+                               f"{t.device} is not the current device cuda:{cur}; the library launches on the "
+                               f"current device: call inside `with torch.cuda.device({t.device})`")
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
