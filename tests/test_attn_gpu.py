@@ -399,29 +399,32 @@ def test_one_call_backward_is_ordered_on_the_caller_stream(S, H):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("H", [3, 40], ids=["forked", "in_order"])
-def test_backward_from_two_host_threads(H):
+@pytest.mark.parametrize("S,H", [(900, 3), (900, 40), (2048, 2)], ids=["forked", "in_order", "split"])
+def test_backward_from_two_host_threads(S, H):
     """Each host thread gets its own side stream and events (H = 3 forks dQ;
-    H = 40, 160 workgroups of the 8-wave kernels, runs in order): two threads
-    calling fa_attn_bwd at once give the single-threaded bits."""
+    H = 40, 160 workgroups of the 8-wave kernels, runs in order; S = 2048,
+    H = 2 splits, each call with its own workspace): two threads calling
+    fa_attn_fwd / fa_attn_bwd at once give the single-threaded bits."""
     import threading
     torch.manual_seed(6)
     cases = []
     for _ in range(2):
-        q, k, v, do = (torch.randn(1, 900, H, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
+        q, k, v, do = (torch.randn(1, S, H, 128, device="cuda").to(torch.bfloat16) for _ in range(4))
         o, lse = attn_fwd(q, k, v)
         cases.append((q, k, v, o, do, lse))
-    refs = [attn_bwd(*c) for c in cases]
+    refs = [(c[3], c[5]) + tuple(attn_bwd(*c)) for c in cases]
     torch.cuda.synchronize()
     results, errors = {}, []
 
     def work(i):
         try:
+            q, k, v, _, do, _ = cases[i]
             st = torch.cuda.Stream()
             st.wait_stream(torch.cuda.default_stream())
             with torch.cuda.stream(st):
                 for _ in range(3):
-                    r = attn_bwd(*cases[i])
+                    o, lse = attn_fwd(q, k, v)
+                    r = (o, lse) + tuple(attn_bwd(q, k, v, o, do, lse))
             st.synchronize()
             results[i] = r
         except Exception as e:  # surfaced below
