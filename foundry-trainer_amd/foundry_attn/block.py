@@ -278,37 +278,46 @@ class DoubleBlockLoRA:
         self._batched = batch_qkv_adapters and self.dtype == torch.bfloat16 and 3 * self.rank <= 64
         if self._batched:
             r = self.rank
-            self._a_qkv, self._a_qkv_t, self._b_t = {}, {}, {}
+            self._a_qkv, self._a_qkv_t, self._b_qkv, self._b_qkv_t, self._b_t = {}, {}, {}, {}, {}
             for name in STREAMS:
                 w = weights[name]
+                # A_q|A_k|A_v as one [3r, C] tensor and B_q|B_k|B_v as one
+                # [3, C, r] tensor; lora_a[t] / lora_b[t] are views of them
+                # (AdamW updates the stacks in place)
                 a = torch.cat([w.lora_a[t] for t in QKV]).contiguous()
+                b = torch.stack([w.lora_b[t] for t in QKV]).contiguous()
                 for j, t in enumerate(QKV):
-                    w.lora_a[t] = a[j * r:(j + 1) * r]  # AdamW updates the stack in place
-                self._a_qkv[name] = a
+                    w.lora_a[t] = a[j * r:(j + 1) * r]
+                    w.lora_b[t] = b[j]
+                self._a_qkv[name], self._b_qkv[name] = a, b
                 self._a_qkv_t[name] = torch.empty((a.shape[1], 3 * r), dtype=a.dtype, device=a.device)
-                self._b_t[name] = {t: torch.empty((r, w.lora_b[t].shape[0]), dtype=a.dtype, device=a.device)
-                                   for t in QKV}
+                bt = torch.empty((3, r, b.shape[1]), dtype=a.dtype, device=a.device)
+                self._b_qkv_t[name] = bt
+                self._b_t[name] = {t: bt[j] for j, t in enumerate(QKV)}
             self.refresh_adapters()
 
     def refresh_adapters(self) -> None:
         """Re-derive what the batched adapter products read from the LoRA
-        factors: the stacked A_qkv, A_qkv^T (for dh += s t A_qkv) and B_j^T
-        (for t_j = dy_j B_j).  apply_adamw calls it; call it after changing
-        lora_a / lora_b any other way (loading a LoRA file: a tensor assigned
-        to lora_a[t] is copied into the stack and replaced by its view)."""
+        factors: the stacked A_qkv and B_qkv, A_qkv^T (for dh += s t A_qkv)
+        and the B_j^T (for t_j = dy_j B_j), two copies per stream.
+        apply_adamw calls it; call it after changing lora_a / lora_b any other
+        way (loading a LoRA file: a tensor assigned to lora_a[t] or lora_b[t]
+        is copied into its stack and replaced by its view)."""
         if not self._batched:
             return
         r = self.rank
         for name in STREAMS:
-            w, a = self.w[name], self._a_qkv[name]
+            w, a, b = self.w[name], self._a_qkv[name], self._b_qkv[name]
             for j, t in enumerate(QKV):
                 view = a[j * r:(j + 1) * r]
                 if w.lora_a[t].data_ptr() != view.data_ptr():
                     view.copy_(w.lora_a[t])
                     w.lora_a[t] = view
+                if w.lora_b[t].data_ptr() != b[j].data_ptr():
+                    b[j].copy_(w.lora_b[t])
+                    w.lora_b[t] = b[j]
             self._a_qkv_t[name].copy_(a.t())
-            for t in QKV:
-                self._b_t[name][t].copy_(w.lora_b[t].t())
+            self._b_qkv_t[name].copy_(b.transpose(1, 2))
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
