@@ -160,3 +160,25 @@ def test_forward_workspace_too_small_is_refused():
     ref, _ = attn_fwd(q, k, v, split=False)
     torch.cuda.synchronize()
     assert torch.equal(o_null, ref)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5, 6])
+def test_split_random_shapes(seed):
+    """Seeded random split shapes (B 1-2, H 1-3, ragged S 1024-3000, D 64 or
+    128, half of them with a random key mask that keeps every batch item's
+    first key) against the oracle on one head."""
+    rng = np.random.default_rng(100 + seed)
+    B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+    S, D = int(rng.integers(1024, 3001)), int(rng.choice([64, 128]))
+    print(f"  B={B} S={S} H={H} D={D}", flush=True)
+    assert _splits(B, S, H, D)[0] > 0, "shape does not split"
+    from oracle import bf16_round
+    q, k, v, do = (bf16_round(rng.standard_normal((B, S, H, D), dtype=np.float32)) for _ in range(4))
+    keep = None
+    if seed % 2:
+        keep = (rng.random((B, S)) > 0.3).astype(np.uint8)
+        keep[:, 0] = 1
+    scale = 1.0 / np.sqrt(D)
+    g = run_gpu(q, k, v, do, torch.bfloat16, scale, keep)
+    h = int(rng.integers(0, H))
+    compare(g, q, k, v, do, scale, keep, True, (h, h + 1))
