@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 from typing import Optional, Sequence, Tuple
 
 import numpy as np
@@ -163,9 +164,13 @@ def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None
             if t.shape != q4.shape or t.dtype != q4.dtype or t.device != q4.device:
                 raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "out grads do not match q")
     kk = _keep(key_keep, B, S, q4.device)
+    # the launch reads lse asynchronously: a contiguous copy must stay alive
+    # (and out of the caching allocator) until it has been enqueued, or the
+    # workspace allocated below could reuse its block
+    lse_c = lse.contiguous()
     a = _abi.AttnBwdArgs(dtype=_dtype_code(q4), batch=B, seq=S, heads=H, head_dim=D, scale=scale,
                          q=_ptr(q4), k=_ptr(k4), v=_ptr(v4), o=_ptr(o4), dout=_ptr(do4),
-                         lse=_ptr(lse.contiguous()), key_keep=_ptr(kk), dq=_ptr(dq), dk=_ptr(dk),
+                         lse=_ptr(lse_c), key_keep=_ptr(kk), dq=_ptr(dq), dk=_ptr(dk),
                          dv=_ptr(dv), q_stride=_strides(q4), k_stride=_strides(k4),
                          v_stride=_strides(v4), o_stride=_strides(o4), do_stride=_strides(do4),
                          dq_stride=_strides(dq), dk_stride=_strides(dk), dv_stride=_strides(dv))
@@ -185,6 +190,7 @@ def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None
         for ph, st in phases:
             sp = _stream(q4) if st is None else st.cuda_stream
             check(lib().fa_attn_bwd_phase(ctypes.byref(a), int(ph), sp))
+    del lse_c, kk  # enqueued: the stream orders any reuse of their blocks
     if squeeze:
         return dq[0], dk[0], dv[0]
     return dq, dk, dv
@@ -196,24 +202,32 @@ class AttnBwd:
     `fwd` takes the place of `cuda_fwd` (lib.rs:189-214) and `cpu_fwd`
     (lib.rs:158-187); `bwd` keeps the reference signature
     (q, k, v, res, grad_res) -> (dq, dk, dv) (lib.rs:216-263).  The forward's
-    LSE is kept per output tensor so `bwd` can recompute P from it; if the
-    slot is missing (a `res` this instance did not produce) the forward is
-    rerun to regenerate it, as the reference's backward recomputes its
-    probabilities.
+    LSE is kept for the call that produced `res`: `bwd` reuses it only when
+    it is handed that very `res` object and the same q, k, v (same storage,
+    shape and strides), none of them modified since (tensor versions).
+    Otherwise the forward is rerun to regenerate it, as the reference's
+    backward recomputes its probabilities from q and k.  The slot is
+    released once a backward has used it.
 
     Host (CPU) tensors take the `cpu_fwd` route as the Rust shim does: they
-    are staged to the current GPU, the HIP kernels run there, and the results
-    come back as host tensors (no CPU computation path exists).
+    must be contiguous with storage offset 0, as `cpu_fwd` requires
+    (lib.rs:167-172); they are staged to the current GPU, the HIP kernels run
+    there, and the results come back as host tensors (no CPU computation
+    path exists).
     """
 
     def __init__(self, scale: Optional[float] = None, key_keep=None):
         self.scale = scale
         self.key_keep = key_keep
-        self._saved = None  # (data_ptr of res, version, lse on the device)
+        self._saved = None  # (weakref to res, identity keys of q, k, v, res, lse on the device)
 
     @staticmethod
     def name() -> str:
         return lib().fa_op_name().decode()
+
+    @staticmethod
+    def _key(t: torch.Tensor):
+        return (t.device, t.data_ptr(), tuple(t.shape), t.stride(), t._version)
 
     @staticmethod
     def _staged(*ts):
@@ -223,17 +237,31 @@ class AttnBwd:
     def fwd(self, q, k, v):
         host = not q.is_cuda
         if host:
+            for name, t in (("q", q), ("k", k), ("v", v)):
+                if t.is_cuda or not t.is_contiguous() or t.storage_offset() != 0:
+                    raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
+                                           f"cpu_fwd requires contiguous offset-0 host inputs ({name})")
+            keys = tuple(self._key(t) for t in (q, k, v))
             q, k, v = self._staged(q, k, v)
+        else:
+            keys = tuple(self._key(t) for t in (q, k, v))
         o, lse = attn_fwd(q, k, v, self.scale, self.key_keep)
         if host:
             o = o.cpu()
-        self._saved = (o.data_ptr(), o._version, lse)
+        self._saved = (weakref.ref(o), keys + (self._key(o),), lse)
         return o
 
+    def _saved_lse(self, q, k, v, res):
+        if self._saved is None:
+            return None
+        ref, keys, lse = self._saved
+        if ref() is not res or keys != tuple(self._key(t) for t in (q, k, v, res)):
+            return None
+        return lse
+
     def bwd(self, q, k, v, res, grad_res):
-        lse = None
-        if self._saved is not None and self._saved[0] == res.data_ptr() and self._saved[1] == res._version:
-            lse = self._saved[2]
+        lse = self._saved_lse(q, k, v, res)
+        self._saved = None
         host = not q.is_cuda
         if host:
             q, k, v, res, grad_res = self._staged(q, k, v, res, grad_res)
@@ -407,45 +435,81 @@ def lora_bwd(x, a, b, u, dy, scale: float, dx: Optional[torch.Tensor] = None):
 # ---------------------------------------------------------------------------
 # adapter pieces around a base GEMM that carries the adapter (bf16)
 # ---------------------------------------------------------------------------
-def _rank_view(t: torch.Tensor, N: int, r: int, name: str) -> torch.Tensor:
-    if t.shape != (N, r) or t.stride(1) != 1 or t.dtype != torch.bfloat16:
-        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be a bf16 [{N}, {r}] view with unit column stride")
+def _rank_view(t: torch.Tensor, N: int, r: int, name: str, dev) -> torch.Tensor:
+    if t.dim() != 2 or t.shape != (N, r) or t.stride(1) != 1 or t.dtype != torch.bfloat16 \
+            or t.device != dev:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
+                               f"{name} must be a bf16 [{N}, {r}] view with unit column stride on {dev}")
     return t
+
+
+def _rows(t: torch.Tensor, name: str, dtype=None, dev=None) -> torch.Tensor:
+    """A 2-D row view with unit column stride (the kernels read whole rows)."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be 2-D with unit column stride")
+    if (dtype is not None and t.dtype != dtype) or (dev is not None and t.device != dev):
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, f"{name} must be {dtype} on {dev}")
+    return t
+
+
+def _factor(t: torch.Tensor, shape, name: str, like: torch.Tensor) -> torch.Tensor:
+    if tuple(t.shape) != tuple(shape) or t.dtype != like.dtype or t.device != like.device:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
+                               f"{name} must be {like.dtype} {list(shape)} on {like.device}")
+    return t.contiguous()
 
 
 def lora_down(x, a, scale: float, out: torch.Tensor):
     """out = scale * x a^T, bf16, into a [N, r] view (e.g. the extra K-columns
-    of a GEMM operand)."""
+    of a GEMM operand).  x [N, K] bf16 rows, a [r, K]."""
+    x = _rows(x, "x", torch.bfloat16)
     N, K = x.shape
+    if a.dim() != 2:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "lora_a must be 2-D [r, K]")
     r = a.shape[0]
-    _rank_view(out, N, r, "out")
+    a_c = _factor(a, (r, K), "lora_a", x)
+    _rank_view(out, N, r, "out", x.device)
     args = _abi.LoraDownArgs(dtype=_dtype_code(x), tokens=N, in_features=K, rank=r, scale=float(scale),
-                             x=_ptr(x), ldx=x.stride(0), a=_ptr(a.contiguous()), u=_ptr(out), ldu=out.stride(0))
+                             x=_ptr(x), ldx=x.stride(0), a=_ptr(a_c), u=_ptr(out), ldu=out.stride(0))
     check(lib().fa_lora_down(ctypes.byref(args), _stream(x)))
     return out
 
 
 def lora_up(u, b, y, scale: float):
-    """y += scale * u b^T in place; u a bf16 [N, r] view, b [M, r]."""
+    """y += scale * u b^T in place; u a bf16 [N, r] view, b [M, r], y [N, M]
+    bf16 rows."""
+    y = _rows(y, "y", torch.bfloat16)
     N, M = y.shape
+    if b.dim() != 2:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "lora_b must be 2-D [M, r]")
     r = b.shape[1]
-    _rank_view(u, N, r, "u")
-    if y.stride(1) != 1:
-        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "y must have contiguous rows")
+    b_c = _factor(b, (M, r), "lora_b", y)
+    _rank_view(u, N, r, "u", y.device)
     args = _abi.LoraUpArgs(dtype=_dtype_code(y), tokens=N, out_features=M, rank=r, scale=float(scale),
-                           u=_ptr(u), ldu=u.stride(0), b=_ptr(b.contiguous()), y=_ptr(y), ldy=y.stride(0))
+                           u=_ptr(u), ldu=u.stride(0), b=_ptr(b_c), y=_ptr(y), ldy=y.stride(0))
     check(lib().fa_lora_up(ctypes.byref(args), _stream(y)))
     return y
 
 
 def lora_grad(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor] = None):
     """f32 scale * u^T x: [r, C] (lora_a layout) or, with transpose, [C, r]
-    (lora_b layout).  u a bf16 [N, r] view, x [N, C]."""
+    (lora_b layout).  u a bf16 [N, r] view, x [N, C] bf16 rows; `out`, when
+    given, a contiguous f32 tensor of that shape on x's device."""
+    x = _rows(x, "x", torch.bfloat16)
     N, C = x.shape
+    if u.dim() != 2:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "u must be 2-D [N, r]")
     r = u.shape[1]
-    _rank_view(u, N, r, "u")
+    _rank_view(u, N, r, "u", x.device)
     shape = (C, r) if transpose else (r, C)
-    g = torch.empty(shape, dtype=torch.float32, device=x.device) if out is None else out
+    if out is None:
+        g = torch.empty(shape, dtype=torch.float32, device=x.device)
+    else:
+        if tuple(out.shape) != shape or out.dtype != torch.float32 or not out.is_contiguous() \
+                or out.device != x.device:
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
+                                   f"out must be a contiguous float32 {list(shape)} tensor on {x.device}")
+        g = out
     args = _abi.LoraGradArgs(dtype=_dtype_code(x), tokens=N, features=C, rank=r, scale=float(scale), u=_ptr(u),
                              ldu=u.stride(0), x=_ptr(x), ldx=x.stride(0), grad=_ptr(g), transpose=int(transpose))
     need = lib().fa_lora_grad_workspace_size(ctypes.byref(args))
