@@ -299,6 +299,47 @@ def test_c4_block_step_properties():
         assert not torch.equal(b0, blk.w[k[0]].lora_b[k[1]]), k
 
 
+def test_c4_full_size_step_matches_oracle():
+    """Config c4 at full size (img 4096 = 64 x 64 + txt 512 tokens, dim 3072,
+    24 x 128 heads, MLP 4x, LoRA r16 alpha 16 on q/k/v/out of both streams,
+    A ~ N(0, 1/r^2), B ~ N(0, 1e-3^2)): one bf16 block step with the
+    block-input gradient against the composed CPU restatement (block_ref),
+    both block outputs, both dX and all 8 adapters' dA/dB at the block gate
+    (rel-L2 <= 2e-2, the reference's threshold), as the reference's block
+    test compares its gradients (block_backward.rs:34-136)."""
+    case = make_case(C=3072, H=24, T=512, rows=64, cols=64, r=16, alpha=16.0, bf16=True, seed=41)
+    for name in ("txt", "img"):
+        for t in fb.LORA_TARGETS:
+            b = case["W"][name]["lora_b"][t]
+            case["W"][name]["lora_b"][t] = oracle.bf16_round(b * (1e-3 / 0.02))
+    case = oracle_mods(case)
+    blk = device_block(case, torch.bfloat16)
+    x = {k: dev(v, torch.bfloat16) for k, v in case["x"].items()}
+    dy = {k: dev(v, torch.bfloat16) for k, v in case["dy"].items()}
+    y, grads = blk.forward_backward(x, dy, want_dx=True)
+    torch.cuda.synchronize()
+    y = {k: host(v) for k, v in y.items()}
+    grads = {k: (host(v) if k[1] == "x" else tuple(host(t) for t in v)) for k, v in grads.items()}
+    wy, wgrads, _ = block_ref.block_step(case["x"], case["dy"], case["W"], case["H"], case["D"], case["cos"],
+                                         case["sin"], case["axes"], case["scale"], bf16=True, want_dx=True)
+    gate = 2e-2
+    for name in ("txt", "img"):
+        for label, got, want in (("y", y[name], wy[name]), ("dx", grads[(name, "x")], wgrads[(name, "x")])):
+            r = rel_l2(got, want)
+            print(f"  {label}.{name}: rel_l2={r:.2e}", flush=True)
+            assert r <= gate, (label, name, r)
+    n_adapters = 0
+    for key, g in wgrads.items():
+        if key[1] == "x":
+            continue
+        (wa, wb), (da, db) = g, grads[key]
+        ra, rb = rel_l2(da, wa), rel_l2(db, wb)
+        print(f"  grad {key}: dA {ra:.2e} dB {rb:.2e}", flush=True)
+        assert ra <= gate and rb <= gate, key
+        n_adapters += 1
+    assert n_adapters == 8
+
+
 def device_single_block(case, dtype):
     W = case["W"]
     w = fb.SingleWeights(w_in=dev(W["w_in"], dtype), w_out=dev(W["w_out"], dtype), q_norm=dev(W["q_norm"], dtype),
