@@ -10,16 +10,26 @@ region; V, dO ~ N(0,1).  One step = attention forward (O + LSE) + backward
 
 value = 14*B*H*S^2*D / step time (forward 4*B*H*S^2*D, backward 2.5x that).
 
+Before the W warm-up steps the GPU runs the step untimed for --settle-s
+seconds (default 0.3): MI355X ramps its clocks over the first ~100 ms of
+work, and the driver's short warm-up would otherwise time part of that ramp.
+The timed region is exactly K steps either way.
+
 Prints ONE JSON line.  Besides the contract fields it carries:
   roofline      for the kernel with the largest share of the step time
                 (HIP events on the launch stream, averaged over the timed steps)
   cpu_baseline  the CPU oracle (restatement of the reference's Candle CPU path,
                 materialised f32 scores, 5-GEMM backward) timed on this host
-                on a bounded sample of the same workload
+                on a bounded sample of the same workload, with the host's
+                logical, physical and usable (affinity) core counts
   kernels       per-kernel times and rates
+  configs       the same measurement at c3 (B4 S1536) and c5 (B2 S6656,
+                key-padding mask): step, forward, backward and per-kernel rates
   ulysses_shards  fwd+bwd at one GPU's share of the heads (H/2, H/4, H/8) at
                 the full sequence, the per-GPU attention of 2-, 4- and 8-way
                 sequence parallelism
+--only-headline runs the c2 measurement alone (no other section), so that a
+profiler trace of the run holds only c2 attention dispatches.
 """
 from __future__ import annotations
 
@@ -37,14 +47,15 @@ METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block st
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per launch of a kernel: rocprofv3 FETCH_SIZE and WRITE_SIZE runs
-# of this script (--calib-copy-mib 256), scaled by what the same counters read
-# for that 256 MiB copy (2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE, KiB).  Kept in
-# profiles/attn_c2_pmc.md; None for a kernel or workload not measured.
+# of this script (--only-headline --calib-copy-mib 256), scaled by what the
+# same counters read for that 256 MiB copy (2.0 x FETCH_SIZE + 1.0 x
+# WRITE_SIZE, KiB).  Kept in profiles/attn_c2_pmc.md; None for a kernel or
+# workload not measured.
 TRAFFIC = {
-    ("c2", "attn_fwd"): int((2.0 * 50776.0 + 28711.8) * 1024),
-    ("c2", "attn_bwd_prepass"): int((2.0 * 29408.6 + 5760.5) * 1024),
-    ("c2", "attn_bwd_dkdv"): int((2.0 * 65622.5 + 56160.0) * 1024),
-    ("c2", "attn_bwd_dq"): int((2.0 * 65026.4 + 28366.4) * 1024),
+    ("c2", "attn_fwd"): int((2.0 * 50771.8 + 28748.9) * 1024),
+    ("c2", "attn_bwd_prepass"): int((2.0 * 29408.5 + 5760.5) * 1024),
+    ("c2", "attn_bwd_dkdv"): int((2.0 * 65710.3 + 56160.0) * 1024),
+    ("c2", "attn_bwd_dq"): int((2.0 * 65789.3 + 28364.9) * 1024),
 }
 
 
@@ -58,6 +69,10 @@ def parse():
                     help="bound on the CPU baseline sample (0 = skip)")
     ap.add_argument("--block-steps", type=int, default=10,
                     help="timed c4 LoRA block steps (0 = skip the block measurement)")
+    ap.add_argument("--settle-s", type=float, default=0.3,
+                    help="untimed seconds of steps before the warm-up steps (clock ramp)")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="measure the --config attention step only (for profiler runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to HBM bytes")
@@ -295,13 +310,41 @@ def stack_bench(torch, steps: int, warmup: int):
     return out
 
 
+def host_cores():
+    """(logical CPUs, physical cores, CPUs this process may run on, CPU model)
+    from os.cpu_count (nproc --all), /proc/cpuinfo's distinct (physical id,
+    core id) pairs (lscpu's core count) and the scheduler affinity."""
+    model, pairs, phys, core = "", set(), None, None
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and not model:
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif not key and phys is not None and core is not None:
+                pairs.add((phys, core))
+                phys = core = None
+        if phys is not None and core is not None:
+            pairs.add((phys, core))
+    except OSError:
+        pass
+    return os.cpu_count() or 0, len(pairs) or None, len(os.sched_getaffinity(0)), model
+
+
 def cpu_baseline(cfg, budget_s: float):
     """The oracle (port of the reference's Candle CPU path) on whole heads of
-    the same workload, f32 arithmetic on bf16-valued inputs, all host cores."""
+    the same workload, f32 arithmetic on bf16-valued inputs, one OpenMP thread
+    per CPU this process may use (the box's share of the host: its
+    scheduler affinity)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    threads = oracle.default_threads()
+    nproc, physical, affinity, cpu_model = host_cores()
+    threads = affinity
     rng = np.random.default_rng(0)
     B, S, D = 1, cfg.seq, cfg.head_dim
     mk = lambda: oracle.bf16_round(rng.standard_normal((B, S, 1, D)).astype(np.float32))
@@ -314,19 +357,115 @@ def cpu_baseline(cfg, budget_s: float):
         t += time.perf_counter() - t0
         heads += 1
     flops = 14.0 * S * S * D * heads
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"{heads} head(s) of {cfg.name} (S={S}, D={D}) fwd+bwd, oracle "
-                      f"(materialised f32 scores, 5-GEMM backward), {t:.1f} s on {cpu_model}",
-            "ms_per_head": round(1e3 * t / heads, 1)}
+                      f"(materialised f32 scores, 5-GEMM backward), {t:.1f} s on {cpu_model}, "
+                      f"{threads} OpenMP threads",
+            "ms_per_head": round(1e3 * t / heads, 1),
+            "host": {"nproc": nproc, "physical_cores": physical, "affinity_cpus": affinity,
+                     "threads_used": threads, "cpu_model": cpu_model}}
+
+
+def attention_bench(torch, fa, cfg, steps: int, warmup: int, settle_s: float):
+    """Time `steps` fwd+bwd steps of cfg through the ABI (after settle_s
+    seconds of untimed steps and `warmup` warm-up steps), then time each
+    launch with HIP events in a separate pass over the same number of steps.
+    Returns the step time (ms) and the per-kernel means (ms)."""
+    q, k, v, do, keep = make_inputs(cfg, torch, fa)
+    lse = torch.empty((cfg.batch, cfg.heads, cfg.seq), dtype=torch.float32, device="cuda")
+    o = torch.empty_like(q)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    grads = (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q))
+    ph = [(fa._abi.FA_BWD_PREPASS, None), (fa._abi.FA_BWD_DKDV, None), (fa._abi.FA_BWD_DQ, None)]
+
+    def step(ev=None):
+        """One fwd+bwd.  With `ev`, HIP events bracket each launch on the
+        launch stream (the ABI launches on torch's current stream)."""
+        if ev is None:
+            fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
+            fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws, out=grads)
+            return
+        ev[0].record(stream)
+        fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
+        ev[1].record(stream)
+        for i, p_ in enumerate(ph):
+            fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws, out=grads, phases=[p_])
+            ev[2 + i].record(stream)
+
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    names = ["attn_fwd", "attn_bwd_prepass", "attn_bwd_dkdv", "attn_bwd_dq"]
+    kms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / len(evs) for i, nm in enumerate(names)}
+    return 1e3 * wall / steps, kms, keep is not None
+
+
+def attention_record(cfg, ms: float, kms: dict) -> dict:
+    """Rates of one attention measurement: the fwd+bwd step, the forward and
+    the three backward launches (algorithmic FLOPs per launch: forward 2G,
+    dK/dV 4G -- the S recompute, dP, dV, dK --, dQ 1G; G = 2*B*H*S_q*S_kv*D)."""
+    B, H, S, D = cfg.batch, cfg.heads, cfg.seq, cfg.head_dim
+    unit = cfg.fwd_flops() / 2.0
+    kflops = {"attn_fwd": 2 * unit, "attn_bwd_dkdv": 4 * unit, "attn_bwd_dq": 1 * unit}
+    pre_bytes = 2 * B * S * H * D * 2 + 3 * B * H * S * 4  # read O, dO, LSE; write delta, lse2
+    tf = lambda fl, t: fl / (t * 1e-3) / 1e12
+    pct = lambda x: round(100 * x / PEAK_BF16_TFLOPS, 2)
+    kernels = {}
+    for nm, t in kms.items():
+        if nm in kflops:
+            kernels[nm] = {"ms": round(t, 4), "tflops": round(tf(kflops[nm], t), 2),
+                           "pct_of_peak": pct(tf(kflops[nm], t))}
+        else:
+            gbs = pre_bytes / (t * 1e-3) / 1e9
+            kernels[nm] = {"ms": round(t, 4), "gbs": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
+    bwd_ms = kms["attn_bwd_prepass"] + kms["attn_bwd_dkdv"] + kms["attn_bwd_dq"]
+    value = tf(cfg.fwd_flops() + cfg.bwd_flops(), ms)
+    dominant = max(kflops, key=lambda nm: kms[nm])
+    return {
+        "value": value, "ms": ms, "kernels": kernels, "dominant": dominant,
+        "dominant_tflops": tf(kflops[dominant], kms[dominant]),
+        "fwd": {"ms": round(kms["attn_fwd"], 4), "tflops": round(tf(cfg.fwd_flops(), kms["attn_fwd"]), 2),
+                "pct_of_peak": pct(tf(cfg.fwd_flops(), kms["attn_fwd"]))},
+        "bwd": {"ms": round(bwd_ms, 4), "tflops": round(tf(cfg.bwd_flops(), bwd_ms), 2),
+                "pct_of_peak": pct(tf(cfg.bwd_flops(), bwd_ms))},
+    }
+
+
+def configs_bench(torch, fa, steps: int, warmup: int, settle_s: float):
+    """c3 and c5 measured as the
+    headline is: step time over `steps` timed fwd+bwd steps, then per-launch
+    HIP events."""
+    from foundry_attn.configs import CONFIGS
+    out = {}
+    for name in ("c3", "c5"):
+        cfg = CONFIGS[name]
+        ms, kms, masked = attention_bench(torch, fa, cfg, steps, warmup, settle_s)
+        r = attention_record(cfg, ms, kms)
+        out[name] = {"workload": f"B={cfg.batch} H={cfg.heads} S={cfg.seq} ({cfg.txt_len} txt + "
+                                 f"{cfg.img_rows}x{cfg.img_cols} img) D={cfg.head_dim} bf16"
+                                 + (", key-padding mask (FLOPs count kept keys)" if masked else ""),
+                     "ms_per_step": round(ms, 4), "tflops": round(r["value"], 2),
+                     "pct_of_peak": round(100 * r["value"] / PEAK_BF16_TFLOPS, 2),
+                     "fwd": r["fwd"], "bwd": r["bwd"], "kernels": r["kernels"]}
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -348,76 +487,9 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    q, k, v, do, keep = make_inputs(cfg, torch, fa)
-    lse = torch.empty((cfg.batch, cfg.heads, cfg.seq), dtype=torch.float32, device="cuda")
-    o = torch.empty_like(q)
-    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream()
-
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(q)
-    dv = torch.empty_like(q)
-    grads = (dq, dk, dv)
-    ph = [(fa._abi.FA_BWD_PREPASS, None), (fa._abi.FA_BWD_DKDV, None), (fa._abi.FA_BWD_DQ, None)]
-
-    def step(ev=None):
-        """One fwd+bwd.  With `ev`, HIP events bracket each launch on the
-        launch stream (the ABI launches on torch's current stream)."""
-        if ev is None:
-            fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
-            fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws, out=grads)
-            return
-        ev[0].record(stream)
-        fa.attn_fwd(q, k, v, cfg.scale, keep, out=o, lse=lse)
-        ev[1].record(stream)
-        for i, p_ in enumerate(ph):
-            fa.attn_bwd(q, k, v, o, do, lse, cfg.scale, keep, workspace=ws, out=grads, phases=[p_])
-            ev[2 + i].record(stream)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = 1e3 * wall / args.steps
-
-    # per-kernel HIP-event timing in a separate pass over the same steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-    for e in evs:
-        step(e)
-    torch.cuda.synchronize()
-    names = ["attn_fwd", "attn_bwd_prepass", "attn_bwd_dkdv", "attn_bwd_dq"]
-    kms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / len(evs) for i, nm in enumerate(names)}
-
-    B, H, S, D = cfg.batch, cfg.heads, cfg.seq, cfg.head_dim
-    unit = cfg.fwd_flops() / 2.0  # one S x S x D GEMM (2*B*H*S_q*S_kv*D)
-    # algorithmic FLOPs per launch: fwd = QK^T + PV; dk/dv = S recompute, dP,
-    # dV, dK; dq = dQ only (its S/dP recompute is redundant work)
-    kflops = {"attn_fwd": 2 * unit, "attn_bwd_dkdv": 4 * unit, "attn_bwd_dq": 1 * unit}
-    # pre-pass bytes: read O and dO, read LSE, write delta and lse2
-    pre_bytes = 2 * B * S * H * D * 2 + 3 * B * H * S * 4
-    f_fwd = cfg.fwd_flops()
-    f_all = f_fwd + cfg.bwd_flops()
-    value = f_all / (ms * 1e-3) / 1e12
-    kernels = {}
-    for nm in names:
-        t = kms[nm]
-        if nm in kflops:
-            tf = kflops[nm] / (t * 1e-3) / 1e12
-            kernels[nm] = {"ms": round(t, 4), "tflops": round(tf, 2),
-                           "pct_of_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
-        else:
-            gbs = pre_bytes / (t * 1e-3) / 1e9
-            kernels[nm] = {"ms": round(t, 4), "gbs": round(gbs, 1),
-                           "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
-    dominant = max(kflops, key=lambda nm: kms[nm])
-    dom_tf = kflops[dominant] / (kms[dominant] * 1e-3) / 1e12
-    fwd_tf = f_fwd / (kms["attn_fwd"] * 1e-3) / 1e12
-    bwd_ms = kms["attn_bwd_prepass"] + kms["attn_bwd_dkdv"] + kms["attn_bwd_dq"]
-    bwd_tf = cfg.bwd_flops() / (bwd_ms * 1e-3) / 1e12
+    ms, kms, masked = attention_bench(torch, fa, cfg, args.steps, args.warmup, args.settle_s)
+    r = attention_record(cfg, ms, kms)
+    value, dominant, dom_tf = r["value"], r["dominant"], r["dominant_tflops"]
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -433,30 +505,28 @@ def main():
         "data": "synthetic (seeded N(0,1) Q/K/V/dO; Q/K RMSNormed + axial RoPE by the prologue kernel)",
         "config": {"workload": f"{cfg.name}: joint attention fwd+bwd, B={cfg.batch} H={cfg.heads} "
                                f"S={cfg.seq} ({cfg.txt_len} txt + {cfg.img_rows}x{cfg.img_cols} img) "
-                               f"D={cfg.head_dim} bf16" + (", key-padding mask" if keep is not None else ""),
+                               f"D={cfg.head_dim} bf16" + (", key-padding mask" if masked else ""),
                    "batch": cfg.batch, "heads": cfg.heads, "seq_len": cfg.seq,
                    "head_dim": cfg.head_dim, "parallelism": "single GPU"},
         "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
-        "fwd": {"ms": round(kms["attn_fwd"], 4), "tflops": round(fwd_tf, 2),
-                "pct_of_peak": round(100 * fwd_tf / PEAK_BF16_TFLOPS, 2)},
-        "bwd": {"ms": round(bwd_ms, 4), "tflops": round(bwd_tf, 2),
-                "pct_of_peak": round(100 * bwd_tf / PEAK_BF16_TFLOPS, 2)},
+        "fwd": r["fwd"],
+        "bwd": r["bwd"],
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": round(dom_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
                      "traffic": TRAFFIC.get((cfg.name, dominant))},
-        "kernels": kernels,
-        "memory_bound": memory_bound_bench(torch, fa, cfg),
-        "ulysses_shards": shard_bench(torch, fa, cfg),
+        "kernels": r["kernels"],
     }
-    if args.block_steps > 0:
-        rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
-        rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.warmup // 4))
-        rec["checkpointed_stack"] = stack_bench(torch, args.block_steps, max(2, args.warmup // 4))
-    if args.cpu_seconds > 0:
-        rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
-    else:
-        rec["cpu_baseline"] = None
+    if not args.only_headline:
+        rec["configs"] = configs_bench(torch, fa, args.steps, args.warmup, args.settle_s)
+        rec["memory_bound"] = memory_bound_bench(torch, fa, cfg)
+        rec["ulysses_shards"] = shard_bench(torch, fa, cfg)
+        if args.block_steps > 0:
+            rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
+            rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.warmup // 4))
+            rec["checkpointed_stack"] = stack_bench(torch, args.block_steps, max(2, args.warmup // 4))
+    rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds) if args.cpu_seconds > 0 and not args.only_headline \
+        else None
     print(json.dumps(rec), flush=True)
     return 0
 
