@@ -14,6 +14,14 @@
 #include "../../include/foundry_block.h"
 #include "fa_kernels.hpp"
 
+// Scratch of fa_attn_bwd_noalloc: the backward's delta and lse2 rows
+// ([B,H,S] f32 each, 256-byte aligned), FA_BWD_NOALLOC_MAX_ROWS rows apiece.
+// Every GPU holds its own copy for the life of the process, and every call on
+// one GPU shares it.  On the host `scratch` names a host-side stand-in, not
+// device memory: kernels and copies get the per-device address that
+// init_device looks up (g_scratch), never the array's name.
+static __device__ __align__(256) unsigned char scratch[FA_BWD_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -40,6 +48,11 @@ fa_status hip_fail(hipError_t e, const char *what) {
     return fail(FA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+constexpr int kNoallocScratchBytes = FA_BWD_NOALLOC_SCRATCH_BYTES;
+void *g_scratch[kMaxDevices];  // device address of `scratch` per device (under g_init_mu)
+
+bool aligned_ptr(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
 fa_status init_device(int device) {
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
@@ -57,6 +70,20 @@ fa_status init_device(int device) {
                         device, prop.gcnArchName);
     }
     if (g_dev_state[device] < 0) return fail(FA_ERR_LOAD_FAILED, "device %d is not gfx950", device);
+    if (!g_scratch[device]) {
+        // the symbol's address is per device: look it up with `device` current
+        int cur = 0;
+        hipError_t e = hipGetDevice(&cur);
+        if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+        if (cur != device && (e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        const hipError_t e2 = cur != device ? hipSetDevice(cur) : hipSuccess;
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (e2 != hipSuccess) return hip_fail(e2, "hipSetDevice (restore)");
+        if (!ptr || !aligned_ptr(ptr, 256)) return fail(FA_ERR_HIP, "no-allocation scratch is misaligned");
+        g_scratch[device] = ptr;
+    }
     if (!g_prepared) {
         hipError_t e = fa::prepare_attn_kernels();
         if (e != hipSuccess) return hip_fail(e, "kernel attribute setup");
@@ -74,7 +101,20 @@ fa_status init_current() {
     return init_device(dev);
 }
 
-bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+bool aligned(const void *p, size_t a) { return aligned_ptr(p, a); }
+
+// Device address of the no-allocation scratch on the current device (set up
+// by init_current, which the caller has run).
+fa_status scratch_for_current(char **out) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    if (dev < 0 || dev >= kMaxDevices || !g_scratch[dev])
+        return fail(FA_ERR_HIP, "no-allocation scratch of device %d is not set up", dev);
+    *out = static_cast<char *>(g_scratch[dev]);
+    return FA_OK;
+}
 
 const char *dtype_name(int32_t dt) { return dt == FA_DTYPE_BF16 ? "bf16" : "f32"; }
 
@@ -305,14 +345,10 @@ hipError_t launch_bwd_forked(const fa::AttnBwdParams &p, int D, hipStream_t s) {
     if (e == hipSuccess) e = hipStreamWaitEvent(s, f->done, 0);
     return e;
 }
-}  // namespace
 
-extern "C" {
 
-fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stream) {
-    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
-    if (phase < FA_BWD_ALL || phase > FA_BWD_DQ)
-        return fail(FA_ERR_INVALID_ARG, "unknown backward phase %d", phase);
+// Validates a backward call's shapes, views and LSE (not its workspace).
+fa_status check_bwd_args(const fa_attn_bwd_args *a) {
     FA_TRY(check_attn_shape(a->dtype, a->batch, a->seq, a->heads, a->head_dim, a->scale));
     FA_TRY(check_view("q", a->q, a->q_stride, a->dtype));
     FA_TRY(check_view("k", a->k, a->k_stride, a->dtype));
@@ -329,20 +365,18 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stre
         FA_TRY(check_buffer_view("v", a->v_stride, a->seq, a->head_dim));
         FA_TRY(check_buffer_view("dout", a->do_stride, a->seq, a->head_dim));
     }
-    const size_t need = bwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
-    if (!a->workspace || !aligned(a->workspace, 256))
-        return fail(FA_ERR_INVALID_ARG, "workspace is NULL or not 256-byte aligned");
-    if (a->workspace_bytes < need)
-        return fail(FA_ERR_INVALID_ARG, "workspace of %zu bytes is smaller than the %zu needed",
-                    a->workspace_bytes, need);
-    FA_TRY(init_current());
+    return FA_OK;
+}
 
-    fa::AttnBwdParams p{};
+// Kernel parameters of a validated backward call whose scratch starts at ws
+// (delta rows, lse2 rows, then, for split > 1, the three partial arrays).
+void fill_bwd_params(const fa_attn_bwd_args *a, char *ws, int split, fa::AttnBwdParams &p) {
+    p = fa::AttnBwdParams{};
+    const size_t rows = round256((size_t)a->batch * a->heads * a->seq * sizeof(float));
     p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
     p.keep = a->key_keep; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
-    p.delta = static_cast<float *>(a->workspace);
-    p.lse2 = reinterpret_cast<float *>(static_cast<char *>(a->workspace) +
-                                       round256((size_t)a->batch * a->heads * a->seq * sizeof(float)));
+    p.delta = reinterpret_cast<float *>(ws);
+    p.lse2 = reinterpret_cast<float *>(ws + rows);
     p.q_sb = a->q_stride.b; p.q_ss = a->q_stride.s; p.q_sh = a->q_stride.h;
     p.k_sb = a->k_stride.b; p.k_ss = a->k_stride.s; p.k_sh = a->k_stride.h;
     p.v_sb = a->v_stride.b; p.v_ss = a->v_stride.s; p.v_sh = a->v_stride.h;
@@ -354,20 +388,66 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stre
     p.B = a->batch; p.S = a->seq; p.H = a->heads;
     p.scale = a->scale;
     p.scale_log2 = a->scale * 1.4426950408889634f;
-    p.split = split_for(a->dtype, a->batch, a->seq, a->heads);
-    if (p.split > 1) {
-        const size_t rows = round256((size_t)a->batch * a->heads * a->seq * sizeof(float));
+    p.split = split;
+    if (split > 1) {
         const size_t part = round256(
-            fa::attn_split_elems(a->batch, a->heads, a->seq, a->head_dim, p.split) * sizeof(float));
-        char *base = static_cast<char *>(a->workspace) + 2 * rows;
+            fa::attn_split_elems(a->batch, a->heads, a->seq, a->head_dim, split) * sizeof(float));
+        char *base = ws + 2 * rows;
         p.part_dq = reinterpret_cast<float *>(base);
         p.part_dk = reinterpret_cast<float *>(base + part);
         p.part_dv = reinterpret_cast<float *>(base + 2 * part);
     }
+}
+}  // namespace
+
+extern "C" {
+
+fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (phase < FA_BWD_ALL || phase > FA_BWD_DQ)
+        return fail(FA_ERR_INVALID_ARG, "unknown backward phase %d", phase);
+    FA_TRY(check_bwd_args(a));
+    const size_t need = bwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+    if (!a->workspace || !aligned(a->workspace, 256))
+        return fail(FA_ERR_INVALID_ARG, "workspace is NULL or not 256-byte aligned");
+    if (a->workspace_bytes < need)
+        return fail(FA_ERR_INVALID_ARG, "workspace of %zu bytes is smaller than the %zu needed",
+                    a->workspace_bytes, need);
+    FA_TRY(init_current());
+
+    fa::AttnBwdParams p;
+    fill_bwd_params(a, static_cast<char *>(a->workspace), split_for(a->dtype, a->batch, a->seq, a->heads), p);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t e = a->dtype != FA_DTYPE_BF16 ? fa::launch_attn_bwd_f32(p, a->head_dim, phase, s)
                          : phase == FA_BWD_ALL     ? launch_bwd_forked(p, a->head_dim, s)
                                                    : fa::launch_attn_bwd_bf16(p, a->head_dim, phase, s);
+    if (e != hipSuccess) return hip_fail(e, "attention backward launch");
+    return ok();
+}
+
+fa_status fa_attn_bwd_noalloc(const fa_attn_bwd_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    FA_TRY(check_bwd_args(a));
+    if (a->workspace || a->workspace_bytes)
+        return fail(FA_ERR_INVALID_ARG,
+                    "fa_attn_bwd_noalloc takes no workspace (workspace must be NULL, workspace_bytes 0)");
+    const int64_t rows = (int64_t)a->batch * a->heads * a->seq;
+    if (rows > FA_BWD_NOALLOC_MAX_ROWS)
+        return fail(FA_ERR_INVALID_ARG,
+                    "batch*heads*seq = %lld exceeds the %d rows the no-allocation scratch holds (%d bytes "
+                    "per device); call fa_attn_bwd with a workspace",
+                    (long long)rows, FA_BWD_NOALLOC_MAX_ROWS, kNoallocScratchBytes);
+    FA_TRY(init_current());
+    char *ws = nullptr;
+    FA_TRY(scratch_for_current(&ws));
+
+    // never split (the split partials would not fit), every launch in order on
+    // the caller's stream (no side stream to create)
+    fa::AttnBwdParams p;
+    fill_bwd_params(a, ws, 1, p);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const hipError_t e = a->dtype != FA_DTYPE_BF16 ? fa::launch_attn_bwd_f32(p, a->head_dim, FA_BWD_ALL, s)
+                                                   : fa::launch_attn_bwd_bf16(p, a->head_dim, FA_BWD_ALL, s);
     if (e != hipSuccess) return hip_fail(e, "attention backward launch");
     return ok();
 }

@@ -22,7 +22,7 @@ FA_MAX_ROPE_AXES = 8
 EXPORTED = [
     "fa_version", "fa_last_error", "fa_op_name", "fa_init",
     "fa_attn_fwd", "fa_attn_fwd_workspace_size", "fa_attn_bwd_workspace_size", "fa_attn_bwd",
-    "fa_attn_bwd_phase",
+    "fa_attn_bwd_phase", "fa_attn_bwd_noalloc",
     "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
     # include/foundry_block.h
@@ -195,6 +195,7 @@ def lib() -> ctypes.CDLL:
     L.fa_init.restype = ctypes.c_int
     L.fa_init.argtypes = [ctypes.c_int]
     for name, st in (("fa_attn_fwd", AttnFwdArgs), ("fa_attn_bwd", AttnBwdArgs),
+                     ("fa_attn_bwd_noalloc", AttnBwdArgs),
                      ("fa_qk_prologue_fwd", QkPrologueArgs),
                      ("fa_qk_prologue_bwd", QkPrologueBwdArgs),
                      ("fa_lora_fwd", LoraArgs), ("fa_lora_bwd", LoraBwdArgs)):

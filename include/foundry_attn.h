@@ -168,6 +168,29 @@ typedef enum fa_bwd_phase {
 } fa_bwd_phase;
 fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *args, int32_t phase, void *stream);
 
+/* Largest B * heads * seq that fa_attn_bwd_noalloc accepts, and the scratch
+ * it holds per device for them (delta and LSE*log2(e) rows, f32 each). */
+#define FA_BWD_NOALLOC_MAX_ROWS (1 << 21)
+#define FA_BWD_NOALLOC_SCRATCH_BYTES (2 * FA_BWD_NOALLOC_MAX_ROWS * 4)
+
+/* fa_attn_bwd without a workspace and without any allocation: no counterpart
+ * in the reference.  It is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  `workspace` must be NULL and `workspace_bytes` 0; the scratch
+ * is a fixed array of FA_BWD_NOALLOC_SCRATCH_BYTES (16 MiB) in the library's
+ * device code, one per GPU, held until the process ends, so calls with
+ * B * heads * seq > FA_BWD_NOALLOC_MAX_ROWS fail with FA_ERR_INVALID_ARG.
+ * The call never splits key or query ranges (the split partials would not
+ * fit), runs every launch in order on `stream` (no side stream), and calls no
+ * allocating routine.  For shapes fa_attn_bwd does not split the results are
+ * bit-identical to fa_attn_bwd's; for shapes it splits they are the unsplit
+ * kernels' results (deterministic, within the same tolerance of the exact
+ * gradients).  All calls on one GPU share its scratch, and every call
+ * overwrites all the scratch rows it reads before reading them, so nothing
+ * carries over from an earlier call; calls that overlap on one GPU (two
+ * streams, or two host threads, at once) race on it. */
+fa_status fa_attn_bwd_noalloc(const fa_attn_bwd_args *args, void *stream);
+
 /* ------------------------------------------------------------------------- */
 /* QK prologue: RMSNorm -> axial RoPE -> joint buffer                        */
 /* ------------------------------------------------------------------------- */

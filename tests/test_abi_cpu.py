@@ -122,6 +122,31 @@ def test_bwd_workspace_size_and_validation():
     assert b"workspace" in lib().fa_last_error()
 
 
+def test_bwd_noalloc_validates_before_device_work():
+    """fa_attn_bwd_noalloc refuses a workspace and shapes past its fixed
+    scratch before touching the device; a valid call without a GPU reports
+    NO_DEVICE."""
+    fake = 1 << 20
+    st = _abi.Strides(128 * 256, 256, 128)
+    mk = lambda **kw: _abi.AttnBwdArgs(**{**dict(dtype=0, batch=2, seq=100, heads=3, head_dim=128, scale=0.1,
+                                                 q=fake, k=fake, v=fake, o=fake, dout=fake, lse=fake,
+                                                 dq=fake, dk=fake, dv=fake, q_stride=st, k_stride=st,
+                                                 v_stride=st, o_stride=st, do_stride=st, dq_stride=st,
+                                                 dk_stride=st, dv_stride=st), **kw})
+    assert lib().fa_attn_bwd_noalloc(None, None) == _abi.FA_ERR_INVALID_ARG
+    a = mk(workspace=fake, workspace_bytes=4096)
+    assert lib().fa_attn_bwd_noalloc(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
+    assert b"no workspace" in lib().fa_last_error()
+    # one row past the scratch: (2^21 + 1) rows as B=1, H=1, S=2^21+1 (f32 needs
+    # no 2 GiB buffer-view check)
+    a = mk(dtype=1, batch=1, heads=1, seq=(1 << 21) + 1)
+    assert lib().fa_attn_bwd_noalloc(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
+    assert b"2097152 rows" in lib().fa_last_error()
+    if not gpu_available():
+        a = mk(dtype=1, batch=1, heads=1, seq=1 << 21)
+        assert lib().fa_attn_bwd_noalloc(ctypes.byref(a), None) == _abi.FA_ERR_NO_DEVICE
+
+
 @pytest.mark.skipif(gpu_available(), reason="checks the GPU-less error path")
 def test_valid_call_without_device_reports_no_device():
     a = _fwd_args()
