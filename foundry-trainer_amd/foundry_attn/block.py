@@ -10,6 +10,12 @@ backward, adamw_step on the LoRA factors), with the c4 choices:
   - the upstream gradient is a given dY per stream (the seed trick,
     attn_backward.rs:220-222) instead of the MSE loss;
   - the frozen linears have no bias.
+The same class also replays the reference's own double block
+(crates/foundry-spike/src/lib.rs:301-392, the fixture block of
+tools/fixtures/gen_block.py:199-240): frozen linears with biases, a SwiGLU
+MLP (mlp="swiglu", lib.rs:293-297), LoRA on only some projections (the
+fixture adapts the image stream's to_q and to_v), one modulation linear
+shared by both streams, and the caller's RoPE positions.
 
 Compute path: the memory-bound ops (layer_norm_mod and its backward, gated
 residuals, GELU, the fused QK-RMSNorm + RoPE prologue, the LoRA adapters,
@@ -211,11 +217,17 @@ STREAMS = ("txt", "img")  # joint order: txt first (throughput.rs:545-547)
 @dataclass
 class StreamWeights:
     """Frozen weights of one stream (torch tensors, compute dtype) and its
-    LoRA factors with their AdamW moments."""
+    LoRA factors with their AdamW moments.
+
+    MLP: tanh-GELU (the block's mlp="gelu"): w1 [F, C], w2 [C, F];
+    SwiGLU (mlp="swiglu", lib.rs:293-297): w1 [2M, C] = gate rows then up
+    rows, w2 [C, M] = down.  Biases are optional (None: no bias, as klein's
+    linears; the reference fixture has one on every linear).  LoRA factors
+    exist only for the targets in lora_a / lora_b."""
     w_qkv: torch.Tensor   # [3C, C]: to_q, to_k, to_v stacked
     w_out: torch.Tensor   # [C, C]
-    w1: torch.Tensor      # [F, C]
-    w2: torch.Tensor      # [C, F]
+    w1: torch.Tensor      # [F, C] (gelu) or [2M, C] (swiglu: gate | up)
+    w2: torch.Tensor      # [C, F] (gelu) or [C, M] (swiglu: down)
     q_norm: torch.Tensor  # [D]
     k_norm: torch.Tensor  # [D]
     w_mod: torch.Tensor   # [6C, C]: shift1, scale1, gate1, shift2, scale2, gate2
@@ -224,6 +236,18 @@ class StreamWeights:
     m: Dict[str, torch.Tensor] = field(default_factory=dict)
     v: Dict[str, torch.Tensor] = field(default_factory=dict)
     mod: Tuple[torch.Tensor, ...] = ()
+    b_qkv: Optional[torch.Tensor] = None  # [3C]
+    b_out: Optional[torch.Tensor] = None  # [C]
+    b1: Optional[torch.Tensor] = None     # [F] or [2M]
+    b2: Optional[torch.Tensor] = None     # [C]
+    b_mod: Optional[torch.Tensor] = None  # [6C]
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor], out: torch.Tensor) -> torch.Tensor:
+    """out = x w^T (+ b): one library GEMM, the bias in its epilogue."""
+    if b is None:
+        return torch.mm(x, w.t(), out=out)
+    return torch.addmm(b, x, w.t(), out=out)
 
 
 class DoubleBlockLoRA:
@@ -247,8 +271,14 @@ class DoubleBlockLoRA:
     def __init__(self, weights: Dict[str, StreamWeights], heads: int, head_dim: int, txt_tokens: int,
                  img_rows: int, img_cols: int, axes: Sequence[int] = (16, 56, 56), theta: float = 1e4,
                  lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
-                 tuned_gemms: bool = True, batch_qkv_adapters: bool = True):
+                 tuned_gemms: bool = True, batch_qkv_adapters: bool = True, mlp: str = "gelu",
+                 positions: Optional[np.ndarray] = None):
+        """positions: [S, n_axes] RoPE position ids of the joint sequence (txt
+        rows first); None gives txt (l, 0, 0), img (0, r, c)."""
+        if mlp not in ("gelu", "swiglu"):
+            raise ValueError(f"mlp must be 'gelu' or 'swiglu', not {mlp!r}")
         self.w = weights
+        self.mlp = mlp
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
         self.T, self.I = txt_tokens, img_rows * img_cols
@@ -259,11 +289,19 @@ class DoubleBlockLoRA:
         self.attn_scale = 1.0 / math.sqrt(head_dim)
         ref = weights["img"].w_qkv
         self.dtype, self.device = ref.dtype, ref.device
-        pos = np.zeros((self.S, 3), np.float32)
-        pos[:self.T, 0] = np.arange(self.T)
-        rr, cc = np.meshgrid(np.arange(img_rows), np.arange(img_cols), indexing="ij")
-        pos[self.T:, 1] = rr.ravel()
-        pos[self.T:, 2] = cc.ravel()
+        # capture: None, or a dict the forward and backward fill with copies
+        # of their intermediates (for replaying a fixture's activations)
+        self.capture: Optional[Dict[str, torch.Tensor]] = None
+        if positions is None:
+            pos = np.zeros((self.S, 3), np.float32)
+            pos[:self.T, 0] = np.arange(self.T)
+            rr, cc = np.meshgrid(np.arange(img_rows), np.arange(img_cols), indexing="ij")
+            pos[self.T:, 1] = rr.ravel()
+            pos[self.T:, 2] = cc.ravel()
+        else:
+            pos = np.asarray(positions, np.float32)
+            if pos.shape != (self.S, len(self.axes)):
+                raise ValueError(f"positions must be [{self.S}, {len(self.axes)}], got {pos.shape}")
         cos, sin = rope_tables(pos, self.axes, theta, dtype=self.dtype, device=self.device)
         self.rope = {"txt": (cos[:self.T].contiguous(), sin[:self.T].contiguous()),
                      "img": (cos[self.T:].contiguous(), sin[self.T:].contiguous())}
@@ -274,8 +312,13 @@ class DoubleBlockLoRA:
         self._side = torch.cuda.Stream(device=self.device) if overlap_streams else None
         if tuned_gemms and self.dtype == torch.bfloat16:
             gemm_tuning.enable()
-        self.rank = int(weights["img"].lora_a["q"].shape[0])
-        self._batched = batch_qkv_adapters and self.dtype == torch.bfloat16 and 3 * self.rank <= 64
+        ranks = {int(a.shape[0]) for w in weights.values() for a in w.lora_a.values()}
+        if len(ranks) > 1:
+            raise ValueError(f"LoRA factors of one block share a rank, got {sorted(ranks)}")
+        self.rank = ranks.pop() if ranks else 0
+        full_qkv = all(t in weights[name].lora_a for name in STREAMS for t in QKV)
+        self._batched = (batch_qkv_adapters and full_qkv and self.dtype == torch.bfloat16
+                         and 3 * self.rank <= 64)
         if self._batched:
             r = self.rank
             self._a_qkv, self._a_qkv_t, self._b_qkv, self._b_qkv_t, self._b_t = {}, {}, {}, {}, {}
@@ -325,13 +368,16 @@ class DoubleBlockLoRA:
         sc = silu(c.reshape(1, -1))
         for name in STREAMS:
             w = self.w[name]
-            m = torch.mm(sc, w.w_mod.t()).reshape(-1)
-            w.mod = tuple(t.contiguous() for t in m.split(self.C))
+            m = torch.empty((1, w.w_mod.shape[0]), dtype=self.dtype, device=self.device)
+            _linear(sc, w.w_mod, w.b_mod, m)
+            w.mod = tuple(t.contiguous() for t in m.reshape(-1).split(self.C))
 
     def _buffers(self):
         if self._buf is None:
             C, S, H, D = self.C, self.S, self.H, self.D
-            F = self.w["img"].w1.shape[0]
+            F = self.w["img"].w1.shape[0]        # pre-activation width (gelu F, swiglu 2M)
+            FA = self.w["img"].w2.shape[1]       # activation width (gelu F, swiglu M)
+            R = max(3 * self.rank, 1)
             kw = dict(dtype=self.dtype, device=self.device)
             b = {"qkv": torch.empty((S, 3 * C), **kw), "dqkv": torch.empty((S, 3 * C), **kw),
                  "q": torch.empty((1, S, H, D), **kw), "k": torch.empty((1, S, H, D), **kw),
@@ -342,8 +388,8 @@ class DoubleBlockLoRA:
             for name in STREAMS:
                 n = self.rows[name]
                 for key, width in (("h", C), ("out", C), ("x1", C), ("h2", C), ("y", C), ("t1", C),
-                                   ("t2", C), ("dx1", C), ("dx", C), ("pre", F), ("act", F), ("dact", F),
-                                   ("mlp", C), ("su", 3 * self.rank), ("tq", 3 * self.rank)):
+                                   ("t2", C), ("dx1", C), ("dx", C), ("pre", F), ("act", FA), ("dact", FA),
+                                   ("dpre", F), ("mlp", C), ("su", R), ("tq", R)):
                     b[f"{key}.{name}"] = torch.empty((n, width), **kw)
             self._buf = b
         return self._buf
@@ -393,7 +439,7 @@ class DoubleBlockLoRA:
         h, mean1, rstd1 = ln_mod_fwd(x[name], w.mod[0], w.mod[1], self.eps, out=B[f"h.{name}"], stats=True)
         saved[(name, "ln1")] = (mean1, rstd1)
         rows = B["qkv"][off:off + n]
-        torch.mm(h, w.w_qkv.t(), out=rows)
+        _linear(h, w.w_qkv, w.b_qkv, rows)
         if self._batched:
             r = self.rank
             su = lora_down(h, self._a_qkv[name], s, out=B[f"su.{name}"])  # [n, 3r] = s h A_qkv^T
@@ -401,12 +447,17 @@ class DoubleBlockLoRA:
                 lora_up(su[:, j * r:(j + 1) * r], w.lora_b[t], rows[:, j * C:(j + 1) * C], 1.0)
         else:
             for j, t in enumerate(QKV):
-                saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
+                if t in w.lora_a:
+                    saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
         cos, sin = self.rope[name]
         qk_prologue(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, self.eps,
                     out=B["q"], seq_offset=off)
         qk_prologue(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, self.eps,
                     out=B["k"], seq_offset=off)
+        if self.capture is not None:
+            self.capture[f"{name}_norm1"] = h.clone()
+            self.capture[f"{name}.q"] = B["q"][0, off:off + n].clone()
+            self.capture[f"{name}.k"] = B["k"][0, off:off + n].clone()
 
     def _out_phase(self, name, x, dy, o_t, y, saved):
         """Out projection, gated residuals, MLP; with dy, the backward down to dO."""
@@ -414,27 +465,39 @@ class DoubleBlockLoRA:
         w, off, n = self.w[name], self.offset[name], self.rows[name]
         sh2, sc2, g1, g2 = w.mod[3], w.mod[4], w.mod[2], w.mod[5]
         a = o_t[0, off:off + n].reshape(n, C)
-        out = torch.mm(a, w.w_out.t(), out=B[f"out.{name}"])
-        u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s)
+        out = _linear(a, w.w_out, w.b_out, B[f"out.{name}"])
+        u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s) if "out" in w.lora_a else None
         x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
         h2, mean2, rstd2 = ln_mod_fwd(x1, sh2, sc2, self.eps, out=B[f"h2.{name}"], stats=True)
-        pre = torch.mm(h2, w.w1.t(), out=B[f"pre.{name}"])
-        act = gelu(pre, out=B[f"act.{name}"])
-        mlp = torch.mm(act, w.w2.t(), out=B[f"mlp.{name}"])
+        pre = _linear(h2, w.w1, w.b1, B[f"pre.{name}"])
+        M = w.w2.shape[1]
+        if self.mlp == "swiglu":
+            act = swiglu(pre[:, :M], pre[:, M:], out=B[f"act.{name}"])
+        else:
+            act = gelu(pre, out=B[f"act.{name}"])
+        mlp = _linear(act, w.w2, w.b2, B[f"mlp.{name}"])
         y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
+        if self.capture is not None:
+            self.capture[f"{name}_post_attn"] = x1.clone()
+            self.capture[f"{name}_out"] = y[name].clone()
         if dy is None:
             return
         # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
         dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
         dact = torch.mm(dmlp, w.w2, out=B[f"dact.{name}"])
-        gelu_bwd(dact, pre, out=dact)
-        dh2 = torch.mm(dact, w.w1, out=B[f"t2.{name}"])
+        if self.mlp == "swiglu":
+            dpre = B[f"dpre.{name}"]
+            swiglu_bwd(dact, pre[:, :M], pre[:, M:], dgate=dpre[:, :M], dup=dpre[:, M:])
+        else:
+            dpre = gelu_bwd(dact, pre, out=dact)
+        dh2 = torch.mm(dpre, w.w1, out=B[f"t2.{name}"])
         dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
         dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
         do_rows = B["do"][0, off:off + n].reshape(n, C)
         torch.mm(dout, w.w_out, out=do_rows)
-        saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
-                                                dx=do_rows)
+        if u_out is not None:
+            saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
+                                                    dx=do_rows)
 
     def _qkv_bwd_phase(self, name, x, want_dx, saved, grads):
         """Prologue backward, the three adapters' gradients, and the input gradient."""
@@ -461,9 +524,11 @@ class DoubleBlockLoRA:
                 grads[(name, t)] = (da[j * r:(j + 1) * r], db)
         else:
             for j, t in enumerate(QKV):
-                grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
-                                            drows[:, j * C:(j + 1) * C], s, dx=dh)
-        grads[(name, "out")] = saved[(name, "out", "grad")]
+                if t in w.lora_a:
+                    grads[(name, t)] = lora_bwd(h, w.lora_a[t], w.lora_b[t], saved[(name, t)],
+                                                drows[:, j * C:(j + 1) * C], s, dx=dh)
+        if (name, "out", "grad") in saved:
+            grads[(name, "out")] = saved[(name, "out", "grad")]
         if want_dx:
             mean1, rstd1 = saved[(name, "ln1")]
             grads[(name, "x")] = ln_mod_bwd(x[name], dh, w.mod[1], mean1, rstd1, self.eps,
@@ -485,6 +550,9 @@ class DoubleBlockLoRA:
         else:
             o_t, lse_t = attention
         kept = (o_t.clone(), lse_t.clone()) if keep_attention else None
+        if self.capture is not None:
+            self.capture["attn_in.q"], self.capture["attn_in.k"] = B["q"][0].clone(), B["k"][0].clone()
+            self.capture["attn_in.v"], self.capture["attn"] = v[0].clone(), o_t[0].clone()
         self._fork()
         for name in STREAMS:
             with self._on(name):
@@ -495,6 +563,10 @@ class DoubleBlockLoRA:
         dv = B["dqkv"][:, 2 * C:].view(1, S, H, D)
         attn_bwd(B["q"], B["k"], v, o_t, B["do"], lse_t, self.attn_scale, None, workspace=B["ws"],
                  out=(B["dq"], B["dk"], dv))
+        if self.capture is not None:
+            for key, t in (("grad_attn.out", B["do"]), ("grad_attn.q", B["dq"]), ("grad_attn.k", B["dk"]),
+                           ("grad_attn.v", dv)):
+                self.capture[key] = t[0].clone()
         self._fork()
         for name in STREAMS:
             with self._on(name):

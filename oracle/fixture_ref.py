@@ -66,7 +66,8 @@ def _ln_bwd_drop_proj(x, dy, scale, mean, rstd, dres):
 def pipeline(f, bf16=False, mutate=None):
     """f: name -> float32 array (fixture weights and inputs, bf16-valued for
     bf16).  Returns (acts, grads): acts has the fixture's activation names,
-    grads has grad/inputs/{img,txt} and grad/<lora linear>.lora_{a,b}."""
+    grads has grad/inputs/{img,txt}, grad/<lora linear>.lora_{a,b} and the
+    double block's output gradients grad/double.{txt,img}_out."""
     C, H, D = DIM, HEADS, HEAD_DIM
     r = lambda a: _r(a, bf16)
     W = lambda name: f[f"weights/{name}.weight"]
@@ -194,6 +195,9 @@ def pipeline(f, bf16=False, mutate=None):
 
     # ---- double block backward
     dx2 = {"txt": np.ascontiguousarray(djoint[:TXT]), "img": np.ascontiguousarray(djoint[TXT:])}
+    # the gradient at the double block's outputs (not a fixture tensor: it
+    # lets a block be checked on its own from here down)
+    grads["grad/double.txt_out"], grads["grad/double.img_out"] = dx2["txt"], dx2["img"]
     dx1, dO = {}, []
     for name in ("txt", "img"):
         s = sv[name]
