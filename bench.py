@@ -133,23 +133,25 @@ def _event_ms(torch, fn, n: int = 20) -> float:
 def memory_bound_bench(torch, fa, cfg):
     """Achieved HBM rates of the memory-bound kernels around the attention,
     from algorithmic bytes (each tensor read or written once) over HIP-event
-    time: the QK-RMSNorm + RoPE prologue at the attention config's Q shape
-    (forward reads x, writes the joint buffer; backward reads x and dy,
-    writes dx; both read the per-token cos/sin rows and the weight) and the
-    LoRA down / up pieces at the c4 img stream's shape (x [4096, 3072],
-    r = 16: down reads x and A, writes u; up reads u and B and updates y in
-    place)."""
+    time: the QK-RMSNorm + RoPE prologue of Q and K at the attention config's
+    shape in one fused launch, as the blocks run it (forward reads x, writes
+    the joint buffer; backward reads x and dy, writes dx; both read the
+    per-token cos/sin rows and the weights), and the LoRA down / up pieces at
+    the c4 img stream's shape (x [4096, 3072], r = 16: down reads x and A,
+    writes u; up reads u and B and updates y in place)."""
     from foundry_attn.configs import C4
     g = torch.Generator(device="cuda").manual_seed(7)
     bf = torch.bfloat16
     B, S, H, D = cfg.batch, cfg.seq, cfg.heads, cfg.head_dim
-    x = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
-    dy = torch.randn((B, S, H, D), device="cuda", generator=g).to(bf)
-    w = (1 + 0.02 * torch.randn(D, device="cuda", generator=g)).to(bf)
+    xs = [torch.randn((B, S, H, D), device="cuda", generator=g).to(bf) for _ in range(2)]
+    dys = [torch.randn((B, S, H, D), device="cuda", generator=g).to(bf) for _ in range(2)]
+    ws = [(1 + 0.02 * torch.randn(D, device="cuda", generator=g)).to(bf) for _ in range(2)]
     cos, sin = fa.rope_tables(cfg.positions(), cfg.axes, cfg.theta, dtype=bf)
-    y, dx = torch.empty_like(x), torch.empty_like(x)
+    ys, dxs = [torch.empty_like(x) for x in xs], [torch.empty_like(x) for x in xs]
+    fwd_segs = [(xs[i], ws[i], cos, sin, cfg.axes, ys[i], 0) for i in range(2)]
+    bwd_segs = [(xs[i], ws[i], cos, sin, cfg.axes, dys[i], 0, dxs[i]) for i in range(2)]
     row = B * S * H * D * 2
-    tables = 2 * S * D * 2 + D * 2
+    tables = 2 * (2 * S * D * 2 + D * 2)  # each segment reads the tables and its weight
     N, C, r = C4.img_tokens, C4.hidden, C4.lora_rank
     lx = torch.randn((N, C), device="cuda", generator=g).to(bf)
     la = (torch.randn((r, C), device="cuda", generator=g) / r).to(bf)
@@ -157,8 +159,8 @@ def memory_bound_bench(torch, fa, cfg):
     lu = torch.empty((N, r), device="cuda", dtype=bf)
     ly = torch.randn((N, C), device="cuda", generator=g).to(bf)
     cases = {
-        "qk_prologue_fwd": (lambda: fa.qk_prologue(x, w, cos, sin, cfg.axes, out=y), 2 * row + tables),
-        "qk_prologue_bwd": (lambda: fa.qk_prologue_bwd(x, w, cos, sin, cfg.axes, dy, dx=dx), 3 * row + tables),
+        "qk_prologue_fwd": (lambda: fa.qk_prologue_multi(fwd_segs), 4 * row + tables),
+        "qk_prologue_bwd": (lambda: fa.qk_prologue_bwd_multi(bwd_segs), 6 * row + tables),
         "lora_down": (lambda: fa.lora_down(lx, la, 1.0, out=lu), N * C * 2 + r * C * 2 + N * r * 2),
         "lora_up": (lambda: fa.lora_up(lu, lb, ly, 1.0), 2 * N * C * 2 + N * r * 2 + C * r * 2),
     }
@@ -168,7 +170,8 @@ def memory_bound_bench(torch, fa, cfg):
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
                      "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
-    out["shapes"] = (f"prologue: B={B} S={S} H={H} D={D} bf16; lora: N={N} C={C} r={r} bf16")
+    out["shapes"] = (f"prologue: Q and K in one launch, each B={B} S={S} H={H} D={D} bf16; "
+                     f"lora: N={N} C={C} r={r} bf16")
     return out
 
 

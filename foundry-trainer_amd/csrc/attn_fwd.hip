@@ -537,9 +537,8 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(AttnFwdParams p) {
 // L2 -> LDS bytes per FLOP but only pay when the 8-wave grid's last round is
 // at least half full: measured on MI355X, c2 (B1 H24 S4608: last round 69%
 // full) +3.6% and c5 (B2 S6656: 88%) +3% fwd+bwd, c3 (B4 S1536: 25%) -13%.
-namespace {
 // CU count of the current device (cached per device; 256 if unknown).
-int device_cus() {
+int device_cu_count() {
     static int cus[64];
     int dev = 0;
     int n = 256;
@@ -552,12 +551,11 @@ int device_cus() {
     }
     return n;
 }
-}  // namespace
 
 int attn_waves(int B, int H, int S) {
     if (S < 512) return 4;  // fewer than two 256-row tiles per (b, h)
     if (attn_split(B, H, S) > 1) return 8;
-    const int n = device_cus();
+    const int n = device_cu_count();
     const int64_t wg = (int64_t)B * H * ((S + 255) / 256);
     const int64_t last = wg % n == 0 ? n : wg % n;
     return 2 * last >= n ? 8 : 4;
@@ -571,7 +569,7 @@ int attn_waves(int B, int H, int S) {
 // partials cost an f32 write and read of split x O (or of each gradient).
 int attn_split(int B, int H, int S) {
     if (S < 1024) return 1;
-    const int n = device_cus();
+    const int n = device_cu_count();
     const int64_t wg = (int64_t)B * H * ((S + 255) / 256);
     if (2 * wg > n) return 1;
     const int nc = (S + kSplitChunk - 1) / kSplitChunk;

@@ -528,26 +528,76 @@ size_t lora_bwd_workspace_bytes(int N, int K, int M, int r, int elt);
 extern "C" {
 
 fa_status fa_qk_prologue_fwd(const fa_qk_prologue_args *a, void *stream) {
-    FA_TRY(check_prologue(a));
+    return fa_qk_prologue_fwd_multi(a, 1, stream);
+}
+
+fa_status fa_qk_prologue_bwd(const fa_qk_prologue_bwd_args *a, void *stream) {
+    return fa_qk_prologue_bwd_multi(a, 1, stream);
+}
+
+// Rows [off, off + T) of segments i and j overlap in one output view.
+static bool rows_overlap(const void *yi, const fa_strides &si, int oi, int ti, const void *yj, const fa_strides &sj,
+                         int oj, int tj) {
+    if (yi != yj || si.b != sj.b || si.s != sj.s || si.h != sj.h) return false;
+    return oi < oj + tj && oj < oi + ti;
+}
+
+static fa_status check_prologue_set(const fa_qk_prologue_args *const *segs, int32_t count) {
+    if (count < 1 || count > FA_MAX_PROLOGUE_SEGS)
+        return fail(FA_ERR_INVALID_ARG, "count %d outside 1..%d", count, FA_MAX_PROLOGUE_SEGS);
+    for (int i = 1; i < count; ++i)
+        if (segs[i]->dtype != segs[0]->dtype || segs[i]->head_dim != segs[0]->head_dim)
+            return fail(FA_ERR_INVALID_ARG, "segment %d: dtype and head_dim must match segment 0", i);
+    return FA_OK;
+}
+
+fa_status fa_qk_prologue_fwd_multi(const fa_qk_prologue_args *a, int32_t count, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (count < 1 || count > FA_MAX_PROLOGUE_SEGS)
+        return fail(FA_ERR_INVALID_ARG, "count %d outside 1..%d", count, FA_MAX_PROLOGUE_SEGS);
+    const fa_qk_prologue_args *segs[FA_MAX_PROLOGUE_SEGS];
+    fa::QkPrologueParams ps[FA_MAX_PROLOGUE_SEGS]{};
+    for (int i = 0; i < count; ++i) {
+        FA_TRY(check_prologue(&a[i]));
+        segs[i] = &a[i];
+        fill_prologue(&a[i], ps[i]);
+        for (int j = 0; j < i; ++j)
+            if (rows_overlap(a[i].y, a[i].y_stride, a[i].y_seq_offset, a[i].tokens, a[j].y, a[j].y_stride,
+                             a[j].y_seq_offset, a[j].tokens))
+                return fail(FA_ERR_INVALID_ARG, "segments %d and %d write overlapping rows of y", j, i);
+    }
+    FA_TRY(check_prologue_set(segs, count));
     FA_TRY(init_current());
-    fa::QkPrologueParams p{};
-    fill_prologue(a, p);
-    const hipError_t e = fa::launch_qk_prologue_fwd(p, a->dtype, static_cast<hipStream_t>(stream));
+    const hipError_t e = fa::launch_qk_prologue_fwd(ps, count, a[0].dtype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "qk prologue forward launch");
     return ok();
 }
 
-fa_status fa_qk_prologue_bwd(const fa_qk_prologue_bwd_args *a, void *stream) {
+fa_status fa_qk_prologue_bwd_multi(const fa_qk_prologue_bwd_args *a, int32_t count, void *stream) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
-    FA_TRY(check_prologue(&a->fwd));
-    FA_TRY(check_view("dy", a->dy, a->fwd.y_stride, a->fwd.dtype));
-    FA_TRY(check_view("dx", a->dx, a->dx_stride, a->fwd.dtype));
+    if (count < 1 || count > FA_MAX_PROLOGUE_SEGS)
+        return fail(FA_ERR_INVALID_ARG, "count %d outside 1..%d", count, FA_MAX_PROLOGUE_SEGS);
+    const fa_qk_prologue_args *segs[FA_MAX_PROLOGUE_SEGS];
+    fa::QkPrologueParams ps[FA_MAX_PROLOGUE_SEGS]{};
+    for (int i = 0; i < count; ++i) {
+        FA_TRY(check_prologue(&a[i].fwd));
+        FA_TRY(check_view("dy", a[i].dy, a[i].fwd.y_stride, a[i].fwd.dtype));
+        FA_TRY(check_view("dx", a[i].dx, a[i].dx_stride, a[i].fwd.dtype));
+        segs[i] = &a[i].fwd;
+        fill_prologue(&a[i].fwd, ps[i]);
+        ps[i].dy = a[i].dy;
+        ps[i].dx = a[i].dx;
+        ps[i].dx_sb = a[i].dx_stride.b;
+        ps[i].dx_ss = a[i].dx_stride.s;
+        ps[i].dx_sh = a[i].dx_stride.h;
+        for (int j = 0; j < i; ++j)
+            if (rows_overlap(a[i].dx, a[i].dx_stride, 0, a[i].fwd.tokens, a[j].dx, a[j].dx_stride, 0,
+                             a[j].fwd.tokens))
+                return fail(FA_ERR_INVALID_ARG, "segments %d and %d write the same dx rows", j, i);
+    }
+    FA_TRY(check_prologue_set(segs, count));
     FA_TRY(init_current());
-    fa::QkPrologueParams p{};
-    fill_prologue(&a->fwd, p);
-    p.dy = a->dy; p.dx = a->dx;
-    p.dx_sb = a->dx_stride.b; p.dx_ss = a->dx_stride.s; p.dx_sh = a->dx_stride.h;
-    const hipError_t e = fa::launch_qk_prologue_bwd(p, a->fwd.dtype, static_cast<hipStream_t>(stream));
+    const hipError_t e = fa::launch_qk_prologue_bwd(ps, count, a[0].fwd.dtype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "qk prologue backward launch");
     return ok();
 }

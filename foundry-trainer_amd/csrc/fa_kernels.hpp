@@ -67,6 +67,9 @@ int attn_split(int B, int H, int S);
 size_t attn_split_elems(int B, int H, int S, int D, int split);
 hipError_t launch_attn_bwd_f32(const AttnBwdParams &p, int D, int phase, hipStream_t s);
 
+// CU count of the current device (cached per device; 256 if unknown).
+int device_cu_count();
+
 // One-time per-process kernel attribute setup (dynamic LDS limits).
 hipError_t prepare_attn_kernels();
 
@@ -87,8 +90,10 @@ struct QkPrologueParams {
     float inv_h;  // 1 / H, set by the launcher
 };
 
-hipError_t launch_qk_prologue_fwd(const QkPrologueParams &p, int dtype, hipStream_t s);
-hipError_t launch_qk_prologue_bwd(const QkPrologueParams &p, int dtype, hipStream_t s);
+// n segments (1..kMaxPrologueSegs) of one dtype and head_dim in one launch.
+constexpr int kMaxPrologueSegs = 4;
+hipError_t launch_qk_prologue_fwd(const QkPrologueParams *ps, int n, int dtype, hipStream_t s);
+hipError_t launch_qk_prologue_bwd(const QkPrologueParams *ps, int n, int dtype, hipStream_t s);
 
 struct LoraParams {
     const void *x;

@@ -64,6 +64,21 @@ __device__ __forceinline__ void rope_partner(const QkPrologueParams &p, int d, i
     }
 }
 
+// Round two f32 values to bf16 (RNE) and back with one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void round2_bf16(float &a, float &b) {
+    const uint32_t w = pack_bf16x2(a, b);
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+}
+
+// bf16 rows take the fast row statistics: the sum of squares by FMA and one
+// v_rsq_f32 (within 1 ulp) for 1/sigma, then x * (1/sigma) for the division.
+// Their results are cast to bf16 right after (lib.rs:53-56), which an ulp of
+// f32 error changes only for values within that ulp of a bf16 rounding
+// boundary.  f32 rows keep the correctly rounded sqrt and division.
+template <typename T>
+constexpr bool kFastStats = sizeof(T) == 2;
+
 // x / d for every x of a row with one reciprocal per row: q0 = x * r (r =
 // v_rcp_f32(d), within 1 ulp), the exact remainder e = x - q0 * d by FMA, and
 // q = q0 + e * r: the correctly rounded quotient except for rare operands
@@ -152,17 +167,17 @@ __device__ __forceinline__ void row_token_head(const QkPrologueParams &p, int t0
 // before any arithmetic.  Rows past the end load the last row and store
 // nothing.  VEC: cos, sin and weight are 16-byte aligned.
 template <typename T, int D, int R, bool VEC>
-__global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QkPrologueParams p) {
+__device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, int bx, int64_t b) {
     // one rounding per reference op: no FMA contraction of x*cos + rot*sin
 #pragma clang fp contract(off)
     constexpr int EPL = 16 / sizeof(T);   // elements per lane
     constexpr int LPR = D / EPL;          // lanes per row
     constexpr int RPP = 256 / LPR;        // rows per pass
-    __shared__ __attribute__((aligned(16))) float buf[R][RPP][D];
+    // the staged values (n * w) are exact in T: stage them as T
+    __shared__ __attribute__((aligned(16))) T buf[R][RPP][D];
     const int tid = threadIdx.x, lr = tid / LPR, part = tid % LPR;
     const int rows = p.T * p.H;  // per batch item (< 2^31, checked by the ABI)
-    const int64_t b = blockIdx.y;
-    const int r0 = (int)blockIdx.x * (R * RPP);
+    const int r0 = bx * (R * RPP);
     const int t0 = r0 / p.H, h0 = r0 - t0 * p.H;
     __shared__ __attribute__((aligned(16))) signed char ptab[D];
     fill_partner_table<D>(p, ptab);
@@ -187,18 +202,37 @@ __global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QkPrologueParams p
     }
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-        float ss = 0.f;
+        if constexpr (kFastStats<T>) {
+            float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) ss += xv[k][i] * xv[k][i];
-        ss = row_sum<LPR>(ss);
-        const float sc = sqrtf(ss / (float)D + p.eps);
-        const float rc = __builtin_amdgcn_rcpf(sc);
+            for (int i = 0; i < EPL; ++i) ss = __builtin_fmaf(xv[k][i], xv[k][i], ss);
+            ss = row_sum<LPR>(ss);
+            const float rs = __builtin_amdgcn_rsqf(ss * (1.f / (float)D) + p.eps);
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            const float nv = round_dt<T>(div_by(xv[k][i], sc, rc));
-            xv[k][i] = round_dt<T>(nv * wv[i]);  // the normed, weighted row (n * w)
-            buf[k][lr][part * EPL + i] = xv[k][i];
+            for (int i = 0; i < EPL; i += 2) {
+                float n0 = xv[k][i] * rs, n1 = xv[k][i + 1] * rs;
+                round2_bf16(n0, n1);  // n cast to bf16
+                n0 *= wv[i];
+                n1 *= wv[i + 1];
+                round2_bf16(n0, n1);  // n * w in bf16
+                xv[k][i] = n0;
+                xv[k][i + 1] = n1;
+            }
+        } else {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) ss += xv[k][i] * xv[k][i];
+            ss = row_sum<LPR>(ss);
+            const float sc = sqrtf(ss / (float)D + p.eps);
+            const float rc = __builtin_amdgcn_rcpf(sc);
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) {
+                const float nv = round_dt<T>(div_by(xv[k][i], sc, rc));
+                xv[k][i] = round_dt<T>(nv * wv[i]);  // the normed, weighted row (n * w)
+            }
         }
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) buf[k][lr][part * EPL + i] = (T)xv[k][i];
     }
     __syncthreads();
     int pd[EPL];
@@ -215,24 +249,26 @@ __global__ __launch_bounds__(256) void qk_prologue_fwd_kernel(QkPrologueParams p
         T out[EPL];
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
+            // x*cos + rot(x)*sin with rot = sign * partner: the sign
+            // product is exact, so one FMA gives the reference's rounding
+            // of the sum of the two rounded products
             const float a = xv[k][i] * cv[k][i];
-            const float r = sg[i] * buf[k][lr][pd[i]] * sv[k][i];
-            out[i] = cast_out<T>(a + r);
+            const float r = (float)buf[k][lr][pd[i]] * sv[k][i];
+            out[i] = cast_out<T>(__builtin_fmaf(sg[i], r, a));
         }
         st_global_16(static_cast<T *>(p.y) + yoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
 }
 
 template <typename T, int D, int R, bool VEC>
-__global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QkPrologueParams p) {
+__device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, int bx, int64_t b) {
     constexpr int EPL = 16 / sizeof(T);
     constexpr int LPR = D / EPL;
     constexpr int RPP = 256 / LPR;
     __shared__ __attribute__((aligned(16))) float buf[R][RPP][D];
     const int tid = threadIdx.x, lr = tid / LPR, part = tid % LPR;
     const int rows = p.T * p.H;
-    const int64_t b = blockIdx.y;
-    const int r0 = (int)blockIdx.x * (R * RPP);
+    const int r0 = bx * (R * RPP);
     const int t0 = r0 / p.H, h0 = r0 - t0 * p.H;
     __shared__ __attribute__((aligned(16))) signed char ptab[D];
     fill_partner_table<D>(p, ptab);
@@ -276,16 +312,23 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QkPrologueParams p
 #pragma unroll
         for (int i = 0; i < EPL; ++i) ss += xv[k][i] * xv[k][i];
         ss = row_sum<LPR>(ss);
-        const float sigma = sqrtf(ss / (float)D + p.eps);
-        const float rs = __builtin_amdgcn_rcpf(sigma);
+        float sigma = 0.f, rs;
+        if constexpr (kFastStats<T>) {
+            rs = __builtin_amdgcn_rsqf(ss * (1.f / (float)D) + p.eps);
+        } else {
+            sigma = sqrtf(ss / (float)D + p.eps);
+            rs = __builtin_amdgcn_rcpf(sigma);
+        }
+        // x / sigma: one multiply for bf16 rows, the corrected quotient for f32
+        auto over_sigma = [&](float v) { return kFastStats<T> ? v * rs : div_by(v, sigma, rs); };
         float dn[EPL], nv[EPL];
         float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
             // rot^T takes the partner with the opposite sign of rot
-            const float gv = dyv[k][i] * cv[k][i] - sg[i] * buf[k][lr][pd[i]];
+            const float gv = __builtin_fmaf(-sg[i], buf[k][lr][pd[i]], dyv[k][i] * cv[k][i]);
             dn[i] = gv * wv[i];
-            nv[i] = div_by(xv[k][i], sigma, rs);
+            nv[i] = over_sigma(xv[k][i]);
             dot += dn[i] * nv[i];
         }
         dot = row_sum<LPR>(dot);
@@ -293,50 +336,96 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(QkPrologueParams p
         const float mdot = dot * (1.f / (float)D);
         T out[EPL];
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) out[i] = cast_out<T>(div_by(dn[i] - nv[i] * mdot, sigma, rs));
+        for (int i = 0; i < EPL; ++i) out[i] = cast_out<T>(over_sigma(dn[i] - nv[i] * mdot));
         st_global_16(static_cast<T *>(p.dx) + dxoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
 }
 
-constexpr int kPrologueRows = 2;  // rows per lane (passes per workgroup)
+#ifndef FA_PROLOGUE_ROWS
+#define FA_PROLOGUE_ROWS 2
+#endif
+constexpr int kPrologueRows = FA_PROLOGUE_ROWS;  // rows per lane (passes per workgroup)
+
+// Several prologue segments (Q and K of the txt and img streams) in one
+// launch: the grid's x blocks are the segments' blocks end to end, and a
+// workgroup finds its segment from the prefix table (wave-uniform), so the
+// launch ramp and each workgroup's setup serve every segment at once.
+struct QkPrologueMulti {
+    QkPrologueParams seg[kMaxPrologueSegs];
+    int wg0[kMaxPrologueSegs + 1];  // first grid x block of each segment; wg0[count] = grid x
+    int count;
+};
+
+template <typename T, int D, int R, bool VEC, bool BWD>
+__global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti m) {
+    const int bx = blockIdx.x;
+    int sgi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxPrologueSegs; ++i)
+        if (i < m.count && bx >= m.wg0[i]) sgi = i;
+    // one segment's parameters, selected by constant index (kernel-argument
+    // loads, no copy to scratch)
+    auto run = [&](const QkPrologueParams &p) {
+        if ((int)blockIdx.y >= p.B) return;  // a segment with a smaller batch
+        if constexpr (BWD)
+            qk_prologue_bwd_body<T, D, R, VEC>(p, bx - m.wg0[sgi], blockIdx.y);
+        else
+            qk_prologue_fwd_body<T, D, R, VEC>(p, bx - m.wg0[sgi], blockIdx.y);
+    };
+    if (sgi == 0) run(m.seg[0]);
+    else if (sgi == 1) run(m.seg[1]);
+    else if (sgi == 2) run(m.seg[2]);
+    else run(m.seg[3]);
+}
 
 template <typename T, int D, bool BWD, bool VEC>
-hipError_t launch_prologue_v(const QkPrologueParams &p, hipStream_t s) {
+hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
     constexpr int LPR = D * sizeof(T) / 16;
     constexpr int RPB = 256 / LPR * kPrologueRows;
-    const int64_t rows = (int64_t)p.T * p.H;
-    const dim3 grid((unsigned)((rows + RPB - 1) / RPB), (unsigned)p.B), block(256);
-    QkPrologueParams q = p;
-    q.inv_h = 1.f / (float)p.H;
-    if (BWD)
-        hipLaunchKernelGGL((qk_prologue_bwd_kernel<T, D, kPrologueRows, VEC>), grid, block, 0, s, q);
-    else
-        hipLaunchKernelGGL((qk_prologue_fwd_kernel<T, D, kPrologueRows, VEC>), grid, block, 0, s, q);
+    QkPrologueMulti m{};
+    m.count = n;
+    int64_t wg = 0;
+    unsigned by = 1;
+    for (int i = 0; i < n; ++i) {
+        m.seg[i] = ps[i];
+        m.seg[i].inv_h = 1.f / (float)ps[i].H;
+        m.wg0[i] = (int)wg;
+        wg += ((int64_t)ps[i].T * ps[i].H + RPB - 1) / RPB;
+        by = by > (unsigned)ps[i].B ? by : (unsigned)ps[i].B;
+    }
+    if (wg >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
+    for (int i = n; i <= kMaxPrologueSegs; ++i) m.wg0[i] = (int)wg;
+    const dim3 grid((unsigned)wg, by), block(256);
+    hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, kPrologueRows, VEC, BWD>), grid, block, 0, s, m);
     return hipGetLastError();
 }
 
 template <typename T, int D, bool BWD>
-hipError_t launch_prologue(const QkPrologueParams &p, hipStream_t s) {
-    const bool vec = reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && reinterpret_cast<uintptr_t>(p.cos) % 16 == 0 &&
-                     reinterpret_cast<uintptr_t>(p.sin) % 16 == 0;
-    return vec ? launch_prologue_v<T, D, BWD, true>(p, s) : launch_prologue_v<T, D, BWD, false>(p, s);
+hipError_t launch_prologue(const QkPrologueParams *ps, int n, hipStream_t s) {
+    bool vec = true;
+    for (int i = 0; i < n; ++i)
+        vec = vec && reinterpret_cast<uintptr_t>(ps[i].w) % 16 == 0 && reinterpret_cast<uintptr_t>(ps[i].cos) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(ps[i].sin) % 16 == 0;
+    return vec ? launch_prologue_v<T, D, BWD, true>(ps, n, s) : launch_prologue_v<T, D, BWD, false>(ps, n, s);
 }
 
 template <bool BWD>
-hipError_t dispatch(const QkPrologueParams &p, int dtype, hipStream_t s) {
+hipError_t dispatch(const QkPrologueParams *ps, int n, int dtype, hipStream_t s) {
+    if (n < 1 || n > kMaxPrologueSegs) return hipErrorInvalidValue;
+    const int D = ps[0].D;
     if (dtype == 0)
-        return p.D == 128 ? launch_prologue<bf16, 128, BWD>(p, s) : launch_prologue<bf16, 64, BWD>(p, s);
-    return p.D == 128 ? launch_prologue<float, 128, BWD>(p, s) : launch_prologue<float, 64, BWD>(p, s);
+        return D == 128 ? launch_prologue<bf16, 128, BWD>(ps, n, s) : launch_prologue<bf16, 64, BWD>(ps, n, s);
+    return D == 128 ? launch_prologue<float, 128, BWD>(ps, n, s) : launch_prologue<float, 64, BWD>(ps, n, s);
 }
 
 }  // namespace
 
-hipError_t launch_qk_prologue_fwd(const QkPrologueParams &p, int dtype, hipStream_t s) {
-    return dispatch<false>(p, dtype, s);
+hipError_t launch_qk_prologue_fwd(const QkPrologueParams *ps, int n, int dtype, hipStream_t s) {
+    return dispatch<false>(ps, n, dtype, s);
 }
 
-hipError_t launch_qk_prologue_bwd(const QkPrologueParams &p, int dtype, hipStream_t s) {
-    return dispatch<true>(p, dtype, s);
+hipError_t launch_qk_prologue_bwd(const QkPrologueParams *ps, int n, int dtype, hipStream_t s) {
+    return dispatch<true>(ps, n, dtype, s);
 }
 
 }  // namespace fa

@@ -7,8 +7,9 @@ library and fails loudly if it is missing.
 from ._abi import FoundryAttnError, LIB_PATH, lib
 from .ops import (AttnBwd, attention, attn_bwd, attn_fwd, attn_workspace_bytes, lora_bwd, lora_down, lora_fwd,
                   lora_grad, lora_up,
-                  qk_prologue, qk_prologue_bwd, rope_tables)
+                  qk_prologue, qk_prologue_bwd, qk_prologue_bwd_multi, qk_prologue_multi, rope_tables)
 
 __all__ = ["AttnBwd", "attention", "attn_fwd", "attn_bwd", "attn_workspace_bytes", "qk_prologue", "qk_prologue_bwd",
+           "qk_prologue_multi", "qk_prologue_bwd_multi",
            "rope_tables", "lora_fwd", "lora_bwd", "lora_down", "lora_up", "lora_grad", "FoundryAttnError",
            "LIB_PATH", "lib"]

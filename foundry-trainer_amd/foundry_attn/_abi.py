@@ -24,6 +24,7 @@ EXPORTED = [
     "fa_attn_fwd", "fa_attn_fwd_workspace_size", "fa_attn_bwd_workspace_size", "fa_attn_bwd",
     "fa_attn_bwd_phase", "fa_attn_bwd_noalloc",
     "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
+    "fa_qk_prologue_fwd_multi", "fa_qk_prologue_bwd_multi",
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
     # include/foundry_block.h
     "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
@@ -202,6 +203,10 @@ def lib() -> ctypes.CDLL:
         fn = getattr(L, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+    L.fa_qk_prologue_fwd_multi.restype = ctypes.c_int
+    L.fa_qk_prologue_fwd_multi.argtypes = [ctypes.POINTER(QkPrologueArgs), ctypes.c_int32, ctypes.c_void_p]
+    L.fa_qk_prologue_bwd_multi.restype = ctypes.c_int
+    L.fa_qk_prologue_bwd_multi.argtypes = [ctypes.POINTER(QkPrologueBwdArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_adamw_step_many.restype = ctypes.c_int
     L.fa_adamw_step_many.argtypes = [ctypes.POINTER(AdamwArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_attn_bwd_phase.restype = ctypes.c_int

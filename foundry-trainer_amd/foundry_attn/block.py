@@ -42,7 +42,7 @@ import torch
 from . import _abi, gemm_tuning
 from ._abi import FoundryAttnError, check, lib
 from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_down, lora_fwd, lora_grad,
-                  lora_up, qk_prologue, qk_prologue_bwd, rope_tables)
+                  lora_up, qk_prologue_bwd_multi, qk_prologue_multi, rope_tables)
 
 
 # ---------------------------------------------------------------------------
@@ -433,7 +433,8 @@ class DoubleBlockLoRA:
         return contextlib.nullcontext()
 
     def _qkv_phase(self, name, x, saved):
-        """layer_norm_mod -> frozen fused qkv + three adapters -> prologue."""
+        """layer_norm_mod -> frozen fused qkv + three adapters (the prologue of
+        all four Q / K segments follows in one launch, _prologue_fwd)."""
         B, C, H, D, s = self._buf, self.C, self.H, self.D, self.lora_scale
         w, off, n = self.w[name], self.offset[name], self.rows[name]
         h, mean1, rstd1 = ln_mod_fwd(x[name], w.mod[0], w.mod[1], self.eps, out=B[f"h.{name}"], stats=True)
@@ -449,15 +450,36 @@ class DoubleBlockLoRA:
             for j, t in enumerate(QKV):
                 if t in w.lora_a:
                     saved[(name, t)] = lora_fwd(h, w.lora_a[t], w.lora_b[t], rows[:, j * C:(j + 1) * C], s)
-        cos, sin = self.rope[name]
-        qk_prologue(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, self.eps,
-                    out=B["q"], seq_offset=off)
-        qk_prologue(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, self.eps,
-                    out=B["k"], seq_offset=off)
         if self.capture is not None:
             self.capture[f"{name}_norm1"] = h.clone()
-            self.capture[f"{name}.q"] = B["q"][0, off:off + n].clone()
-            self.capture[f"{name}.k"] = B["k"][0, off:off + n].clone()
+
+    def _prologue_segments(self, bwd: bool):
+        """Q and K of both streams as the four segments of one fused
+        RMSNorm + RoPE launch (forward: into the joint Q / K buffers;
+        backward: dQ / dK of the joint buffers into the dqkv rows)."""
+        B, C, H, D = self._buf, self.C, self.H, self.D
+        segs = []
+        for name in STREAMS:
+            w, off, n = self.w[name], self.offset[name], self.rows[name]
+            rows, drows = B["qkv"][off:off + n], B["dqkv"][off:off + n]
+            cos, sin = self.rope[name]
+            for j, (wn, dst, grad) in enumerate(((w.q_norm, "q", "dq"), (w.k_norm, "k", "dk"))):
+                x = rows[:, j * C:(j + 1) * C].view(1, n, H, D)
+                if bwd:
+                    segs.append((x, wn, cos, sin, self.axes, B[grad], off,
+                                 drows[:, j * C:(j + 1) * C].view(1, n, H, D)))
+                else:
+                    segs.append((x, wn, cos, sin, self.axes, B[dst], off))
+        return segs
+
+    def _prologue_fwd(self):
+        B = self._buf
+        qk_prologue_multi(self._prologue_segments(False), self.eps)
+        if self.capture is not None:
+            for name in STREAMS:
+                off, n = self.offset[name], self.rows[name]
+                self.capture[f"{name}.q"] = B["q"][0, off:off + n].clone()
+                self.capture[f"{name}.k"] = B["k"][0, off:off + n].clone()
 
     def _out_phase(self, name, x, dy, o_t, y, saved):
         """Out projection, gated residuals, MLP; with dy, the backward down to dO."""
@@ -500,15 +522,11 @@ class DoubleBlockLoRA:
                                                     dx=do_rows)
 
     def _qkv_bwd_phase(self, name, x, want_dx, saved, grads):
-        """Prologue backward, the three adapters' gradients, and the input gradient."""
+        """The three adapters' gradients and the input gradient (the prologue
+        backward of all four segments ran before, in one launch)."""
         B, C, H, D, s = self._buf, self.C, self.H, self.D, self.lora_scale
         w, off, n = self.w[name], self.offset[name], self.rows[name]
-        rows, drows = B["qkv"][off:off + n], B["dqkv"][off:off + n]
-        cos, sin = self.rope[name]
-        qk_prologue_bwd(rows[:, :C].view(1, n, H, D), w.q_norm, cos, sin, self.axes, B["dq"],
-                        seq_offset=off, eps=self.eps, dx=drows[:, :C].view(1, n, H, D))
-        qk_prologue_bwd(rows[:, C:2 * C].view(1, n, H, D), w.k_norm, cos, sin, self.axes, B["dk"],
-                        seq_offset=off, eps=self.eps, dx=drows[:, C:2 * C].view(1, n, H, D))
+        drows = B["dqkv"][off:off + n]
         h = B[f"h.{name}"]
         dh = torch.mm(drows, w.w_qkv, out=B[f"t2.{name}"]) if want_dx else None
         if self._batched:
@@ -544,6 +562,7 @@ class DoubleBlockLoRA:
             with self._on(name):
                 self._qkv_phase(name, x, saved)
         self._join()
+        self._prologue_fwd()
         v = B["qkv"][:, 2 * C:].view(1, S, H, D)
         if attention is None:
             o_t, lse_t = attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=B["o"], lse=B["lse"])
@@ -567,6 +586,7 @@ class DoubleBlockLoRA:
             for key, t in (("grad_attn.out", B["do"]), ("grad_attn.q", B["dq"]), ("grad_attn.k", B["dk"]),
                            ("grad_attn.v", dv)):
                 self.capture[key] = t[0].clone()
+        qk_prologue_bwd_multi(self._prologue_segments(True), self.eps)
         self._fork()
         for name in STREAMS:
             with self._on(name):
@@ -793,8 +813,8 @@ class SingleBlockLoRA:
             torch.mm(nh, w.w_in.t(), out=fused)
             u_in = lora_fwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], fused, s)
         q_raw, k_raw, v = self._heads(fused[:, :C]), self._heads(fused[:, C:2 * C]), self._heads(fused[:, 2 * C:3 * C])
-        qk_prologue(q_raw, w.q_norm, self.cos, self.sin, self.axes, self.eps, out=B["q"])
-        qk_prologue(k_raw, w.k_norm, self.cos, self.sin, self.axes, self.eps, out=B["k"])
+        qk_prologue_multi([(q_raw, w.q_norm, self.cos, self.sin, self.axes, B["q"], 0),
+                           (k_raw, w.k_norm, self.cos, self.sin, self.axes, B["k"], 0)], self.eps)
         o = self._heads(joined[:, :C])
         if attention is None:
             _, lse = attn_fwd(B["q"], B["k"], v, self.attn_scale, None, out=o, lse=B["lse"])
@@ -833,10 +853,10 @@ class SingleBlockLoRA:
         swiglu_bwd(djoined[:, C:], gate, up, dgate=dfused[:, 3 * C:3 * C + M], dup=dfused[:, 3 * C + M:])
         attn_bwd(B["q"], B["k"], v, o, self._heads(djoined[:, :C]), lse, self.attn_scale, None,
                  workspace=B["ws"], out=(B["dq"], B["dk"], self._heads(dfused[:, 2 * C:3 * C])))
-        qk_prologue_bwd(q_raw, w.q_norm, self.cos, self.sin, self.axes, B["dq"], eps=self.eps,
-                        dx=self._heads(dfused[:, :C]))
-        qk_prologue_bwd(k_raw, w.k_norm, self.cos, self.sin, self.axes, B["dk"], eps=self.eps,
-                        dx=self._heads(dfused[:, C:2 * C]))
+        qk_prologue_bwd_multi([(q_raw, w.q_norm, self.cos, self.sin, self.axes, B["dq"], 0,
+                                self._heads(dfused[:, :C])),
+                               (k_raw, w.k_norm, self.cos, self.sin, self.axes, B["dk"], 0,
+                                self._heads(dfused[:, C:2 * C]))], self.eps)
         if F:
             if want_dx:
                 # dfused [W_in | B_in | 0] = [dfused W_in | dfused B_in | 0]

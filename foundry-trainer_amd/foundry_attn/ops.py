@@ -334,6 +334,16 @@ def _prologue_args(x4, weight, cos, sin, axes, eps, y4, seq_offset) -> _abi.QkPr
                                y_seq_offset=int(seq_offset))
 
 
+def _prologue_fwd_args(x, weight, cos, sin, axes, eps, out, seq_offset):
+    x4 = _as4(x, "x")
+    B, T, H, D = x4.shape
+    y4 = torch.empty((B, T, H, D), dtype=x4.dtype, device=x4.device) if out is None else _as4(out, "out")
+    if y4.shape[0] != B or y4.shape[2:] != (H, D) or seq_offset + T > y4.shape[1] \
+            or y4.dtype != x4.dtype or y4.device != x4.device or seq_offset < 0:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "out does not fit x at seq_offset")
+    return _prologue_args(x4, weight, cos, sin, axes, eps, y4, seq_offset), x4, y4
+
+
 def qk_prologue(x, weight, cos, sin, axes: Sequence[int], eps: float = 1e-6,
                 out: Optional[torch.Tensor] = None, seq_offset: int = 0):
     """apply_rope(rms_norm(x, weight, eps), cos, sin) written to out[:, seq_offset:+T].
@@ -341,25 +351,27 @@ def qk_prologue(x, weight, cos, sin, axes: Sequence[int], eps: float = 1e-6,
     x: (B,T,H,D) or (T,H,D) linear output (any row strides); out: the joint
     (B,S,H,D) buffer (allocated as (B,T,H,D) if None).  Returns out.
     """
-    squeeze = x.dim() == 3
-    x4 = _as4(x, "x")
-    B, T, H, D = x4.shape
-    y4 = torch.empty((B, T, H, D), dtype=x4.dtype, device=x4.device) if out is None else _as4(out, "out")
-    if y4.shape[0] != B or y4.shape[2:] != (H, D) or seq_offset + T > y4.shape[1] \
-            or y4.dtype != x4.dtype or y4.device != x4.device or seq_offset < 0:
-        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "out does not fit x at seq_offset")
-    a = _prologue_args(x4, weight, cos, sin, axes, eps, y4, seq_offset)
+    a, x4, y4 = _prologue_fwd_args(x, weight, cos, sin, axes, eps, out, seq_offset)
     check(lib().fa_qk_prologue_fwd(ctypes.byref(a), _stream(x4)))
-    if out is None and squeeze:
+    if out is None and x.dim() == 3:
         return y4[0]
     return out if out is not None else y4
 
 
-def qk_prologue_bwd(x, weight, cos, sin, axes: Sequence[int], dy, seq_offset: int = 0,
-                    eps: float = 1e-6, dx: Optional[torch.Tensor] = None):
-    """Gradient wrt x of qk_prologue, given dy wrt the joint buffer; written to
-    `dx` (a view shaped like x, any row strides) when given."""
-    squeeze = x.dim() == 3
+def qk_prologue_multi(segments, eps: float = 1e-6):
+    """Several qk_prologue calls in one launch (fa_qk_prologue_fwd_multi).
+
+    segments: up to 4 tuples (x, weight, cos, sin, axes, out, seq_offset)
+    sharing dtype and head_dim, e.g. Q and K of a block's txt and img
+    streams; `out` is required.  Same results as the separate calls."""
+    segs = [_prologue_fwd_args(x, w, c, s_, ax, eps, out, off) for (x, w, c, s_, ax, out, off) in segments]
+    if not 1 <= len(segs) <= 4:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "1..4 segments")
+    arr = (_abi.QkPrologueArgs * len(segs))(*[a for a, _, _ in segs])
+    check(lib().fa_qk_prologue_fwd_multi(arr, len(segs), _stream(segs[0][1])))
+
+
+def _prologue_bwd_args(x, weight, cos, sin, axes, dy, seq_offset, eps, dx):
     x4, dy4 = _as4(x, "x"), _as4(dy, "dy")
     B, T, H, D = x4.shape
     if dy4.shape[0] != B or dy4.shape[2:] != (H, D) or seq_offset + T > dy4.shape[1] \
@@ -373,8 +385,29 @@ def qk_prologue_bwd(x, weight, cos, sin, axes: Sequence[int], dy, seq_offset: in
             raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "dx must match x")
     a = _abi.QkPrologueBwdArgs(fwd=_prologue_args(x4, weight, cos, sin, axes, eps, dy4, seq_offset),
                                dy=_ptr(dy4), dx=_ptr(dx), dx_stride=_strides(dx))
+    return a, x4, dx
+
+
+def qk_prologue_bwd(x, weight, cos, sin, axes: Sequence[int], dy, seq_offset: int = 0,
+                    eps: float = 1e-6, dx: Optional[torch.Tensor] = None):
+    """Gradient wrt x of qk_prologue, given dy wrt the joint buffer; written to
+    `dx` (a view shaped like x, any row strides) when given."""
+    a, x4, dx = _prologue_bwd_args(x, weight, cos, sin, axes, dy, seq_offset, eps, dx)
     check(lib().fa_qk_prologue_bwd(ctypes.byref(a), _stream(x4)))
-    return dx[0] if squeeze else dx
+    return dx[0] if x.dim() == 3 else dx
+
+
+def qk_prologue_bwd_multi(segments, eps: float = 1e-6):
+    """Several qk_prologue_bwd calls in one launch (fa_qk_prologue_bwd_multi).
+
+    segments: up to 4 tuples (x, weight, cos, sin, axes, dy, seq_offset, dx)
+    sharing dtype and head_dim; `dx` is required.  Same results as the
+    separate calls."""
+    segs = [_prologue_bwd_args(x, w, c, s_, ax, dy, off, eps, dx) for (x, w, c, s_, ax, dy, off, dx) in segments]
+    if not 1 <= len(segs) <= 4:
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "1..4 segments")
+    arr = (_abi.QkPrologueBwdArgs * len(segs))(*[a for a, _, _ in segs])
+    check(lib().fa_qk_prologue_bwd_multi(arr, len(segs), _stream(segs[0][1])))
 
 
 # ---------------------------------------------------------------------------

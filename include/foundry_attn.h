@@ -234,6 +234,20 @@ typedef struct fa_qk_prologue_bwd_args {
  * The norm weight is frozen, so no weight gradient is produced. */
 fa_status fa_qk_prologue_bwd(const fa_qk_prologue_bwd_args *args, void *stream);
 
+/* Up to FA_MAX_PROLOGUE_SEGS prologues in one launch: args[0..count) are
+ * independent calls of fa_qk_prologue_fwd (or _bwd) that share dtype and
+ * head_dim -- typically Q and K of the txt and img streams of one block
+ * (lib.rs:322-357), each writing its rows of the joint Q or K buffer.  One
+ * launch amortises the launch ramp and each workgroup's setup over all of
+ * them; results are those of the separate calls, bit for bit.  Segments
+ * that write the same buffer (same y, or dx, and strides) must write
+ * disjoint rows; arguments are validated as the single calls validate them.
+ * No reference counterpart: the reference runs these as separate Candle op
+ * chains. */
+#define FA_MAX_PROLOGUE_SEGS 4
+fa_status fa_qk_prologue_fwd_multi(const fa_qk_prologue_args *args, int32_t count, void *stream);
+fa_status fa_qk_prologue_bwd_multi(const fa_qk_prologue_bwd_args *args, int32_t count, void *stream);
+
 /* Host helper: RoPE tables exactly as rope_tables_dtype (lib.rs:77-105):
  * inv_j = theta^(-2j/d_a), f = pos[a]*inv_j in f32, cos/sin duplicated per
  * axis segment, then cast to `dtype` (bf16 tables are written as uint16 bf16

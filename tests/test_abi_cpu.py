@@ -170,6 +170,38 @@ def test_prologue_validation():
     assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
 
 
+def test_prologue_multi_validation():
+    """fa_qk_prologue_{fwd,bwd}_multi check the count, each segment, matching
+    dtype / head_dim and overlapping output rows before any device work."""
+    fake = 1 << 20
+    st = _abi.Strides(0, 3072, 128)
+    ax = (ctypes.c_int32 * 8)(16, 56, 56, 0, 0, 0, 0, 0)
+    mk = lambda **kw: _abi.QkPrologueArgs(**{**dict(dtype=0, batch=1, tokens=4, heads=24, head_dim=128, eps=1e-6,
+                                                    x=fake, x_stride=st, weight=fake, cos=fake, sin=fake, n_axes=3,
+                                                    axes=ax, y=fake, y_stride=st, y_seq_offset=0), **kw})
+    L = lib()
+    arr = (_abi.QkPrologueArgs * 5)(mk(), mk(), mk(), mk(), mk())
+    assert L.fa_qk_prologue_fwd_multi(arr, 0, None) == _abi.FA_ERR_INVALID_ARG
+    assert L.fa_qk_prologue_fwd_multi(arr, 5, None) == _abi.FA_ERR_INVALID_ARG
+    # same y, same strides, rows 0..4 twice
+    arr = (_abi.QkPrologueArgs * 2)(mk(), mk())
+    assert L.fa_qk_prologue_fwd_multi(arr, 2, None) == _abi.FA_ERR_INVALID_ARG
+    assert b"overlapping" in L.fa_last_error()
+    arr = (_abi.QkPrologueArgs * 2)(mk(), mk(y_seq_offset=4, head_dim=64,
+                                              axes=(ctypes.c_int32 * 8)(16, 24, 24, 0, 0, 0, 0, 0)))
+    assert L.fa_qk_prologue_fwd_multi(arr, 2, None) == _abi.FA_ERR_INVALID_ARG
+    assert b"head_dim" in L.fa_last_error()
+    arr = (_abi.QkPrologueArgs * 2)(mk(), mk(y_seq_offset=4, n_axes=9))
+    assert L.fa_qk_prologue_fwd_multi(arr, 2, None) == _abi.FA_ERR_INVALID_ARG
+    b = (_abi.QkPrologueBwdArgs * 2)(_abi.QkPrologueBwdArgs(fwd=mk(), dy=fake, dx=fake, dx_stride=st),
+                                     _abi.QkPrologueBwdArgs(fwd=mk(y_seq_offset=4), dy=fake, dx=fake, dx_stride=st))
+    assert L.fa_qk_prologue_bwd_multi(b, 2, None) == _abi.FA_ERR_INVALID_ARG
+    assert b"dx" in L.fa_last_error()
+    if not gpu_available():
+        arr = (_abi.QkPrologueArgs * 2)(mk(), mk(y_seq_offset=4))
+        assert L.fa_qk_prologue_fwd_multi(arr, 2, None) == _abi.FA_ERR_NO_DEVICE
+
+
 def test_lora_validation():
     fake = 1 << 20
     a = _abi.LoraArgs(dtype=0, tokens=8, in_features=3072, out_features=9216, rank=64, scale=1.0,

@@ -227,3 +227,48 @@ def test_lora_pieces_strided_views(r):
     fused = host(torch.mm(xe, We.t()))
     ref = host(torch.mm(xe[:, :K], We[:, :K].t()).float() + torch.mm(xe[:, K:K + r].float(), We[:, K:K + r].t().float()))
     assert rel_l2(fused, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prologue_multi_matches_separate_calls(dtype):
+    """fa_qk_prologue_fwd_multi / _bwd_multi: the block's four segments (Q
+    and K of the txt and img streams, different norm weights, tables and joint
+    offsets) in one launch give the bits of four separate calls."""
+    from foundry_attn import qk_prologue_bwd_multi, qk_prologue_multi
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    g = torch.Generator(device="cpu").manual_seed(11)
+    T_txt, T_img, H, D = 77, 300, 6, 128
+    S = T_txt + T_img
+    axes = [16, 56, 56]
+    pos = np.zeros((S, 3), np.float32)
+    pos[:T_txt, 0] = np.arange(T_txt)
+    pos[T_txt:, 1] = np.arange(T_img) // 20
+    pos[T_txt:, 2] = np.arange(T_img) % 20
+    cos, sin = rope_tables(pos, axes, 1e4, dtype=tdt)
+    r = lambda *sh: torch.randn(*sh, generator=g).to(device="cuda", dtype=tdt)
+    x = {(n, t): r(1, T, H, D) for n, T in (("txt", T_txt), ("img", T_img)) for t in "qk"}
+    w = {t: (1 + 0.02 * torch.randn(D, generator=g)).to(device="cuda", dtype=tdt) for t in "qk"}
+    off = {"txt": 0, "img": T_txt}
+    tab = {"txt": (cos[:T_txt].contiguous(), sin[:T_txt].contiguous()),
+           "img": (cos[T_txt:].contiguous(), sin[T_txt:].contiguous())}
+    sep = {t: torch.full((1, S, H, D), float("nan"), dtype=tdt, device="cuda") for t in "qk"}
+    one = {t: torch.full((1, S, H, D), float("nan"), dtype=tdt, device="cuda") for t in "qk"}
+    segs = []
+    for (n, t), xv in x.items():
+        qk_prologue(xv, w[t], *tab[n], axes, out=sep[t], seq_offset=off[n])
+        segs.append((xv, w[t], *tab[n], axes, one[t], off[n]))
+    qk_prologue_multi(segs)
+    torch.cuda.synchronize()
+    for t in "qk":
+        assert torch.equal(sep[t], one[t]), t
+    dy = {t: r(1, S, H, D) for t in "qk"}
+    dsep = {k: torch.empty_like(v) for k, v in x.items()}
+    done = {k: torch.empty_like(v) for k, v in x.items()}
+    bsegs = []
+    for (n, t), xv in x.items():
+        qk_prologue_bwd(xv, w[t], *tab[n], axes, dy[t], seq_offset=off[n], dx=dsep[(n, t)])
+        bsegs.append((xv, w[t], *tab[n], axes, dy[t], off[n], done[(n, t)]))
+    qk_prologue_bwd_multi(bsegs)
+    torch.cuda.synchronize()
+    for k in x:
+        assert torch.equal(dsep[k], done[k]), k
