@@ -454,6 +454,21 @@ fa_status fa_attn_bwd_noalloc(const fa_attn_bwd_args *a, void *stream) {
 
 }  // extern "C"
 
+// The prologue kernels address a batch item's rows with 32-bit offsets made
+// of 24-bit products: token and head strides below 2^24 elements, and the
+// rows of one batch item within 2^31 elements of its first.
+static fa_status check_prologue_span(const char *name, const fa_strides &st, int32_t tokens, int32_t heads,
+                                     int32_t D) {
+    if (st.s >= (int64_t(1) << 24) || st.h >= (int64_t(1) << 24))
+        return fail(FA_ERR_UNSUPPORTED, "%s token/head strides (%lld, %lld) must be < 2^24 elements", name,
+                    (long long)st.s, (long long)st.h);
+    const int64_t span = (int64_t)(tokens - 1) * st.s + (int64_t)(heads - 1) * st.h + D;
+    if (span >= (int64_t(1) << 31))
+        return fail(FA_ERR_UNSUPPORTED, "%s spans %lld elements per batch item; this build addresses < 2^31", name,
+                    (long long)span);
+    return FA_OK;
+}
+
 static fa_status check_prologue(const fa_qk_prologue_args *a) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
     if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)
@@ -478,6 +493,8 @@ static fa_status check_prologue(const fa_qk_prologue_args *a) {
     if (a->y_seq_offset < 0) return fail(FA_ERR_INVALID_ARG, "y_seq_offset < 0");
     FA_TRY(check_view("x", a->x, a->x_stride, a->dtype));
     FA_TRY(check_view("y", a->y, a->y_stride, a->dtype));
+    FA_TRY(check_prologue_span("x", a->x_stride, a->tokens, a->heads, a->head_dim));
+    FA_TRY(check_prologue_span("y", a->y_stride, a->tokens, a->heads, a->head_dim));
     const size_t elt = a->dtype == FA_DTYPE_BF16 ? 2 : 4;
     if (!a->weight || !aligned(a->weight, elt)) return fail(FA_ERR_INVALID_ARG, "weight is NULL or misaligned");
     if (!a->cos || !a->sin || !aligned(a->cos, elt) || !aligned(a->sin, elt))
@@ -583,6 +600,7 @@ fa_status fa_qk_prologue_bwd_multi(const fa_qk_prologue_bwd_args *a, int32_t cou
         FA_TRY(check_prologue(&a[i].fwd));
         FA_TRY(check_view("dy", a[i].dy, a[i].fwd.y_stride, a[i].fwd.dtype));
         FA_TRY(check_view("dx", a[i].dx, a[i].dx_stride, a[i].fwd.dtype));
+        FA_TRY(check_prologue_span("dx", a[i].dx_stride, a[i].fwd.tokens, a[i].fwd.heads, a[i].fwd.head_dim));
         segs[i] = &a[i].fwd;
         fill_prologue(&a[i].fwd, ps[i]);
         ps[i].dy = a[i].dy;

@@ -149,7 +149,7 @@ __device__ __forceinline__ void fill_partner_table(const QkPrologueParams &p, si
 __device__ __forceinline__ void row_token_head(const QkPrologueParams &p, int t0, int h0, int off, int &t, int &h) {
     const int u = h0 + off;
     int q = (int)((float)u * p.inv_h);
-    int r = u - q * p.H;
+    int r = u - (int)__umul24((unsigned)q, (unsigned)p.H);  // q <= u / H + 1, H < 2^24
     if (r >= p.H) {
         ++q;
         r -= p.H;
@@ -159,6 +159,13 @@ __device__ __forceinline__ void row_token_head(const QkPrologueParams &p, int t0
     }
     t = t0 + q;
     h = r;
+}
+
+// Element offset of row (t, h) within its batch item.  The ABI bounds the
+// token and head strides below 2^24 elements and a batch item's rows below
+// 2^31 elements, so two 24-bit products (full-rate VALU) give it in 32 bits.
+__device__ __forceinline__ uint32_t row_offset(int t, int h, int64_t ss, int64_t sh) {
+    return __umul24((unsigned)t, (unsigned)ss) + __umul24((unsigned)h, (unsigned)sh);
 }
 
 // Rows are (b, token, head) triples in row-major order; a workgroup covers
@@ -184,7 +191,10 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
     float wv[EPL];
     load_row_part<T, VEC>(static_cast<const T *>(p.w) + part * EPL, wv);
     float xv[R][EPL], cv[R][EPL], sv[R][EPL];
-    int64_t yoff[R];
+    // rows of batch item b: 32-bit element offsets from uniform bases
+    const T *xb = static_cast<const T *>(p.x) + b * p.x_sb;
+    T *yb = static_cast<T *>(p.y) + b * p.y_sb + (int64_t)p.y_off * p.y_ss;
+    uint32_t yoff[R];
     bool live[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -193,12 +203,12 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
         const int off = live[k] ? off0 : rows - 1 - r0;
         int ti, hi;
         row_token_head(p, t0, h0, off, ti, hi);
-        const int64_t t = ti, h = hi;
-        const T *x = static_cast<const T *>(p.x) + b * p.x_sb + t * p.x_ss + h * p.x_sh;
-        load_row_part<T, true>(x + part * EPL, xv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + t * D + part * EPL, cv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + t * D + part * EPL, sv[k]);
-        yoff[k] = b * p.y_sb + (p.y_off + t) * p.y_ss + h * p.y_sh + part * EPL;
+        const uint32_t xo = row_offset(ti, hi, p.x_ss, p.x_sh) + part * EPL;
+        const uint32_t to = (uint32_t)ti * D + part * EPL;
+        load_row_part<T, true>(xb + xo, xv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + to, sv[k]);
+        yoff[k] = row_offset(ti, hi, p.y_ss, p.y_sh) + part * EPL;
     }
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -256,7 +266,7 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
             const float r = (float)buf[k][lr][pd[i]] * sv[k][i];
             out[i] = cast_out<T>(__builtin_fmaf(sg[i], r, a));
         }
-        st_global_16(static_cast<T *>(p.y) + yoff[k], *reinterpret_cast<const u32x4 *>(out));
+        st_global_16(yb + yoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
 }
 
@@ -275,7 +285,11 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
     float wv[EPL];
     load_row_part<T, VEC>(static_cast<const T *>(p.w) + part * EPL, wv);
     float xv[R][EPL], dyv[R][EPL], cv[R][EPL], sv[R][EPL];
-    int64_t dxoff[R];
+    // rows of batch item b: 32-bit element offsets from uniform bases
+    const T *xb = static_cast<const T *>(p.x) + b * p.x_sb;
+    const T *dyb = static_cast<const T *>(p.dy) + b * p.y_sb + (int64_t)p.y_off * p.y_ss;
+    T *dxb = static_cast<T *>(p.dx) + b * p.dx_sb;
+    uint32_t dxoff[R];
     bool live[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -284,14 +298,12 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
         const int off = live[k] ? off0 : rows - 1 - r0;
         int ti, hi;
         row_token_head(p, t0, h0, off, ti, hi);
-        const int64_t t = ti, h = hi;
-        const T *x = static_cast<const T *>(p.x) + b * p.x_sb + t * p.x_ss + h * p.x_sh;
-        const T *dy = static_cast<const T *>(p.dy) + b * p.y_sb + (p.y_off + t) * p.y_ss + h * p.y_sh;
-        load_row_part<T, true>(x + part * EPL, xv[k]);
-        load_row_part<T, true>(dy + part * EPL, dyv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + t * D + part * EPL, cv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + t * D + part * EPL, sv[k]);
-        dxoff[k] = b * p.dx_sb + t * p.dx_ss + h * p.dx_sh + part * EPL;
+        const uint32_t to = (uint32_t)ti * D + part * EPL;
+        load_row_part<T, true>(xb + row_offset(ti, hi, p.x_ss, p.x_sh) + part * EPL, xv[k]);
+        load_row_part<T, true>(dyb + row_offset(ti, hi, p.y_ss, p.y_sh) + part * EPL, dyv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[k]);
+        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + to, sv[k]);
+        dxoff[k] = row_offset(ti, hi, p.dx_ss, p.dx_sh) + part * EPL;
     }
 #pragma unroll
     for (int k = 0; k < R; ++k)
@@ -337,7 +349,7 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
         T out[EPL];
 #pragma unroll
         for (int i = 0; i < EPL; ++i) out[i] = cast_out<T>(over_sigma(dn[i] - nv[i] * mdot));
-        st_global_16(static_cast<T *>(p.dx) + dxoff[k], *reinterpret_cast<const u32x4 *>(out));
+        st_global_16(dxb + dxoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
 }
 

@@ -168,6 +168,19 @@ def test_prologue_validation():
     a.axes[2] = 56
     a.tokens, a.heads = 1 << 26, 32  # tokens * heads = 2^31 rows per batch item
     assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+    # the kernels address a batch item's rows in 32 bits from 24-bit products
+    a.tokens, a.heads = 4, 24
+    a.x_stride = _abi.Strides(0, 1 << 24, 128)  # token stride of 2^24 elements
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"2^24" in lib().fa_last_error()
+    a.x_stride = st
+    a.tokens, a.y_stride = 1 << 20, _abi.Strides(0, 3072, 128)  # (2^20 - 1) * 3072 + ... >= 2^31
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"2^31" in lib().fa_last_error()
+    a.tokens = 4
+    b = _abi.QkPrologueBwdArgs(fwd=a, dy=fake, dx=fake, dx_stride=_abi.Strides(0, 3072, 1 << 24))
+    assert lib().fa_qk_prologue_bwd(ctypes.byref(b), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"dx" in lib().fa_last_error()
 
 
 def test_prologue_multi_validation():
