@@ -219,7 +219,10 @@ typedef struct fa_qk_prologue_args {
 /* y[:, off:off+tokens] = apply_rope(rms_norm(x, weight, eps), cos, sin), with
  * the reference's cast points (stats f32; normalised value cast to dtype, then
  * * weight in dtype; rotation in f32, cast back).  Fuses lib.rs:45-58,
- * lib.rs:122-129 and the txt||img concatenation lib.rs:363-365. */
+ * lib.rs:122-129 and the txt||img concatenation lib.rs:363-365.
+ * Views of x, y (and dx): token and head strides below 2^24 elements, and a
+ * batch item's rows within 2^31 elements of its first (FA_ERR_UNSUPPORTED
+ * otherwise). */
 fa_status fa_qk_prologue_fwd(const fa_qk_prologue_args *args, void *stream);
 
 typedef struct fa_qk_prologue_bwd_args {
