@@ -173,7 +173,7 @@ __device__ __forceinline__ uint32_t row_offset(int t, int h, int64_t ss, int64_t
 // global loads of the R rows (x, and the token's cos / sin rows) are issued
 // before any arithmetic.  Rows past the end load the last row and store
 // nothing.  VEC: cos, sin and weight are 16-byte aligned.
-template <typename T, int D, int R, bool VEC>
+template <typename T, int D, int R, bool VEC, bool TOK>
 __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, int bx, int64_t b) {
     // one rounding per reference op: no FMA contraction of x*cos + rot*sin
 #pragma clang fp contract(off)
@@ -190,24 +190,33 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
     fill_partner_table<D>(p, ptab);
     float wv[EPL];
     load_row_part<T, VEC>(static_cast<const T *>(p.w) + part * EPL, wv);
-    float xv[R][EPL], cv[R][EPL], sv[R][EPL];
+    // TOK: the lane's R rows are R adjacent heads of one token (H % R == 0),
+    // so one cos / sin load serves them all; otherwise rows k*RPP + lr
+    constexpr int NTAB = TOK ? 1 : R;
+    float xv[R][EPL], cv[NTAB][EPL], sv[NTAB][EPL];
     // rows of batch item b: 32-bit element offsets from uniform bases
     const T *xb = static_cast<const T *>(p.x) + b * p.x_sb;
     T *yb = static_cast<T *>(p.y) + b * p.y_sb + (int64_t)p.y_off * p.y_ss;
     uint32_t yoff[R];
     bool live[R];
+    int ti, hi;
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-        const int off0 = k * RPP + lr;
+        const int off0 = TOK ? lr * R + k : k * RPP + lr;
         live[k] = r0 + off0 < rows;
-        const int off = live[k] ? off0 : rows - 1 - r0;
-        int ti, hi;
-        row_token_head(p, t0, h0, off, ti, hi);
+        if (!TOK || k == 0) {
+            const int off = live[k] ? off0 : rows - 1 - r0;
+            row_token_head(p, t0, h0, off, ti, hi);
+        } else if (live[k]) {
+            ++hi;  // the next head of the same token
+        }
         const uint32_t xo = row_offset(ti, hi, p.x_ss, p.x_sh) + part * EPL;
-        const uint32_t to = (uint32_t)ti * D + part * EPL;
         load_row_part<T, true>(xb + xo, xv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + to, sv[k]);
+        if (!TOK || k == 0) {
+            const uint32_t to = (uint32_t)ti * D + part * EPL;
+            load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[TOK ? 0 : k]);
+            load_row_part<T, VEC>(static_cast<const T *>(p.sin) + to, sv[TOK ? 0 : k]);
+        }
         yoff[k] = row_offset(ti, hi, p.y_ss, p.y_sh) + part * EPL;
     }
 #pragma unroll
@@ -262,15 +271,15 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
             // x*cos + rot(x)*sin with rot = sign * partner: the sign
             // product is exact, so one FMA gives the reference's rounding
             // of the sum of the two rounded products
-            const float a = xv[k][i] * cv[k][i];
-            const float r = (float)buf[k][lr][pd[i]] * sv[k][i];
+            const float a = xv[k][i] * cv[TOK ? 0 : k][i];
+            const float r = (float)buf[k][lr][pd[i]] * sv[TOK ? 0 : k][i];
             out[i] = cast_out<T>(__builtin_fmaf(sg[i], r, a));
         }
         st_global_16(yb + yoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
 }
 
-template <typename T, int D, int R, bool VEC>
+template <typename T, int D, int R, bool VEC, bool TOK>
 __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, int bx, int64_t b) {
     constexpr int EPL = 16 / sizeof(T);
     constexpr int LPR = D / EPL;
@@ -284,31 +293,39 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
     fill_partner_table<D>(p, ptab);
     float wv[EPL];
     load_row_part<T, VEC>(static_cast<const T *>(p.w) + part * EPL, wv);
-    float xv[R][EPL], dyv[R][EPL], cv[R][EPL], sv[R][EPL];
+    // TOK: as in the forward, the lane's R rows share one token's cos / sin
+    constexpr int NTAB = TOK ? 1 : R;
+    float xv[R][EPL], dyv[R][EPL], cv[NTAB][EPL], sv[NTAB][EPL];
     // rows of batch item b: 32-bit element offsets from uniform bases
     const T *xb = static_cast<const T *>(p.x) + b * p.x_sb;
     const T *dyb = static_cast<const T *>(p.dy) + b * p.y_sb + (int64_t)p.y_off * p.y_ss;
     T *dxb = static_cast<T *>(p.dx) + b * p.dx_sb;
     uint32_t dxoff[R];
     bool live[R];
+    int ti, hi;
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-        const int off0 = k * RPP + lr;
+        const int off0 = TOK ? lr * R + k : k * RPP + lr;
         live[k] = r0 + off0 < rows;
-        const int off = live[k] ? off0 : rows - 1 - r0;
-        int ti, hi;
-        row_token_head(p, t0, h0, off, ti, hi);
-        const uint32_t to = (uint32_t)ti * D + part * EPL;
+        if (!TOK || k == 0) {
+            const int off = live[k] ? off0 : rows - 1 - r0;
+            row_token_head(p, t0, h0, off, ti, hi);
+        } else if (live[k]) {
+            ++hi;  // the next head of the same token
+        }
         load_row_part<T, true>(xb + row_offset(ti, hi, p.x_ss, p.x_sh) + part * EPL, xv[k]);
         load_row_part<T, true>(dyb + row_offset(ti, hi, p.y_ss, p.y_sh) + part * EPL, dyv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[k]);
-        load_row_part<T, VEC>(static_cast<const T *>(p.sin) + to, sv[k]);
+        if (!TOK || k == 0) {
+            const uint32_t to = (uint32_t)ti * D + part * EPL;
+            load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[TOK ? 0 : k]);
+            load_row_part<T, VEC>(static_cast<const T *>(p.sin) + to, sv[TOK ? 0 : k]);
+        }
         dxoff[k] = row_offset(ti, hi, p.dx_ss, p.dx_sh) + part * EPL;
     }
 #pragma unroll
     for (int k = 0; k < R; ++k)
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) buf[k][lr][part * EPL + i] = dyv[k][i] * sv[k][i];
+        for (int i = 0; i < EPL; ++i) buf[k][lr][part * EPL + i] = dyv[k][i] * sv[TOK ? 0 : k][i];
     __syncthreads();
     int pd[EPL];
     float sg[EPL];
@@ -338,7 +355,7 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
             // rot^T takes the partner with the opposite sign of rot
-            const float gv = __builtin_fmaf(-sg[i], buf[k][lr][pd[i]], dyv[k][i] * cv[k][i]);
+            const float gv = __builtin_fmaf(-sg[i], buf[k][lr][pd[i]], dyv[k][i] * cv[TOK ? 0 : k][i]);
             dn[i] = gv * wv[i];
             nv[i] = over_sigma(xv[k][i]);
             dot += dn[i] * nv[i];
@@ -368,7 +385,7 @@ struct QkPrologueMulti {
     int count;
 };
 
-template <typename T, int D, int R, bool VEC, bool BWD>
+template <typename T, int D, int R, bool VEC, bool BWD, bool TOK>
 __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti m) {
     const int bx = blockIdx.x;
     int sgi = 0;
@@ -380,9 +397,9 @@ __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti 
     auto run = [&](const QkPrologueParams &p) {
         if ((int)blockIdx.y >= p.B) return;  // a segment with a smaller batch
         if constexpr (BWD)
-            qk_prologue_bwd_body<T, D, R, VEC>(p, bx - m.wg0[sgi], blockIdx.y);
+            qk_prologue_bwd_body<T, D, R, VEC, TOK>(p, bx - m.wg0[sgi], blockIdx.y);
         else
-            qk_prologue_fwd_body<T, D, R, VEC>(p, bx - m.wg0[sgi], blockIdx.y);
+            qk_prologue_fwd_body<T, D, R, VEC, TOK>(p, bx - m.wg0[sgi], blockIdx.y);
     };
     if (sgi == 0) run(m.seg[0]);
     else if (sgi == 1) run(m.seg[1]);
@@ -408,7 +425,14 @@ hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
     if (wg >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
     for (int i = n; i <= kMaxPrologueSegs; ++i) m.wg0[i] = (int)wg;
     const dim3 grid((unsigned)wg, by), block(256);
-    hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, kPrologueRows, VEC, BWD>), grid, block, 0, s, m);
+    // a lane's rows share a token when every segment's head count is a
+    // multiple of the rows per lane (the workgroup's first row is too)
+    bool tok = true;
+    for (int i = 0; i < n; ++i) tok = tok && ps[i].H % kPrologueRows == 0;
+    if (tok)
+        hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, kPrologueRows, VEC, BWD, true>), grid, block, 0, s, m);
+    else
+        hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, kPrologueRows, VEC, BWD, false>), grid, block, 0, s, m);
     return hipGetLastError();
 }
 

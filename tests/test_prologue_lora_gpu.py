@@ -80,11 +80,42 @@ def test_prologue_fixture_replay():
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_prologue_bwd_matches_oracle(dtype):
+@pytest.mark.parametrize("H", [4, 3], ids=["even_heads", "odd_heads"])
+def test_prologue_fwd_strided_matches_oracle(dtype, H):
+    """A strided input view (a q slice of a packed qkv buffer), at an even
+    head count (a lane's two rows are adjacent heads of one token and share
+    one cos / sin load) and an odd one (rows from different tokens)."""
+    bf = dtype == "bf16"
+    tdt = torch.bfloat16 if bf else torch.float32
+    rng = np.random.default_rng(12)
+    T, D = 301, 128
+    rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
+    qkv = rnd(rng.standard_normal((1, T, 3, H, D)).astype(np.float32) * 2)
+    w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    pos = np.stack([np.zeros(T), np.arange(T) // 20, np.arange(T) % 20], -1).astype(np.float32)
+    axes = [16, 56, 56]
+    cos, sin = oracle.rope_tables(pos, axes, 1e4, bf16=bf)
+    want = oracle.apply_rope(oracle.rms_norm(qkv[0, :, 0], w, bf16=bf), cos, sin, axes, bf16=bf)
+    x = dev(qkv, tdt)[:, :, 0]  # token stride 3*H*D, head stride D
+    out = torch.full((1, T + 7, H, D), float("nan"), dtype=tdt, device="cuda")
+    qk_prologue(x, dev(w, tdt), dev(cos, tdt), dev(sin, tdt), axes, out=out, seq_offset=7)
+    got = host(out)[0]
+    assert np.all(np.isnan(got[:7]))
+    got = got[7:]
+    if bf:
+        assert np.mean(got != want) < 1e-3
+        assert max_abs(got, want) <= BF16_MAX_ABS and rel_l2(got, want) <= 1e-3
+    else:
+        assert rel_l2(got, want) <= 1e-6
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("H", [4, 3], ids=["even_heads", "odd_heads"])
+def test_prologue_bwd_matches_oracle(dtype, H):
     bf = dtype == "bf16"
     tdt = torch.bfloat16 if bf else torch.float32
     rng = np.random.default_rng(8)
-    T, H, D = 300, 4, 128
+    T, D = 300, 128
     rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
     x = rnd(rng.standard_normal((T, H, D)).astype(np.float32))
     w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
