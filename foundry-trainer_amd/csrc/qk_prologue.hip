@@ -144,8 +144,10 @@ __device__ __forceinline__ void fill_partner_table(const QkPrologueParams &p, si
 }
 
 // Token and head of row r0 + off of batch item blockIdx.y, with (t0, h0) the
-// workgroup's first row: off < 64 and h0 < H keep u = h0 + off small enough
-// for an exact f32 quotient estimate, corrected by one step either way.
+// workgroup's first row: off < 128 and h0 < H keep u = h0 + off small
+// enough for an f32 quotient estimate within one of u / H, corrected by one
+// step either way (exact for every H <= 1024 and off < 128, checked
+// exhaustively against integer division).
 __device__ __forceinline__ void row_token_head(const QkPrologueParams &p, int t0, int h0, int off, int &t, int &h) {
     const int u = h0 + off;
     int q = (int)((float)u * p.inv_h);
@@ -370,10 +372,12 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
     }
 }
 
-#ifndef FA_PROLOGUE_ROWS
-#define FA_PROLOGUE_ROWS 2
-#endif
-constexpr int kPrologueRows = FA_PROLOGUE_ROWS;  // rows per lane (passes per workgroup)
+// Rows per lane (passes per workgroup).  Measured at c2's Q + K (HIP-graph
+// replay): the forward with rows sharing a token runs 4% faster at 4 rows
+// (80 VGPRs) than at 2; the backward, and rows of different tokens (105
+// VGPRs at 4), stay at 2.
+constexpr int kPrologueRows = 2;
+constexpr int kPrologueRowsFwdTok = 4;
 
 // Several prologue segments (Q and K of the txt and img streams) in one
 // launch: the grid's x blocks are the segments' blocks end to end, and a
@@ -407,10 +411,10 @@ __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti 
     else run(m.seg[3]);
 }
 
-template <typename T, int D, bool BWD, bool VEC>
-hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
+template <typename T, int D, bool BWD, bool VEC, int R, bool TOK>
+hipError_t launch_prologue_r(const QkPrologueParams *ps, int n, hipStream_t s) {
     constexpr int LPR = D * sizeof(T) / 16;
-    constexpr int RPB = 256 / LPR * kPrologueRows;
+    constexpr int RPB = 256 / LPR * R;
     QkPrologueMulti m{};
     m.count = n;
     int64_t wg = 0;
@@ -425,15 +429,23 @@ hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
     if (wg >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
     for (int i = n; i <= kMaxPrologueSegs; ++i) m.wg0[i] = (int)wg;
     const dim3 grid((unsigned)wg, by), block(256);
-    // a lane's rows share a token when every segment's head count is a
-    // multiple of the rows per lane (the workgroup's first row is too)
-    bool tok = true;
-    for (int i = 0; i < n; ++i) tok = tok && ps[i].H % kPrologueRows == 0;
-    if (tok)
-        hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, kPrologueRows, VEC, BWD, true>), grid, block, 0, s, m);
-    else
-        hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, kPrologueRows, VEC, BWD, false>), grid, block, 0, s, m);
+    hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, R, VEC, BWD, TOK>), grid, block, 0, s, m);
     return hipGetLastError();
+}
+
+// A lane's rows share a token when every segment's head count is a multiple
+// of the rows per lane (the workgroup's first row is then one too).
+template <typename T, int D, bool BWD, bool VEC>
+hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
+    auto all_heads = [&](int r) {
+        for (int i = 0; i < n; ++i)
+            if (ps[i].H % r) return false;
+        return true;
+    };
+    if (!BWD && all_heads(kPrologueRowsFwdTok))
+        return launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true>(ps, n, s);
+    if (all_heads(kPrologueRows)) return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true>(ps, n, s);
+    return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false>(ps, n, s);
 }
 
 template <typename T, int D, bool BWD>
