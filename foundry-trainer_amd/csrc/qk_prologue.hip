@@ -442,8 +442,8 @@ hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
             if (ps[i].H % r) return false;
         return true;
     };
-    if (!BWD && all_heads(kPrologueRowsFwdTok))
-        return launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true>(ps, n, s);
+    if constexpr (!BWD)
+        if (all_heads(kPrologueRowsFwdTok)) return launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true>(ps, n, s);
     if (all_heads(kPrologueRows)) return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true>(ps, n, s);
     return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false>(ps, n, s);
 }

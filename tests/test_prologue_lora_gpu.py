@@ -80,20 +80,22 @@ def test_prologue_fixture_replay():
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("H", [4, 3], ids=["even_heads", "odd_heads"])
-def test_prologue_fwd_strided_matches_oracle(dtype, H):
-    """A strided input view (a q slice of a packed qkv buffer), at an even
-    head count (a lane's two rows are adjacent heads of one token and share
-    one cos / sin load) and an odd one (rows from different tokens)."""
+@pytest.mark.parametrize("H,D", [(4, 128), (6, 128), (3, 128), (8, 64), (5, 64)],
+                         ids=["h4", "h6", "h3_odd", "h8_d64", "h5_d64_odd"])
+def test_prologue_fwd_strided_matches_oracle(dtype, H, D):
+    """A strided input view (a q slice of a packed qkv buffer).  Head counts
+    that are multiples of 4 give each lane 4 adjacent heads of one token
+    (one cos / sin load; 128-row workgroups at D = 64), even ones 2, and odd
+    ones rows of different tokens."""
     bf = dtype == "bf16"
     tdt = torch.bfloat16 if bf else torch.float32
     rng = np.random.default_rng(12)
-    T, D = 301, 128
+    T = 301
     rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
     qkv = rnd(rng.standard_normal((1, T, 3, H, D)).astype(np.float32) * 2)
     w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
     pos = np.stack([np.zeros(T), np.arange(T) // 20, np.arange(T) % 20], -1).astype(np.float32)
-    axes = [16, 56, 56]
+    axes = [16, 56, 56] if D == 128 else [16, 24, 24]
     cos, sin = oracle.rope_tables(pos, axes, 1e4, bf16=bf)
     want = oracle.apply_rope(oracle.rms_norm(qkv[0, :, 0], w, bf16=bf), cos, sin, axes, bf16=bf)
     x = dev(qkv, tdt)[:, :, 0]  # token stride 3*H*D, head stride D
