@@ -64,6 +64,22 @@ __device__ __forceinline__ void rope_partner(const QkPrologueParams &p, int d, i
     }
 }
 
+// The forward's x rows (read once) and y rows (written once) go through
+// non-temporal loads and stores, which leave the L2 to the reused cos / sin
+// rows and weights: c2 Q + K 2-3% faster.  The backward's loads measured
+// slower that way and stay plain.
+template <typename T>
+__device__ __forceinline__ void load_row_once(const T *ptr, float (&v)[16 / sizeof(T)]) {
+    constexpr int EPL = 16 / sizeof(T);
+    const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ptr));
+    const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) v[i] = (float)e[i];
+}
+__device__ __forceinline__ void store_row_once(void *ptr, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(ptr));
+}
+
 // Round two f32 values to bf16 (RNE) and back with one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ void round2_bf16(float &a, float &b) {
     const uint32_t w = pack_bf16x2(a, b);
@@ -213,7 +229,7 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
             ++hi;  // the next head of the same token
         }
         const uint32_t xo = row_offset(ti, hi, p.x_ss, p.x_sh) + part * EPL;
-        load_row_part<T, true>(xb + xo, xv[k]);
+        load_row_once<T>(xb + xo, xv[k]);
         if (!TOK || k == 0) {
             const uint32_t to = (uint32_t)ti * D + part * EPL;
             load_row_part<T, VEC>(static_cast<const T *>(p.cos) + to, cv[TOK ? 0 : k]);
@@ -277,7 +293,7 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
             const float r = (float)buf[k][lr][pd[i]] * sv[TOK ? 0 : k][i];
             out[i] = cast_out<T>(__builtin_fmaf(sg[i], r, a));
         }
-        st_global_16(yb + yoff[k], *reinterpret_cast<const u32x4 *>(out));
+        store_row_once(yb + yoff[k], *reinterpret_cast<const u32x4 *>(out));
     }
 }
 
