@@ -191,7 +191,7 @@ __device__ __forceinline__ uint32_t row_offset(int t, int h, int64_t ss, int64_t
 // global loads of the R rows (x, and the token's cos / sin rows) are issued
 // before any arithmetic.  Rows past the end load the last row and store
 // nothing.  VEC: cos, sin and weight are 16-byte aligned.
-template <typename T, int D, int R, bool VEC, bool TOK>
+template <typename T, int D, int R, bool VEC, bool TOK, bool QUAD>
 __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, int bx, int64_t b) {
     // one rounding per reference op: no FMA contraction of x*cos + rot*sin
 #pragma clang fp contract(off)
@@ -272,6 +272,40 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
         for (int i = 0; i < EPL; ++i) buf[k][lr][part * EPL + i] = (T)xv[k][i];
     }
     __syncthreads();
+    if constexpr (QUAD) {
+        // Every axis half is a multiple of 4: the partners of an aligned
+        // group of 4 elements are an aligned group of 4 with one sign, read
+        // from LDS in one access (8 bytes of bf16, 16 of f32).
+        using Group = std::conditional_t<sizeof(T) == 2, u32x2, u32x4>;
+        constexpr int NG = EPL / 4;
+        int pq[NG];
+        float sq[NG];
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const int o = ptab[part * EPL + 4 * j];
+            pq[j] = part * EPL + 4 * j + o;
+            sq[j] = o > 0 ? -1.f : 1.f;
+        }
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            if (!live[k]) continue;
+            T out[EPL];
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                const Group raw = *reinterpret_cast<const Group *>(&buf[k][lr][pq[j]]);
+                const T *pv = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * j + e;
+                    const float a = xv[k][i] * cv[TOK ? 0 : k][i];
+                    const float r = (float)pv[e] * sv[TOK ? 0 : k][i];
+                    out[i] = cast_out<T>(__builtin_fmaf(sq[j], r, a));
+                }
+            }
+            store_row_once(yb + yoff[k], *reinterpret_cast<const u32x4 *>(out));
+        }
+        return;
+    }
     int pd[EPL];
     float sg[EPL];
 #pragma unroll
@@ -405,7 +439,7 @@ struct QkPrologueMulti {
     int count;
 };
 
-template <typename T, int D, int R, bool VEC, bool BWD, bool TOK>
+template <typename T, int D, int R, bool VEC, bool BWD, bool TOK, bool QUAD>
 __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti m) {
     const int bx = blockIdx.x;
     int sgi = 0;
@@ -419,7 +453,7 @@ __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti 
         if constexpr (BWD)
             qk_prologue_bwd_body<T, D, R, VEC, TOK>(p, bx - m.wg0[sgi], blockIdx.y);
         else
-            qk_prologue_fwd_body<T, D, R, VEC, TOK>(p, bx - m.wg0[sgi], blockIdx.y);
+            qk_prologue_fwd_body<T, D, R, VEC, TOK, QUAD>(p, bx - m.wg0[sgi], blockIdx.y);
     };
     if (sgi == 0) run(m.seg[0]);
     else if (sgi == 1) run(m.seg[1]);
@@ -427,7 +461,7 @@ __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti 
     else run(m.seg[3]);
 }
 
-template <typename T, int D, bool BWD, bool VEC, int R, bool TOK>
+template <typename T, int D, bool BWD, bool VEC, int R, bool TOK, bool QUAD = false>
 hipError_t launch_prologue_r(const QkPrologueParams *ps, int n, hipStream_t s) {
     constexpr int LPR = D * sizeof(T) / 16;
     constexpr int RPB = 256 / LPR * R;
@@ -445,7 +479,7 @@ hipError_t launch_prologue_r(const QkPrologueParams *ps, int n, hipStream_t s) {
     if (wg >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
     for (int i = n; i <= kMaxPrologueSegs; ++i) m.wg0[i] = (int)wg;
     const dim3 grid((unsigned)wg, by), block(256);
-    hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, R, VEC, BWD, TOK>), grid, block, 0, s, m);
+    hipLaunchKernelGGL((qk_prologue_multi_kernel<T, D, R, VEC, BWD, TOK, QUAD>), grid, block, 0, s, m);
     return hipGetLastError();
 }
 
@@ -458,8 +492,19 @@ hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
             if (ps[i].H % r) return false;
         return true;
     };
-    if constexpr (!BWD)
-        if (all_heads(kPrologueRowsFwdTok)) return launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true>(ps, n, s);
+    // the forward reads rotate-half partners 4 at a time when every axis
+    // half of every segment is a multiple of 4
+    bool quad = true;
+    for (int i = 0; i < n; ++i)
+        for (int a = 0; a < ps[i].n_axes; ++a) quad = quad && (ps[i].axes[a] / 2) % 4 == 0;
+    if constexpr (!BWD) {
+        if (all_heads(kPrologueRowsFwdTok))
+            return quad ? launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true, true>(ps, n, s)
+                        : launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true, false>(ps, n, s);
+        if (quad)
+            return all_heads(kPrologueRows) ? launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true, true>(ps, n, s)
+                                            : launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false, true>(ps, n, s);
+    }
     if (all_heads(kPrologueRows)) return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true>(ps, n, s);
     return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false>(ps, n, s);
 }
