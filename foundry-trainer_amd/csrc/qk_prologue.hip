@@ -331,7 +331,7 @@ __device__ __forceinline__ void qk_prologue_fwd_body(const QkPrologueParams &p, 
     }
 }
 
-template <typename T, int D, int R, bool VEC, bool TOK>
+template <typename T, int D, int R, bool VEC, bool TOK, bool QUAD>
 __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, int bx, int64_t b) {
     constexpr int EPL = 16 / sizeof(T);
     constexpr int LPR = D / EPL;
@@ -379,13 +379,25 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
 #pragma unroll
         for (int i = 0; i < EPL; ++i) buf[k][lr][part * EPL + i] = dyv[k][i] * sv[TOK ? 0 : k][i];
     __syncthreads();
-    int pd[EPL];
-    float sg[EPL];
+    // QUAD: partners in aligned groups of 4 with one sign (as in the
+    // forward), read as one 16-byte LDS access of the f32 staging rows
+    constexpr int NG = EPL / 4;
+    int pd[EPL], pq[NG > 0 ? NG : 1];
+    float sg[EPL], sq[NG > 0 ? NG : 1];
+    if constexpr (QUAD) {
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int o = ptab[part * EPL + i];
-        pd[i] = part * EPL + i + o;
-        sg[i] = o > 0 ? -1.f : 1.f;
+        for (int j = 0; j < NG; ++j) {
+            const int o = ptab[part * EPL + 4 * j];
+            pq[j] = part * EPL + 4 * j + o;
+            sq[j] = o > 0 ? -1.f : 1.f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int o = ptab[part * EPL + i];
+            pd[i] = part * EPL + i + o;
+            sg[i] = o > 0 ? -1.f : 1.f;
+        }
     }
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -404,10 +416,29 @@ __device__ __forceinline__ void qk_prologue_bwd_body(const QkPrologueParams &p, 
         auto over_sigma = [&](float v) { return kFastStats<T> ? v * rs : div_by(v, sigma, rs); };
         float dn[EPL], nv[EPL];
         float dot = 0.f;
+        // the partner value of element i and the sign of rot for it
+        float pv[EPL], ps[EPL];
+        if constexpr (QUAD) {
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                const f32x4 g4 = *reinterpret_cast<const f32x4 *>(&buf[k][lr][pq[j]]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    pv[4 * j + e] = g4[e];
+                    ps[4 * j + e] = sq[j];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) {
+                pv[i] = buf[k][lr][pd[i]];
+                ps[i] = sg[i];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
             // rot^T takes the partner with the opposite sign of rot
-            const float gv = __builtin_fmaf(-sg[i], buf[k][lr][pd[i]], dyv[k][i] * cv[TOK ? 0 : k][i]);
+            const float gv = __builtin_fmaf(-ps[i], pv[i], dyv[k][i] * cv[TOK ? 0 : k][i]);
             dn[i] = gv * wv[i];
             nv[i] = over_sigma(xv[k][i]);
             dot += dn[i] * nv[i];
@@ -451,7 +482,7 @@ __global__ __launch_bounds__(256) void qk_prologue_multi_kernel(QkPrologueMulti 
     auto run = [&](const QkPrologueParams &p) {
         if ((int)blockIdx.y >= p.B) return;  // a segment with a smaller batch
         if constexpr (BWD)
-            qk_prologue_bwd_body<T, D, R, VEC, TOK>(p, bx - m.wg0[sgi], blockIdx.y);
+            qk_prologue_bwd_body<T, D, R, VEC, TOK, QUAD>(p, bx - m.wg0[sgi], blockIdx.y);
         else
             qk_prologue_fwd_body<T, D, R, VEC, TOK, QUAD>(p, bx - m.wg0[sgi], blockIdx.y);
     };
@@ -492,8 +523,8 @@ hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
             if (ps[i].H % r) return false;
         return true;
     };
-    // the forward reads rotate-half partners 4 at a time when every axis
-    // half of every segment is a multiple of 4
+    // rotate-half partners are read 4 at a time when every axis half of
+    // every segment is a multiple of 4
     bool quad = true;
     for (int i = 0; i < n; ++i)
         for (int a = 0; a < ps[i].n_axes; ++a) quad = quad && (ps[i].axes[a] / 2) % 4 == 0;
@@ -501,10 +532,10 @@ hipError_t launch_prologue_v(const QkPrologueParams *ps, int n, hipStream_t s) {
         if (all_heads(kPrologueRowsFwdTok))
             return quad ? launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true, true>(ps, n, s)
                         : launch_prologue_r<T, D, BWD, VEC, kPrologueRowsFwdTok, true, false>(ps, n, s);
-        if (quad)
-            return all_heads(kPrologueRows) ? launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true, true>(ps, n, s)
-                                            : launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false, true>(ps, n, s);
     }
+    if (quad)
+        return all_heads(kPrologueRows) ? launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true, true>(ps, n, s)
+                                        : launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false, true>(ps, n, s);
     if (all_heads(kPrologueRows)) return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, true>(ps, n, s);
     return launch_prologue_r<T, D, BWD, VEC, kPrologueRows, false>(ps, n, s);
 }

@@ -80,13 +80,16 @@ def test_prologue_fixture_replay():
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("H,D", [(4, 128), (6, 128), (3, 128), (8, 64), (5, 64)],
-                         ids=["h4", "h6", "h3_odd", "h8_d64", "h5_d64_odd"])
-def test_prologue_fwd_strided_matches_oracle(dtype, H, D):
+@pytest.mark.parametrize("H,D,axes", [(4, 128, None), (6, 128, None), (3, 128, None), (8, 64, None),
+                                      (5, 64, None), (4, 128, (22, 54, 52)), (3, 128, (22, 54, 52))],
+                         ids=["h4", "h6", "h3_odd", "h8_d64", "h5_d64_odd", "h4_odd_halves", "h3_odd_halves"])
+def test_prologue_fwd_strided_matches_oracle(dtype, H, D, axes):
     """A strided input view (a q slice of a packed qkv buffer).  Head counts
     that are multiples of 4 give each lane 4 adjacent heads of one token
     (one cos / sin load; 128-row workgroups at D = 64), even ones 2, and odd
-    ones rows of different tokens."""
+    ones rows of different tokens.  Axis halves that are all multiples of 4
+    (the default axes) read rotate-half partners 4 at a time; (22, 54, 52)
+    has halves 11, 27, 26 and reads them one by one."""
     bf = dtype == "bf16"
     tdt = torch.bfloat16 if bf else torch.float32
     rng = np.random.default_rng(12)
@@ -95,7 +98,7 @@ def test_prologue_fwd_strided_matches_oracle(dtype, H, D):
     qkv = rnd(rng.standard_normal((1, T, 3, H, D)).astype(np.float32) * 2)
     w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
     pos = np.stack([np.zeros(T), np.arange(T) // 20, np.arange(T) % 20], -1).astype(np.float32)
-    axes = [16, 56, 56] if D == 128 else [16, 24, 24]
+    axes = list(axes) if axes else [16, 56, 56] if D == 128 else [16, 24, 24]
     cos, sin = oracle.rope_tables(pos, axes, 1e4, bf16=bf)
     want = oracle.apply_rope(oracle.rms_norm(qkv[0, :, 0], w, bf16=bf), cos, sin, axes, bf16=bf)
     x = dev(qkv, tdt)[:, :, 0]  # token stride 3*H*D, head stride D
@@ -112,8 +115,9 @@ def test_prologue_fwd_strided_matches_oracle(dtype, H, D):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("H", [4, 3], ids=["even_heads", "odd_heads"])
-def test_prologue_bwd_matches_oracle(dtype, H):
+@pytest.mark.parametrize("H,axes", [(4, (16, 56, 56)), (3, (16, 56, 56)), (4, (22, 54, 52))],
+                         ids=["even_heads", "odd_heads", "odd_halves"])
+def test_prologue_bwd_matches_oracle(dtype, H, axes):
     bf = dtype == "bf16"
     tdt = torch.bfloat16 if bf else torch.float32
     rng = np.random.default_rng(8)
@@ -122,7 +126,7 @@ def test_prologue_bwd_matches_oracle(dtype, H):
     x = rnd(rng.standard_normal((T, H, D)).astype(np.float32))
     w = rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
     pos = np.stack([np.zeros(T), np.arange(T) // 20, np.arange(T) % 20], -1).astype(np.float32)
-    axes = [16, 56, 56]
+    axes = list(axes)
     cos, sin = oracle.rope_tables(pos, axes, 1e4, bf16=bf)
     dy_joint = rnd(rng.standard_normal((1, T + 50, H, D)).astype(np.float32))
     want = oracle.qk_prologue_bwd(x, w, cos, sin, dy_joint[0, 50:], axes)
