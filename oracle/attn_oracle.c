@@ -51,7 +51,7 @@ static void scatter_head(const float *src, float *dst, int b, int h, int S, int 
  * Masked keys (keep[j] == 0) take no part: p = 0.  Returns the natural-log
  * LSE of the scaled scores (-INFINITY when every key is masked).
  */
-static float softmax_row(float *row, int S, float scale, const uint8_t *keep)
+static float softmax_row(float *row, int S, float scale, const uint8_t *keep, float *cast, int bf16)
 {
     float m = -INFINITY;
     for (int j = 0; j < S; ++j) {
@@ -60,6 +60,8 @@ static float softmax_row(float *row, int S, float scale, const uint8_t *keep)
     }
     if (m == -INFINITY) {
         for (int j = 0; j < S; ++j) row[j] = 0.0f;
+        if (cast)
+            for (int j = 0; j < S; ++j) cast[j] = 0.0f;
         return -INFINITY;
     }
     float sum = 0.0f;
@@ -68,21 +70,48 @@ static float softmax_row(float *row, int S, float scale, const uint8_t *keep)
         row[j] = e;
         sum += e;
     }
-    for (int j = 0; j < S; ++j) row[j] = row[j] / sum;
+    if (cast) {
+        for (int j = 0; j < S; ++j) {
+            const float p = row[j] / sum;
+            row[j] = p;
+            cast[j] = rnd(p, bf16);
+        }
+    } else {
+        for (int j = 0; j < S; ++j) row[j] = row[j] / sum;
+    }
     return m + logf(sum);
 }
 
-/* P32 [S][S] = softmax(Qh Kh^T * scale), lse[S]; lib.rs:138-147 / 222-239 */
+/* P32 [S][S] = softmax(Qh Kh^T * scale), lse[S]; lib.rs:138-147 / 222-239.
+ * With P16 (which may be P itself), also P16 = P32 cast to the compute dtype
+ * (`probs.to_dtype(q.dtype())`, lib.rs:147 / 239), elementwise. */
 static void probs_f32(const float *Qh, const float *Kh, float *KT, float *P, float *lse, int S,
-                      int D, float scale, const uint8_t *keep, int nthreads)
+                      int D, float scale, const uint8_t *keep, float *P16, int bf16, int nthreads)
 {
     og_transpose(S, D, Kh, D, KT, S, nthreads);
     og_gemm_nn(S, S, D, Qh, D, KT, S, P, S, nthreads);
 #pragma omp parallel for num_threads(nthreads) schedule(static)
     for (int i = 0; i < S; ++i) {
-        const float l = softmax_row(P + (long)i * S, S, scale, keep);
+        const float l = softmax_row(P + (long)i * S, S, scale, keep, P16 ? P16 + (long)i * S : NULL, bf16);
         if (lse) lse[i] = l;
     }
+}
+
+/* Score-sized [S][S] buffers, kept per thread from one call to the next so
+ * that a run over many heads does not map and fault in fresh pages each time
+ * (held until the thread ends). */
+#define N_SCORE_BUFS 3
+static _Thread_local float *score_buf[N_SCORE_BUFS];
+static _Thread_local size_t score_cap[N_SCORE_BUFS];
+
+static float *score_buffer(int slot, size_t n)
+{
+    if (score_cap[slot] < n) {
+        free(score_buf[slot]);
+        score_buf[slot] = malloc(sizeof(float) * n);
+        score_cap[slot] = score_buf[slot] ? n : 0;
+    }
+    return score_buf[slot];
 }
 
 static int check_dims(int B, int S, int H, int D, int h_begin, int h_end)
@@ -101,9 +130,9 @@ int oracle_attn_fwd(const float *q, const float *k, const float *v, float *o, fl
     float *Qh = malloc(sizeof(float) * S * D), *Kh = malloc(sizeof(float) * S * D);
     float *Vh = malloc(sizeof(float) * S * D), *KT = malloc(sizeof(float) * S * D);
     float *Oh = malloc(sizeof(float) * S * D), *L = malloc(sizeof(float) * S);
-    float *P = malloc(sizeof(float) * (long)S * S);
+    float *P = score_buffer(0, (size_t)S * S);
     if (!Qh || !Kh || !Vh || !KT || !Oh || !L || !P) {
-        free(Qh); free(Kh); free(Vh); free(KT); free(Oh); free(L); free(P);
+        free(Qh); free(Kh); free(Vh); free(KT); free(Oh); free(L);
         return -2;
     }
     for (int b = 0; b < B; ++b) {
@@ -112,9 +141,8 @@ int oracle_attn_fwd(const float *q, const float *k, const float *v, float *o, fl
             gather_head(q, Qh, b, h, S, H, D);
             gather_head(k, Kh, b, h, S, H, D);
             gather_head(v, Vh, b, h, S, H, D);
-            probs_f32(Qh, Kh, KT, P, L, S, D, scale, keep, nthreads);
-            /* probs.to_dtype(q.dtype()) — lib.rs:147 */
-            if (bf16) oracle_round_bf16_inplace(P, (long)S * S);
+            /* softmax, then probs.to_dtype(q.dtype()) in place — lib.rs:146-147 */
+            probs_f32(Qh, Kh, KT, P, L, S, D, scale, keep, P, bf16, nthreads);
             /* probs.matmul(vt) in the compute dtype — lib.rs:148 */
             og_gemm_nn(S, D, S, P, S, Vh, D, Oh, D, nthreads);
             if (bf16) oracle_round_bf16_inplace(Oh, (long)S * D);
@@ -122,7 +150,7 @@ int oracle_attn_fwd(const float *q, const float *k, const float *v, float *o, fl
             if (lse) memcpy(lse + ((long)b * H + h) * S, L, sizeof(float) * S);
         }
     }
-    free(Qh); free(Kh); free(Vh); free(KT); free(Oh); free(L); free(P);
+    free(Qh); free(Kh); free(Vh); free(KT); free(Oh); free(L);
     return 0;
 }
 
@@ -136,10 +164,10 @@ int oracle_attn_bwd(const float *q, const float *k, const float *v, const float 
     float *Qh = malloc(sizeof(float) * SD), *Kh = malloc(sizeof(float) * SD);
     float *Vh = malloc(sizeof(float) * SD), *dOh = malloc(sizeof(float) * SD);
     float *T = malloc(sizeof(float) * SD), *R = malloc(sizeof(float) * SD);
-    float *P32 = malloc(sizeof(float) * SS), *P16 = malloc(sizeof(float) * SS);
-    float *dP = malloc(sizeof(float) * SS);
+    float *P32 = score_buffer(0, (size_t)SS), *P16 = score_buffer(1, (size_t)SS);
+    float *dP = score_buffer(2, (size_t)SS);
     if (!Qh || !Kh || !Vh || !dOh || !T || !R || !P32 || !P16 || !dP) {
-        free(Qh); free(Kh); free(Vh); free(dOh); free(T); free(R); free(P32); free(P16); free(dP);
+        free(Qh); free(Kh); free(Vh); free(dOh); free(T); free(R);
         return -2;
     }
     for (int b = 0; b < B; ++b) {
@@ -149,15 +177,14 @@ int oracle_attn_bwd(const float *q, const float *k, const float *v, const float 
             gather_head(k, Kh, b, h, S, H, D);
             gather_head(v, Vh, b, h, S, H, D);
             gather_head(dout, dOh, b, h, S, H, D);
-            /* recompute the f32 probabilities — lib.rs:227-238 */
-            probs_f32(Qh, Kh, T, P32, NULL, S, D, scale, keep, nthreads);
-            /* probs = probs32.to_dtype(q.dtype()) — lib.rs:239 */
-            memcpy(P16, P32, sizeof(float) * SS);
-            if (bf16) oracle_round_bf16_inplace(P16, SS);
+            /* recompute the f32 probabilities — lib.rs:227-238 — and
+             * probs = probs32.to_dtype(q.dtype()) — lib.rs:239 */
+            probs_f32(Qh, Kh, T, P32, NULL, S, D, scale, keep, P16, bf16, nthreads);
             /* dprobs = dout @ vt^T in the compute dtype — lib.rs:243 */
             og_transpose(S, D, Vh, D, T, S, nthreads);
             og_gemm_nn(S, S, D, dOh, D, T, S, dP, S, nthreads);
-            if (bf16) oracle_round_bf16_inplace(dP, SS);
+            /* (its cast to the compute dtype is taken in the softmax-backward
+             * loop below, which is dP's next reader) */
             /* dV = probs^T @ dout — lib.rs:244 */
             og_gemm_tn(S, D, S, P16, S, dOh, D, R, D, nthreads);
             if (bf16) oracle_round_bf16_inplace(R, SD);
@@ -169,7 +196,10 @@ int oracle_attn_bwd(const float *q, const float *k, const float *v, const float 
                 float *dpr = dP + (long)i * S;
                 const float *pr = P32 + (long)i * S;
                 float rs = 0.0f;
-                for (int j = 0; j < S; ++j) rs += dpr[j] * pr[j];
+                for (int j = 0; j < S; ++j) {
+                    dpr[j] = rnd(dpr[j], bf16);
+                    rs += dpr[j] * pr[j];
+                }
                 for (int j = 0; j < S; ++j) dpr[j] = (pr[j] * (dpr[j] - rs)) * scale;
             }
             /* dQ = dS @ K_f32, dK = dS^T @ Q_f32, f32 matmuls cast back — lib.rs:251-257 */
@@ -181,7 +211,7 @@ int oracle_attn_bwd(const float *q, const float *k, const float *v, const float 
             scatter_head(R, dk, b, h, S, H, D);
         }
     }
-    free(Qh); free(Kh); free(Vh); free(dOh); free(T); free(R); free(P32); free(P16); free(dP);
+    free(Qh); free(Kh); free(Vh); free(dOh); free(T); free(R);
     return 0;
 }
 
