@@ -158,22 +158,28 @@ __global__ __launch_bounds__(256) void ln_mod_bwd_kernel(LnModParams p) {
 // Elementwise over an [N, C] view, 8 elements per thread (C % 8 == 0).
 // op 0: y = x + g * b (x may be null: y = g * b);  1: y = gelu(b);
 // op 2: y = x * gelu'(b) (x = upstream gradient);  3: y = silu(b)
-// gelu(u) = u/2 * (1 + tanh(k0 * (u + k1 u^3))), tanh(z) = 1 - 2/(1 + e^{2z})
+// gelu(u) = u/2 * (1 + tanh(z)), z = k0 * (u + k1 u^3), evaluated as
+// u * sigmoid(2z) (the same function: (1 + tanh z) / 2 = sigmoid(2z)) with one
+// exp2 and one reciprocal; gelu'(u) = sg + 2 u sg (1 - sg) k0 (1 + 3 k1 u^2),
+// sg = sigmoid(2z).
 constexpr float kGeluK0 = 0.7978845608028654f;  // sqrt(2/pi)
 constexpr float kGeluK1 = 0.044715f;
 
-__device__ __forceinline__ float tanh_via_exp(float z) {
-    return 1.f - 2.f / (1.f + exp2_fast(2.f * kLog2e * z));
+// sigmoid(2 k0 (u + k1 u^3)) of the tanh-GELU
+__device__ __forceinline__ float gelu_sigmoid(float u) {
+    const float z2 = (2.f * kGeluK0) * (u + kGeluK1 * u * u * u);
+    return __builtin_amdgcn_rcpf(1.f + exp2_fast(-kLog2e * z2));
 }
 
+// Grid: x over 128-lane groups of a row's 8-element chunks, y over rows
+// (striding by gridDim.y), so no lane divides to find its row.
+constexpr int kEltLanes = 128;
 template <typename T, int OP>
-__global__ __launch_bounds__(256) void elementwise_kernel(EltParams p) {
-    const int64_t per_row = p.C / 8;
-    const int64_t total = (int64_t)p.N * per_row;
+__global__ __launch_bounds__(kEltLanes) void elementwise_kernel(EltParams p) {
+    const int e = (blockIdx.x * kEltLanes + threadIdx.x) * 8;
+    if (e >= p.C) return;
     const T *g = static_cast<const T *>(p.g);
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-        const int64_t row = i / per_row;
-        const int e = (int)(i - row * per_row) * 8;
+    for (int64_t row = blockIdx.y; row < p.N; row += gridDim.y) {
         float bv[8], o[8];
         load8(static_cast<const T *>(p.b) + row * p.ldb + e, bv);
         if constexpr (OP == 0) {
@@ -189,18 +195,15 @@ __global__ __launch_bounds__(256) void elementwise_kernel(EltParams p) {
             for (int j = 0; j < 8; ++j) o[j] = xv[j] + gv[j] * bv[j];
         } else if constexpr (OP == 1) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float u = bv[j];
-                o[j] = 0.5f * u * (1.f + tanh_via_exp(kGeluK0 * (u + kGeluK1 * u * u * u)));
-            }
+            for (int j = 0; j < 8; ++j) o[j] = bv[j] * gelu_sigmoid(bv[j]);
         } else if constexpr (OP == 2) {
             float xv[8];
             load8(static_cast<const T *>(p.x) + row * p.ldx + e, xv);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float u = bv[j];
-                const float t = tanh_via_exp(kGeluK0 * (u + kGeluK1 * u * u * u));
-                const float d = 0.5f * (1.f + t) + 0.5f * u * (1.f - t * t) * kGeluK0 * (1.f + 3.f * kGeluK1 * u * u);
+                const float sg = gelu_sigmoid(u);
+                const float d = sg + (2.f * kGeluK0) * u * (sg - sg * sg) * (1.f + (3.f * kGeluK1) * u * u);
                 o[j] = xv[j] * d;
             }
         } else {
@@ -324,7 +327,13 @@ hipError_t launch_ln_mod_bwd(const LnModParams &p, int dtype, hipStream_t s) {
 
 template <typename T>
 static hipError_t elt_t(const EltParams &p, int op, hipStream_t s) {
-    const dim3 grid(elt_grid((int64_t)p.N * (p.C / 8))), block(256);
+    const unsigned gx = (unsigned)((p.C / 8 + kEltLanes - 1) / kEltLanes);
+    // about 64K workgroups in all; at most 65535 row groups
+    int64_t gy = ((int64_t)1 << 16) / gx;
+    if (gy > p.N) gy = p.N;
+    if (gy > 65535) gy = 65535;
+    if (gy < 1) gy = 1;
+    const dim3 grid(gx, (unsigned)gy), block(kEltLanes);
     switch (op) {
         case 0: hipLaunchKernelGGL((elementwise_kernel<T, 0>), grid, block, 0, s, p); break;
         case 1: hipLaunchKernelGGL((elementwise_kernel<T, 1>), grid, block, 0, s, p); break;

@@ -212,6 +212,10 @@ def adamw_step_many(items, step: int, lr: float = 1e-3, betas=(0.9, 0.999), eps:
 LORA_TARGETS = ("q", "k", "v", "out")
 QKV = ("q", "k", "v")
 STREAMS = ("txt", "img")  # joint order: txt first (throughput.rs:545-547)
+# Host issue order of the two streams' ops between the joint attention calls:
+# img's rows (8x txt's at c4) are the critical path, so its launches go first
+# and the GPU starts on them while the host issues txt's on the side stream.
+ISSUE_ORDER = ("img", "txt")
 
 
 @dataclass
@@ -272,9 +276,27 @@ class DoubleBlockLoRA:
                  img_rows: int, img_cols: int, axes: Sequence[int] = (16, 56, 56), theta: float = 1e4,
                  lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
                  tuned_gemms: bool = True, batch_qkv_adapters: bool = True, mlp: str = "gelu",
-                 positions: Optional[np.ndarray] = None):
+                 positions: Optional[np.ndarray] = None, dx_weights_t: bool = True,
+                 fold_qkv_adapters: bool = True):
         """positions: [S, n_axes] RoPE position ids of the joint sequence (txt
-        rows first); None gives txt (l, 0, 0), img (0, r, c)."""
+        rows first); None gives txt (l, 0, 0), img (0, r, c).
+
+        dx_weights_t: keep a transposed copy of each frozen linear weight, so
+        that the backward's dX = dY W reads W with the contraction dimension
+        contiguous, the operand layout the library GEMMs run fastest on (the
+        forward's x W^T already reads it that way).  Costs one more copy of
+        the frozen weights (12 C^2 values per stream for the GELU MLP); call
+        refresh_frozen() after changing a frozen weight.
+
+        fold_qkv_adapters (with the batched q/k/v adapters): the three
+        adapters ride in the frozen qkv GEMM, as ADAPTER_PAD extra columns of
+        its weight [W_qkv | B_blk | 0], B_blk [3C, 3r] block-diagonal with
+        B_q, B_k, B_v.  Forward: [h | s u | 0] [W_qkv | B_blk | 0]^T = h W_qkv^T
+        + s u_j B_j^T for each of q, k, v, in one GEMM (no separate up
+        projections).  Backward with the input gradient: dY [W_qkv | B_blk | 0]
+        = [dY W_qkv | t | 0], t_j = dY_j B_j, in one GEMM (no separate
+        t_j products).  Each output is one f32 sum rounded once, where the
+        unfolded path rounds the base product and the adapter sum apart."""
         if mlp not in ("gelu", "swiglu"):
             raise ValueError(f"mlp must be 'gelu' or 'swiglu', not {mlp!r}")
         self.w = weights
@@ -310,6 +332,7 @@ class DoubleBlockLoRA:
         self.step_count = 0
         self._buf = None
         self._side = torch.cuda.Stream(device=self.device) if overlap_streams else None
+        self._wt = {name: {} for name in STREAMS} if dx_weights_t else None
         if tuned_gemms and self.dtype == torch.bfloat16:
             gemm_tuning.enable()
         ranks = {int(a.shape[0]) for w in weights.values() for a in w.lora_a.values()}
@@ -337,7 +360,50 @@ class DoubleBlockLoRA:
                 bt = torch.empty((3, r, b.shape[1]), dtype=a.dtype, device=a.device)
                 self._b_qkv_t[name] = bt
                 self._b_t[name] = {t: bt[j] for j, t in enumerate(QKV)}
+        self._fold = self._batched and fold_qkv_adapters and 3 * self.rank <= ADAPTER_PAD
+        if self._fold:
+            C, r, P = self.C, self.rank, ADAPTER_PAD
+            kw = dict(dtype=self.dtype, device=self.device)
+            self._qkv_ext, self._qkv_ext_t, self._bview, self._bview_t = {}, {}, {}, {}
+            for name in STREAMS:
+                ext = torch.zeros((3 * C, C + P), **kw)  # [W_qkv | B_blk | 0]
+                self._qkv_ext[name] = ext
+                # B_j [C, r] at rows jC.., columns C + jr..: one strided [3, C, r] view
+                self._bview[name] = ext.as_strided((3, C, r), (C * (C + P) + r, C + P, 1), C)
+                if self._wt is not None:  # its transpose [C + P, 3C], the backward's operand
+                    ext_t = torch.zeros((C + P, 3 * C), **kw)
+                    self._qkv_ext_t[name] = ext_t
+                    self._bview_t[name] = ext_t.as_strided((3, C, r), (3 * C * r + C, 1, 3 * C), 3 * C * C)
+        self.refresh_frozen()
+        if self._batched:
             self.refresh_adapters()
+
+    def refresh_frozen(self) -> None:
+        """Re-derive the transposed frozen weights the backward reads (with
+        dx_weights_t), in place."""
+        C = self.C
+        for name in STREAMS:
+            if self._fold:
+                self._qkv_ext[name][:, :C].copy_(self.w[name].w_qkv)
+                if self._wt is not None:
+                    self._qkv_ext_t[name][:C].copy_(self.w[name].w_qkv.t())
+        if self._wt is None:
+            return
+        for name in STREAMS:
+            w = self.w[name]
+            for key in ("w_out", "w1", "w2") if self._fold else ("w_qkv", "w_out", "w1", "w2"):
+                src = getattr(w, key)
+                dst = self._wt[name].get(key)
+                if dst is None or dst.shape != (src.shape[1], src.shape[0]):
+                    self._wt[name][key] = src.t().contiguous()
+                else:
+                    dst.copy_(src.t())
+
+    def _dx_weight(self, name: str, key: str) -> torch.Tensor:
+        """W of stream `name` as the right operand of dX = dY W."""
+        if self._wt is None:
+            return getattr(self.w[name], key)
+        return self._wt[name][key].t()
 
     def refresh_adapters(self) -> None:
         """Re-derive what the batched adapter products read from the LoRA
@@ -361,6 +427,10 @@ class DoubleBlockLoRA:
                     w.lora_b[t] = b[j]
             self._a_qkv_t[name].copy_(a.t())
             self._b_qkv_t[name].copy_(b.transpose(1, 2))
+            if self._fold:
+                self._bview[name].copy_(b)
+                if self._wt is not None:
+                    self._bview_t[name].copy_(b)
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
@@ -391,6 +461,10 @@ class DoubleBlockLoRA:
                                    ("t2", C), ("dx1", C), ("dx", C), ("pre", F), ("act", FA), ("dact", FA),
                                    ("dpre", F), ("mlp", C), ("su", R), ("tq", R)):
                     b[f"{key}.{name}"] = torch.empty((n, width), **kw)
+                if self._fold:
+                    # [h | s u | 0]: the padding columns stay zero
+                    b[f"hx.{name}"] = torch.zeros((n, C + ADAPTER_PAD), **kw)
+                    b[f"dhx.{name}"] = torch.empty((n, C + ADAPTER_PAD), **kw)
             self._buf = b
         return self._buf
 
@@ -437,9 +511,18 @@ class DoubleBlockLoRA:
         all four Q / K segments follows in one launch, _prologue_fwd)."""
         B, C, H, D, s = self._buf, self.C, self.H, self.D, self.lora_scale
         w, off, n = self.w[name], self.offset[name], self.rows[name]
+        rows = B["qkv"][off:off + n]
+        if self._fold:
+            hx, r = B[f"hx.{name}"], self.rank
+            h, mean1, rstd1 = ln_mod_fwd(x[name], w.mod[0], w.mod[1], self.eps, out=hx[:, :C], stats=True)
+            saved[(name, "ln1")] = (mean1, rstd1)
+            lora_down(h, self._a_qkv[name], s, out=hx[:, C:C + 3 * r])  # s h A_qkv^T
+            _linear(hx, self._qkv_ext[name], w.b_qkv, rows)
+            if self.capture is not None:
+                self.capture[f"{name}_norm1"] = h.clone()
+            return
         h, mean1, rstd1 = ln_mod_fwd(x[name], w.mod[0], w.mod[1], self.eps, out=B[f"h.{name}"], stats=True)
         saved[(name, "ln1")] = (mean1, rstd1)
-        rows = B["qkv"][off:off + n]
         _linear(h, w.w_qkv, w.b_qkv, rows)
         if self._batched:
             r = self.rank
@@ -506,17 +589,17 @@ class DoubleBlockLoRA:
             return
         # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
         dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
-        dact = torch.mm(dmlp, w.w2, out=B[f"dact.{name}"])
+        dact = torch.mm(dmlp, self._dx_weight(name, "w2"), out=B[f"dact.{name}"])
         if self.mlp == "swiglu":
             dpre = B[f"dpre.{name}"]
             swiglu_bwd(dact, pre[:, :M], pre[:, M:], dgate=dpre[:, :M], dup=dpre[:, M:])
         else:
             dpre = gelu_bwd(dact, pre, out=dact)
-        dh2 = torch.mm(dpre, w.w1, out=B[f"t2.{name}"])
+        dh2 = torch.mm(dpre, self._dx_weight(name, "w1"), out=B[f"t2.{name}"])
         dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
         dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
         do_rows = B["do"][0, off:off + n].reshape(n, C)
-        torch.mm(dout, w.w_out, out=do_rows)
+        torch.mm(dout, self._dx_weight(name, "w_out"), out=do_rows)
         if u_out is not None:
             saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
                                                     dx=do_rows)
@@ -527,13 +610,25 @@ class DoubleBlockLoRA:
         B, C, H, D, s = self._buf, self.C, self.H, self.D, self.lora_scale
         w, off, n = self.w[name], self.offset[name], self.rows[name]
         drows = B["dqkv"][off:off + n]
-        h = B[f"h.{name}"]
-        dh = torch.mm(drows, w.w_qkv, out=B[f"t2.{name}"]) if want_dx else None
+        r = self.rank
+        if self._fold:
+            hx = B[f"hx.{name}"]
+            h, su = hx[:, :C], hx[:, C:C + 3 * r]
+        else:
+            h, su = B[f"h.{name}"], B[f"su.{name}"]
+        if self._fold and want_dx:
+            # dY [W_qkv | B_blk | 0] = [dh | t | 0]
+            dhx = B[f"dhx.{name}"]
+            rhs = self._qkv_ext_t[name].t() if self._wt is not None else self._qkv_ext[name]
+            torch.mm(drows, rhs, out=dhx)
+            dh, tq = dhx[:, :C], dhx[:, C:C + 3 * r]
+        else:
+            dh = torch.mm(drows, self._dx_weight(name, "w_qkv"), out=B[f"t2.{name}"]) if want_dx else None
+            tq = B[f"tq.{name}"] if self._batched else None
         if self._batched:
-            r = self.rank
-            su, tq = B[f"su.{name}"], B[f"tq.{name}"]
-            for j, t in enumerate(QKV):  # t_j = dy_j B_j
-                lora_down(drows[:, j * C:(j + 1) * C], self._b_t[name][t], 1.0, out=tq[:, j * r:(j + 1) * r])
+            if not (self._fold and want_dx):
+                for j, t in enumerate(QKV):  # t_j = dy_j B_j
+                    lora_down(drows[:, j * C:(j + 1) * C], self._b_t[name][t], 1.0, out=tq[:, j * r:(j + 1) * r])
             if dh is not None:
                 lora_up(tq, self._a_qkv_t[name], dh, s)  # dh += s t A_qkv
             da = lora_grad(tq, h, s, transpose=False)  # [3r, C] = s t^T h
@@ -558,7 +653,7 @@ class DoubleBlockLoRA:
         main = torch.cuda.current_stream(self.device)
         saved, y, grads = {}, {}, {}
         self._fork()
-        for name in STREAMS:
+        for name in ISSUE_ORDER:
             with self._on(name):
                 self._qkv_phase(name, x, saved)
         self._join()
@@ -573,7 +668,7 @@ class DoubleBlockLoRA:
             self.capture["attn_in.q"], self.capture["attn_in.k"] = B["q"][0].clone(), B["k"][0].clone()
             self.capture["attn_in.v"], self.capture["attn"] = v[0].clone(), o_t[0].clone()
         self._fork()
-        for name in STREAMS:
+        for name in ISSUE_ORDER:
             with self._on(name):
                 self._out_phase(name, x, dy, o_t, y, saved)
         self._join()
@@ -588,7 +683,7 @@ class DoubleBlockLoRA:
                 self.capture[key] = t[0].clone()
         qk_prologue_bwd_multi(self._prologue_segments(True), self.eps)
         self._fork()
-        for name in STREAMS:
+        for name in ISSUE_ORDER:
             with self._on(name):
                 self._qkv_bwd_phase(name, x, want_dx, saved, grads)
         self._join()
@@ -625,10 +720,10 @@ class DoubleBlockLoRA:
 
 def random_block(dim: int, heads: int, txt_tokens: int, img_rows: int, img_cols: int, mlp_ratio: int = 4,
                  rank: int = 16, alpha: float = 16.0, dtype=torch.bfloat16, device="cuda", seed: int = 20261028,
-                 axes=(16, 56, 56), theta: float = 1e4) -> DoubleBlockLoRA:
+                 axes=(16, 56, 56), theta: float = 1e4, **block_kw) -> DoubleBlockLoRA:
     """c4-style random init: base W ~ N(0, 0.02) frozen, LoRA A ~ N(0, 1/r)
     (PEFT "gaussian"), B ~ N(0, 1e-3), QK-norm scales 1 + N(0, 0.02),
-    modulation W ~ N(0, 0.02)."""
+    modulation W ~ N(0, 0.02).  block_kw go to DoubleBlockLoRA."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     C, F = dim, mlp_ratio * dim
     D = dim // heads
@@ -649,7 +744,7 @@ def random_block(dim: int, heads: int, txt_tokens: int, img_rows: int, img_cols:
                 w.v[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
         ws[name] = w
     return DoubleBlockLoRA(ws, heads, D, txt_tokens, img_rows, img_cols, axes=axes, theta=theta,
-                           lora_scale=alpha / rank)
+                           lora_scale=alpha / rank, **block_kw)
 
 
 # ---------------------------------------------------------------------------
@@ -736,6 +831,8 @@ class SingleBlockLoRA:
             self.w_in_ext[:, :C] = weights.w_in
             self.w_out_ext = torch.zeros((C + P, C + M), **kw)          # [W_out; A_out; 0]
             self.w_out_ext[:C] = weights.w_out
+            self.a_in_t = torch.empty((C, self.r), **kw)    # A_in^T: the dx term's "B"
+            self.b_out_t = torch.empty((self.r, C), **kw)   # B_out^T: du_out = s dout B_out
             self.refresh_adapters()
 
     def refresh_adapters(self) -> None:
@@ -747,8 +844,9 @@ class SingleBlockLoRA:
         C, r, w = self.C, self.r, self.w
         self.w_in_ext[:, C:C + r].copy_(w.lora_b["to_in"])
         self.w_out_ext[C:C + r].copy_(w.lora_a["to_out"])
-        self.a_in_t = w.lora_a["to_in"].t().contiguous()     # [C, r]: the dx term's "B"
-        self.b_out_t = w.lora_b["to_out"].t().contiguous()   # [r, C]: du_out = s dout B_out
+        # copied in place: a captured step (GraphedTrainStep) reads these addresses
+        self.a_in_t.copy_(w.lora_a["to_in"].t())
+        self.b_out_t.copy_(w.lora_b["to_out"].t())
 
     def set_conditioning(self, c: torch.Tensor) -> None:
         """Modulation parts chunk3(silu(c) W_mod^T) (the Mod3 of throughput.rs:284-288)."""
@@ -917,3 +1015,40 @@ def random_single_block(dim: int, heads: int, txt_tokens: int, img_rows: int, im
             w.v[f"{t}.{part}"] = torch.zeros(shape, dtype=torch.float32, device=device)
     return SingleBlockLoRA(w, heads, D, txt_tokens, img_rows, img_cols, axes=axes, theta=theta,
                            lora_scale=alpha / rank)
+
+
+class GraphedTrainStep:
+    """train_step of a DoubleBlockLoRA or SingleBlockLoRA with its forward +
+    backward captured once into a HIP graph: one graph launch per step instead
+    of the ~115 (double) / ~35 (single) host launches, and the txt / img stream
+    fork and joins kept as graph edges.
+
+    - The graph reads the input tensors given here (x and dy): copy each
+      step's data into them (x["img"].copy_(...)) before the call.
+    - Its outputs (y, grads) are tensors of the graph's memory pool,
+      overwritten by the next call.
+    - AdamW and the adapter refresh run eagerly after each replay: their bias
+      corrections change with the step count.  They update the LoRA factors
+      in place, at the addresses the graph reads.
+    - The captured ops record no memset: the step's kernels and hipBLASLt
+      GEMMs write every element they later read.
+    """
+
+    def __init__(self, block, x, dy, want_dx: bool = True, warmup: int = 2):
+        self.block, self.x, self.dy = block, x, dy
+        cur = torch.cuda.current_stream(block.device)
+        side = torch.cuda.Stream(device=block.device)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):  # the block's buffers and GEMM handles, outside the capture
+            for _ in range(max(1, warmup)):
+                block.forward_backward(x, dy, want_dx=want_dx)
+        cur.wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.y, self.grads = block.forward_backward(x, dy, want_dx=want_dx)
+
+    def __call__(self, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8):
+        """One training step on the current contents of x and dy: (y, grads)."""
+        self.graph.replay()
+        self.block.apply_adamw(self.grads, lr, betas, eps)
+        return self.y, self.grads

@@ -418,6 +418,56 @@ def test_klein_single_block_step_properties():
             assert torch.isfinite(a).all() and float(a.abs().max()) > 0 and torch.equal(a, b), t
 
 
+def _flat(y, grads):
+    """Copies of a block step's outputs as a name -> tensor dict."""
+    out = {}
+    for k, v in (y.items() if isinstance(y, dict) else [("y", y)]):
+        out[("y", k)] = v.clone()
+    for k, v in grads.items():
+        for i, t in enumerate(v if isinstance(v, tuple) else (v,)):
+            out[(k, i)] = t.clone()
+    return out
+
+
+@pytest.mark.parametrize("kind", ["double", "single"])
+def test_graphed_train_step_replays_match_eager(kind):
+    """GraphedTrainStep (forward + backward captured in one HIP graph): three
+    replays with an AdamW step between them (the LoRA factors and the
+    adapter operands the graph reads change every step) each give the bits
+    of an eager forward_backward on the same factors, run right after the
+    replay with a synchronisation between; calling the step replays and
+    applies AdamW."""
+    bf = torch.bfloat16
+    if kind == "double":
+        case = oracle_mods(make_case(C=256, H=2, T=16, rows=4, cols=8, r=4, bf16=True, seed=5))
+        blk = device_block(case, bf)
+        x = {k: dev(v, bf) for k, v in case["x"].items()}
+        dy = {k: dev(v, bf) for k, v in case["dy"].items()}
+    else:
+        sc = single_oracle_mods(make_single_case(C=256, H=2, T=40, rows=8, cols=12, r=4, bf16=True, seed=9))
+        blk = device_single_block(sc, bf)
+        x, dy = dev(sc["x"], bf), dev(sc["dy"], bf)
+    gs = fb.GraphedTrainStep(blk, x, dy, want_dx=True)
+    for i in range(3):
+        gs.graph.replay()
+        torch.cuda.synchronize()
+        got = _flat(gs.y, gs.grads)
+        want = _flat(*blk.forward_backward(x, dy, want_dx=True))
+        torch.cuda.synchronize()
+        assert got.keys() == want.keys()
+        for k in got:
+            assert torch.equal(got[k], want[k]), (i, k)
+        grads = {k: v for k, v in gs.grads.items()}
+        blk.apply_adamw(grads)
+    before = blk.step_count
+    a_before = (blk.w["img"] if kind == "double" else blk.w).lora_a["q" if kind == "double" else "to_in"].clone()
+    gs()
+    torch.cuda.synchronize()
+    assert blk.step_count == before + 1
+    a_after = (blk.w["img"] if kind == "double" else blk.w).lora_a["q" if kind == "double" else "to_in"]
+    assert not torch.equal(a_before, a_after)
+
+
 def test_tuned_gemm_file_loads_and_tuned_shapes_stay_accurate():
     """The packaged TunableOp file (solutions measured on MI355X for the block
     GEMM shapes) loads read-only on this image, and a tuned shape (the txt
