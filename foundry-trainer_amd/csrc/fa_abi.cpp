@@ -753,25 +753,80 @@ fa_status fa_lora_up(const fa_lora_up_args *a, void *stream) {
     return ok();
 }
 
-size_t fa_lora_grad_workspace_size(const fa_lora_grad_args *a) {
-    if (!a || a->tokens < 1 || a->features < 1) return 0;
-    return fa::lora_grad_workspace_bytes(a->tokens, a->features);
+static fa::LoraGradItem grad_item(const fa_lora_grad_args *a) {
+    fa::LoraGradItem it{};
+    it.u = a->u;
+    it.ldu = a->ldu;
+    it.x = a->x;
+    it.ldx = a->ldx;
+    it.C = a->features;
+    it.R = a->rank;
+    it.scale = a->scale;
+    it.grad = a->grad;
+    it.transpose = a->transpose != 0;
+    return it;
 }
 
-fa_status fa_lora_grad(const fa_lora_grad_args *a, void *stream) {
+static fa_status check_lora_grad(const fa_lora_grad_args *a) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
     FA_TRY(check_lora_part(a->dtype, a->tokens, a->features, a->rank, a->scale, "features"));
     FA_TRY(check_rank_view("u", a->u, a->ldu, a->rank));
     if (!a->x || !aligned(a->x, 16) || a->ldx < a->features || (a->ldx * 2) % 16)
         return fail(FA_ERR_INVALID_ARG, "x is NULL, misaligned, or ldx < features");
     if (!a->grad || !aligned(a->grad, 4)) return fail(FA_ERR_INVALID_ARG, "grad is NULL or misaligned");
-    const size_t need = fa::lora_grad_workspace_bytes(a->tokens, a->features);
+    return FA_OK;
+}
+
+size_t fa_lora_grad_workspace_size(const fa_lora_grad_args *a) {
+    if (!a || a->tokens < 1 || a->features < 1 || a->rank < 1 || a->rank > 64) return 0;
+    const fa::LoraGradItem it = grad_item(a);
+    return fa::lora_grad_many_workspace_bytes(&it, 1, a->tokens);
+}
+
+fa_status fa_lora_grad(const fa_lora_grad_args *a, void *stream) {
+    FA_TRY(check_lora_grad(a));
+    const fa::LoraGradItem it = grad_item(a);
+    const size_t need = fa::lora_grad_many_workspace_bytes(&it, 1, a->tokens);
     if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < need)
         return fail(FA_ERR_INVALID_ARG, "workspace is NULL, not 256-byte aligned, or smaller than %zu bytes", need);
     FA_TRY(init_current());
-    const hipError_t e = fa::launch_lora_grad_bf16(a->u, a->ldu, a->x, a->ldx, a->tokens, a->features, a->rank,
-                                                   a->scale, a->grad, a->transpose != 0, a->workspace,
-                                                   static_cast<hipStream_t>(stream));
+    const hipError_t e = fa::launch_lora_grad_many_bf16(&it, 1, a->tokens, a->workspace,
+                                                        static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lora grad launch");
+    return ok();
+}
+
+static constexpr int32_t kGradManyMax = 64;
+
+size_t fa_lora_grad_many_workspace_size(const fa_lora_grad_args *args, int32_t count) {
+    if (!args || count < 1 || count > kGradManyMax) return 0;
+    fa::LoraGradItem items[kGradManyMax];
+    for (int32_t i = 0; i < count; ++i) {
+        const fa_lora_grad_args &a = args[i];
+        if (a.tokens != args[0].tokens || a.tokens < 1 || a.features < 1 || a.rank < 1 || a.rank > 64) return 0;
+        items[i] = grad_item(&a);
+    }
+    return fa::lora_grad_many_workspace_bytes(items, count, args[0].tokens);
+}
+
+fa_status fa_lora_grad_many(const fa_lora_grad_args *args, int32_t count, void *workspace, size_t workspace_bytes,
+                            void *stream) {
+    if (!args || count < 1 || count > kGradManyMax)
+        return fail(FA_ERR_INVALID_ARG, "args is NULL or count not in 1..%d", kGradManyMax);
+    fa::LoraGradItem items[kGradManyMax];
+    for (int32_t i = 0; i < count; ++i) {
+        FA_TRY(check_lora_grad(&args[i]));
+        if (args[i].tokens != args[0].tokens)
+            return fail(FA_ERR_INVALID_ARG, "product %d: tokens %d differ from product 0's %d", i, args[i].tokens,
+                        args[0].tokens);
+        items[i] = grad_item(&args[i]);
+    }
+    const size_t need = fa::lora_grad_many_workspace_bytes(items, count, args[0].tokens);
+    if (!workspace || !aligned(workspace, 256) || workspace_bytes < need)
+        return fail(FA_ERR_INVALID_ARG, "workspace is NULL, not 256-byte aligned, or smaller than %zu bytes", need);
+    FA_TRY(init_current());
+    const hipError_t e = fa::launch_lora_grad_many_bf16(items, count, args[0].tokens, workspace,
+                                                        static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lora grad launch");
     return ok();
 }

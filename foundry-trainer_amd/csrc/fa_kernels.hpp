@@ -118,9 +118,19 @@ hipError_t launch_lora_down_bf16(const void *x, int64_t ldx, const void *a, int 
                                  void *u, int64_t ldu, hipStream_t st);
 hipError_t launch_lora_up_bf16(const void *u, int64_t ldu, const void *b, int N, int M, int R, float scale, void *y,
                                int64_t ldy, hipStream_t st);
-size_t lora_grad_workspace_bytes(int N, int C);
-hipError_t launch_lora_grad_bf16(const void *u, int64_t ldu, const void *x, int64_t ldx, int N, int C, int R,
-                                 float scale, float *grad, bool transpose, void *work, hipStream_t st);
+// grad = scale * u^T x ([R, C]) or its transpose ([C, R]); u bf16 [N, R <= 64]
+struct LoraGradItem {
+    const void *u;
+    int64_t ldu;
+    const void *x;
+    int64_t ldx;
+    int C, R;
+    float scale;
+    float *grad;
+    bool transpose;
+};
+size_t lora_grad_many_workspace_bytes(const LoraGradItem *items, int count, int N);
+hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int N, void *work, hipStream_t st);
 
 // LayerNorm-modulation over [N, C] rows (C % 8 == 0, C <= 4096).
 struct LnModParams {

@@ -410,6 +410,128 @@ __global__ void lora_colsum_reduce_kernel(const float *__restrict__ part, float 
     out[j * os_j + (int64_t)c * os_c] = s * acc;
 }
 
+// ---- colsum over several products in one set of launches -----------------
+// Products k = 0..count-1 of one token count N: out_k = s_k * U_k^T X_k (or
+// its transpose), U_k bf16 [N, R_k <= 64].  The same three steps as above,
+// each one launch for all products: U^T in operand order (rw = 32 or 64 rows),
+// split partials over [splits_k][C_k][rw] (R_k > 32: a second accumulator
+// over U^T rows 32..63 shares each X tile), fixed-order sum.  Per output the
+// arithmetic is that of the single-product kernels, so the same bits.
+constexpr int kGradMany = 8;
+struct GradProblem {
+    const bf16 *u;
+    int64_t ldu;
+    const bf16 *x;
+    int64_t ldx;
+    float *out;
+    int64_t os_j, os_c;
+    bf16 *ut;     // [rw][npad]
+    float *part;  // [splits][C][rw]
+    float s;
+    int C, R, rw, splits, chunk, tile0;
+};
+struct GradMany {
+    GradProblem p[kGradMany];
+    int count, N, npad;
+};
+
+__global__ void lora_ut_many_kernel(GradMany g) {
+    const GradProblem &q = g.p[blockIdx.y];
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= q.rw * g.npad) return;
+    const int j = e / g.npad, p = e - j * g.npad;
+    const int grp = p >> 4, r = p & 15;
+    const int n = grp * 16 + ((r & 4) ? 8 : 0) + ((r & 8) ? 4 : 0) + (r & 3);
+    q.ut[e] = j < q.R && n < g.N ? q.u[(int64_t)n * q.ldu + j] : (bf16)0.f;
+}
+
+__global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
+    int k = 0;
+    while (k + 1 < g.count && g.p[k + 1].tile0 <= (int)blockIdx.x) ++k;
+    const GradProblem &q = g.p[k];
+    if ((int)blockIdx.y >= q.splits) return;  // uniform over the workgroup
+    using T = LdsTile<128, kCsRows>;
+    constexpr int WI = T::WAVE_INSTS / 4;
+    __shared__ __align__(16) char st0[T::BYTES], st1[T::BYTES];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31, gh = lane >> 5;
+    const int C = q.C, N = g.N, npad = g.npad;
+    const int64_t ldx = q.ldx;
+    const int c0 = ((int)blockIdx.x - q.tile0) * kCsCols;
+    const int t_begin = blockIdx.y * q.chunk, t_end = min(t_begin + q.chunk, npad);
+    const bool two = q.rw == 64;
+    // rows >= N (and, in the last row, columns >= C) read as zero
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(q.x + c0, (uint32_t)(((int64_t)(N - 1) * ldx + (C - c0)) * 2));
+    const uint32_t xvo = tile_src_off<128>(wave, lane, ldx);
+    const uint32_t row_step = tile_inst_row_step<128>(ldx);
+    const uint32_t stage_step = (uint32_t)(kCsRows * ldx * 2);
+    auto issue = [&](int t0, char *dst) {
+#pragma unroll
+        for (int i = 0; i < WI; ++i)
+            buffer_to_lds_16(xrs, dst + (i * 4 + wave) * 1024, xvo, (uint32_t)(t0 / kCsRows) * stage_step + i * row_step);
+    };
+    uint32_t coff[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) coff[dt] = col_frag_off<128>(0, 0, dt, lane);
+    const bf16 *ub = q.ut + (int64_t)n * npad + gh * 8;
+    const bf16 *ub2 = ub + (int64_t)32 * npad;
+    f32x16 acc, acc2;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc[r] = 0.f;
+        acc2[r] = 0.f;
+    }
+    auto stage = [&](const char *tile, int t0) {
+#pragma unroll
+        for (int ks = 0; ks < kCsRows / 16; ++ks) {
+            const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
+                                               col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
+            const bf16x8 b = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
+            acc = mfma_32x32x16(a, b, acc);
+            if (two) {
+                const bf16x8 b2 = as_bf16x8(ld_global_16(ub2 + t0 + ks * 16));
+                acc2 = mfma_32x32x16(a, b2, acc2);
+            }
+        }
+    };
+    issue(t_begin, st0);
+    for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
+        barrier_keep_dma<0>();
+        if (t0 + kCsRows < t_end) issue(t0 + kCsRows, st1);
+        stage(st0, t0);
+        if (t0 + kCsRows < t_end) {
+            barrier_keep_dma<0>();
+            if (t0 + 2 * kCsRows < t_end) issue(t0 + 2 * kCsRows, st0);
+            stage(st1, t0 + kCsRows);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // acc element r: column c0 + wave*32 + acc_row(r, lane), j = n (acc2: j = 32 + n)
+    const int rw = q.rw;
+    float *pp = q.part + (int64_t)blockIdx.y * C * rw;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int c = c0 + wave * 32 + acc_row(r, lane);
+        if (c < C) {
+            pp[(int64_t)c * rw + n] = acc[r];
+            if (two) pp[(int64_t)c * rw + 32 + n] = acc2[r];
+        }
+    }
+}
+
+// out[j * os_j + c * os_c] = s * sum_sp part[sp][c][j] (fixed order), j < R.
+__global__ void lora_colsum_reduce_many_kernel(GradMany g) {
+    const GradProblem &q = g.p[blockIdx.y];
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)q.C * q.rw) return;
+    const int c = (int)(e / q.rw), j = (int)(e - (int64_t)c * q.rw);
+    if (j >= q.R) return;
+    float acc = 0.f;
+    for (int sp = 0; sp < q.splits; ++sp) acc += q.part[(int64_t)sp * q.C * q.rw + e];
+    q.out[j * q.os_j + (int64_t)c * q.os_c] = q.s * acc;
+}
+
 // Small transpose [R][C] -> [C][R] (dtype).
 template <typename T>
 __global__ void lora_transpose_kernel(const T *__restrict__ src, T *dst, int R, int C) {
@@ -607,25 +729,70 @@ hipError_t launch_lora_up_bf16(const void *u, int64_t ldu, const void *b, int N,
                              ldy, N, M, R, scale, st);
 }
 
-size_t lora_grad_workspace_bytes(int N, int C) {
-    return al256((size_t)32 * colsum_npad(N) * 2) + al256((size_t)colsum_splits(N, C) * C * 32 * 4);
+namespace {
+inline int grad_rows(int R) { return R > 32 ? 64 : 32; }
+inline size_t grad_item_bytes(int N, int C, int R) {
+    return al256((size_t)grad_rows(R) * colsum_npad(N) * 2) +
+           al256((size_t)colsum_splits(N, C) * C * grad_rows(R) * 4);
+}
+}  // namespace
+
+size_t lora_grad_many_workspace_bytes(const LoraGradItem *items, int count, int N) {
+    // sets of kGradMany products run one after another over the same bytes
+    size_t most = 0;
+    for (int k0 = 0; k0 < count; k0 += kGradMany) {
+        size_t b = 0;
+        for (int k = k0; k < count && k < k0 + kGradMany; ++k) b += grad_item_bytes(N, items[k].C, items[k].R);
+        most = b > most ? b : most;
+    }
+    return most;
 }
 
-hipError_t launch_lora_grad_bf16(const void *u, int64_t ldu, const void *x, int64_t ldx, int N, int C, int R,
-                                 float scale, float *grad, bool transpose, void *work, hipStream_t st) {
-    char *ws = static_cast<char *>(work);
-    bf16 *ut = reinterpret_cast<bf16 *>(ws);
-    float *part = reinterpret_cast<float *>(ws + al256((size_t)32 * colsum_npad(N) * 2));
-    // grad [R, C] (lora_a layout): element (j, c) at j * C + c; transposed [C, R]: c * R + j.
-    // The MFMA colsum covers 32 rank columns; R <= 64 runs as two passes over
-    // the same workspace, in stream order.
-    const bf16 *U = static_cast<const bf16 *>(u);
-    const int64_t os_j = transpose ? 1 : C, os_c = transpose ? R : 1;
-    hipError_t e = colsum_bf16<bf16>(U, ldu, static_cast<const bf16 *>(x), ldx, grad, os_j, os_c, N, C,
-                                     R < 32 ? R : 32, scale, ut, part, st);
-    if (e != hipSuccess || R <= 32) return e;
-    return colsum_bf16<bf16>(U + 32, ldu, static_cast<const bf16 *>(x), ldx, grad + 32 * os_j, os_j, os_c, N, C,
-                             R - 32, scale, ut, part, st);
+hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int N, void *work, hipStream_t st) {
+    const int npad = colsum_npad(N), stages = npad / kCsRows;
+    for (int k0 = 0; k0 < count; k0 += kGradMany) {
+        GradMany g{};
+        g.count = count - k0 < kGradMany ? count - k0 : kGradMany;
+        g.N = N;
+        g.npad = npad;
+        char *ws = static_cast<char *>(work);
+        int tiles = 0, max_splits = 1, max_out = 1;
+        for (int k = 0; k < g.count; ++k) {
+            const LoraGradItem &it = items[k0 + k];
+            GradProblem &q = g.p[k];
+            q.u = static_cast<const bf16 *>(it.u);
+            q.ldu = it.ldu;
+            q.x = static_cast<const bf16 *>(it.x);
+            q.ldx = it.ldx;
+            q.out = it.grad;
+            // grad [R, C] (lora_a layout): (j, c) at j * C + c; transposed [C, R]: c * R + j
+            q.os_j = it.transpose ? 1 : it.C;
+            q.os_c = it.transpose ? it.R : 1;
+            q.s = it.scale;
+            q.C = it.C;
+            q.R = it.R;
+            q.rw = grad_rows(it.R);
+            q.splits = colsum_splits(N, it.C);
+            q.chunk = (stages + q.splits - 1) / q.splits * kCsRows;
+            q.tile0 = tiles;
+            q.ut = reinterpret_cast<bf16 *>(ws);
+            ws += al256((size_t)q.rw * npad * 2);
+            q.part = reinterpret_cast<float *>(ws);
+            ws += al256((size_t)q.splits * it.C * q.rw * 4);
+            tiles += (it.C + kCsCols - 1) / kCsCols;
+            max_splits = q.splits > max_splits ? q.splits : max_splits;
+            max_out = it.C * q.rw > max_out ? it.C * q.rw : max_out;
+        }
+        hipLaunchKernelGGL(lora_ut_many_kernel, dim3((unsigned)((64 * npad + 255) / 256), (unsigned)g.count),
+                           dim3(256), 0, st, g);
+        hipLaunchKernelGGL(lora_colsum_many_kernel, dim3((unsigned)tiles, (unsigned)max_splits), dim3(256), 0, st,
+                           g);
+        hipLaunchKernelGGL(lora_colsum_reduce_many_kernel, dim3((unsigned)((max_out + 255) / 256), (unsigned)g.count),
+                           dim3(256), 0, st, g);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace fa

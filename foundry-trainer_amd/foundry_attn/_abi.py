@@ -30,6 +30,7 @@ EXPORTED = [
     "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
     "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step", "fa_adamw_step_many",
     "fa_lora_down", "fa_lora_up", "fa_lora_grad", "fa_lora_grad_workspace_size",
+    "fa_lora_grad_many", "fa_lora_grad_many_workspace_size",
 ]
 
 
@@ -227,6 +228,11 @@ def lib() -> ctypes.CDLL:
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
     L.fa_lora_grad_workspace_size.restype = ctypes.c_size_t
     L.fa_lora_grad_workspace_size.argtypes = [ctypes.POINTER(LoraGradArgs)]
+    L.fa_lora_grad_many.restype = ctypes.c_int
+    L.fa_lora_grad_many.argtypes = [ctypes.POINTER(LoraGradArgs), ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,
+                                    ctypes.c_void_p]
+    L.fa_lora_grad_many_workspace_size.restype = ctypes.c_size_t
+    L.fa_lora_grad_many_workspace_size.argtypes = [ctypes.POINTER(LoraGradArgs), ctypes.c_int32]
     L.fa_rope_tables_host.restype = ctypes.c_int
     L.fa_rope_tables_host.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_void_p, ctypes.c_float, ctypes.c_int32,

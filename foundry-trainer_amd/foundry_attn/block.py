@@ -42,6 +42,7 @@ import torch
 from . import _abi, gemm_tuning
 from ._abi import FoundryAttnError, check, lib
 from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_down, lora_fwd, lora_grad,
+                  lora_grad_many,
                   lora_up, qk_prologue_bwd_multi, qk_prologue_multi, rope_tables)
 
 
@@ -631,10 +632,12 @@ class DoubleBlockLoRA:
                     lora_down(drows[:, j * C:(j + 1) * C], self._b_t[name][t], 1.0, out=tq[:, j * r:(j + 1) * r])
             if dh is not None:
                 lora_up(tq, self._a_qkv_t[name], dh, s)  # dh += s t A_qkv
-            da = lora_grad(tq, h, s, transpose=False)  # [3r, C] = s t^T h
-            for j, t in enumerate(QKV):  # dB_j = dy_j^T (s u_j)
-                db = lora_grad(su[:, j * r:(j + 1) * r], drows[:, j * C:(j + 1) * C], 1.0, transpose=True)
-                grads[(name, t)] = (da[j * r:(j + 1) * r], db)
+            # dA_qkv [3r, C] = s t^T h and dB_j = dy_j^T (s u_j), one set of launches
+            da, *dbs = lora_grad_many([(tq, h, s, False)] +
+                                      [(su[:, j * r:(j + 1) * r], drows[:, j * C:(j + 1) * C], 1.0, True)
+                                       for j in range(len(QKV))])
+            for j, t in enumerate(QKV):
+                grads[(name, t)] = (da[j * r:(j + 1) * r], dbs[j])
         else:
             for j, t in enumerate(QKV):
                 if t in w.lora_a:
@@ -941,8 +944,7 @@ class SingleBlockLoRA:
             dout = gated_residual(None, g, dy, out=dout_ext[:, :C])
             du_out = lora_down(dout, self.b_out_t, s, out=dout_ext[:, C:C + r])
             torch.mm(dout_ext, self.w_out_ext, out=djoined)
-            grads = {"to_out": (lora_grad(du_out, joined, 1.0, transpose=False),
-                                lora_grad(u_out, dout, s, transpose=True))}
+            grads = {"to_out": tuple(lora_grad_many([(du_out, joined, 1.0, False), (u_out, dout, s, True)]))}
         else:
             dout = gated_residual(None, g, dy, out=B["dout"])
             torch.mm(dout, w.w_out, out=djoined)
@@ -965,8 +967,7 @@ class SingleBlockLoRA:
             else:
                 dnh = None
                 t_in = lora_down(dfused, w.lora_b["to_in"].t().contiguous(), 1.0, out=B["t_in"])
-            grads["to_in"] = (lora_grad(t_in, nh, s, transpose=False),
-                              lora_grad(su_in, dfused, 1.0, transpose=True))
+            grads["to_in"] = tuple(lora_grad_many([(t_in, nh, s, False), (su_in, dfused, 1.0, True)]))
         else:
             dnh = torch.mm(dfused, w.w_in, out=B["dnh"]) if want_dx else None
             grads["to_in"] = lora_bwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], u_in, dfused, s, dx=dnh)

@@ -524,10 +524,8 @@ def lora_up(u, b, y, scale: float):
     return y
 
 
-def lora_grad(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor] = None):
-    """f32 scale * u^T x: [r, C] (lora_a layout) or, with transpose, [C, r]
-    (lora_b layout).  u a bf16 [N, r] view, x [N, C] bf16 rows; `out`, when
-    given, a contiguous f32 tensor of that shape on x's device."""
+def _lora_grad_args(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor]):
+    """Validated LoraGradArgs (no workspace yet) and the f32 output tensor."""
     x = _rows(x, "x", torch.bfloat16)
     N, C = x.shape
     if u.dim() != 2:
@@ -545,8 +543,33 @@ def lora_grad(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor] =
         g = out
     args = _abi.LoraGradArgs(dtype=_dtype_code(x), tokens=N, features=C, rank=r, scale=float(scale), u=_ptr(u),
                              ldu=u.stride(0), x=_ptr(x), ldx=x.stride(0), grad=_ptr(g), transpose=int(transpose))
+    return args, g
+
+
+def lora_grad(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor] = None):
+    """f32 scale * u^T x: [r, C] (lora_a layout) or, with transpose, [C, r]
+    (lora_b layout).  u a bf16 [N, r] view, x [N, C] bf16 rows; `out`, when
+    given, a contiguous f32 tensor of that shape on x's device."""
+    args, g = _lora_grad_args(u, x, scale, transpose, out)
     need = lib().fa_lora_grad_workspace_size(ctypes.byref(args))
-    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=g.device)
     args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
-    check(lib().fa_lora_grad(ctypes.byref(args), _stream(x)))
+    check(lib().fa_lora_grad(ctypes.byref(args), _stream(g)))
     return g
+
+
+def lora_grad_many(items):
+    """Several lora_grad products of one token count in one set of launches:
+    items are (u, x, scale, transpose) or (u, x, scale, transpose, out); the
+    results (same bits as separate lora_grad calls) come back in order."""
+    if not items:
+        return []
+    built = [_lora_grad_args(*it[:4], it[4] if len(it) > 4 else None) for it in items]
+    dev = built[0][1].device
+    if any(g.device != dev for _, g in built):
+        raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "all products must be on one device")
+    arr = (_abi.LoraGradArgs * len(built))(*[a for a, _ in built])
+    need = lib().fa_lora_grad_many_workspace_size(arr, len(built))
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    check(lib().fa_lora_grad_many(arr, len(built), ws.data_ptr(), ws.numel(), _stream(built[0][1])))
+    return [g for _, g in built]

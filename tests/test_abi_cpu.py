@@ -361,6 +361,21 @@ def test_lora_pieces_validate_before_device_work():
     assert L.fa_lora_grad_workspace_size(ctypes.byref(gr)) > 0
     assert L.fa_lora_grad(ctypes.byref(gr), None) == _abi.FA_ERR_INVALID_ARG  # no workspace
     assert b"workspace" in L.fa_last_error()
+    # the grouped form: one workspace for all products, one token count
+    arr = (_abi.LoraGradArgs * 3)(*[_abi.LoraGradArgs.from_buffer_copy(gr) for _ in range(3)])
+    arr[1].rank, arr[2].transpose = 48, 1
+    need = L.fa_lora_grad_many_workspace_size(arr, 3)
+    assert need > L.fa_lora_grad_workspace_size(ctypes.byref(gr))
+    assert L.fa_lora_grad_many(arr, 3, None, 0, None) == _abi.FA_ERR_INVALID_ARG
+    assert b"workspace" in L.fa_last_error()
+    assert L.fa_lora_grad_many(arr, 3, _FAKE, need - 256, None) == _abi.FA_ERR_INVALID_ARG
+    assert L.fa_lora_grad_many(arr, 0, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
+    arr[2].tokens = 65
+    assert L.fa_lora_grad_many_workspace_size(arr, 3) == 0
+    assert L.fa_lora_grad_many(arr, 3, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
+    assert b"tokens" in L.fa_last_error()
+    arr[2].tokens, arr[1].rank = 64, 65
+    assert L.fa_lora_grad_many(arr, 3, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
 
 
 def test_public_headers_are_plain_c():

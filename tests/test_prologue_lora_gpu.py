@@ -266,6 +266,34 @@ def test_lora_pieces_strided_views(r):
     assert rel_l2(fused, ref) <= 1e-2
 
 
+def test_lora_grad_many_matches_separate_calls():
+    """fa_lora_grad_many: ten products of one token count (ranks 4..64, so
+    one- and two-accumulator products, dA and dB layouts, strided u and x
+    views, two sets of launches) give the bits of separate fa_lora_grad
+    calls, and one of them matches an f64 product of the same values."""
+    from foundry_attn.ops import lora_grad, lora_grad_many
+    rng = np.random.default_rng(321)
+    N, bf = 300, torch.bfloat16
+    rnd = oracle.bf16_round
+    items = []
+    for k, (r, C, tr) in enumerate([(4, 256, False), (16, 384, True), (40, 128, False), (48, 3072, True),
+                                     (64, 256, False), (12, 512, True), (33, 256, True), (16, 3072, False),
+                                     (8, 128, False), (64, 384, True)]):
+        ue = torch.zeros(N, r + 8, dtype=bf, device="cuda")
+        ue[:, 3:3 + r] = dev(rnd(rng.standard_normal((N, r)).astype(np.float32)), bf)
+        xe = torch.zeros(N, C + 16, dtype=bf, device="cuda")
+        xe[:, :C] = dev(rnd(rng.standard_normal((N, C)).astype(np.float32)), bf)
+        items.append((ue[:, 3:3 + r], xe[:, :C], 0.5 + 0.25 * k, tr))
+    many = lora_grad_many(items)
+    one = [lora_grad(*it) for it in items]
+    torch.cuda.synchronize()
+    for k, (a, b) in enumerate(zip(many, one)):
+        assert a.shape == b.shape and torch.equal(a, b), k
+    u, x, sc, tr = items[3]
+    want = sc * host(x).astype(np.float64).T @ host(u).astype(np.float64)  # [C, r]
+    np.testing.assert_allclose(host(many[3]), want, rtol=1e-4, atol=1e-3)
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_prologue_multi_matches_separate_calls(dtype):
     """fa_qk_prologue_fwd_multi / _bwd_multi: the block's four segments (Q
