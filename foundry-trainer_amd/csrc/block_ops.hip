@@ -292,6 +292,24 @@ __global__ __launch_bounds__(256) void adamw_many_kernel(AdamwMany p) {
         adamw_elem(w, p.grad[k], p.m[k], p.v[k], i, p);
 }
 
+// Strided 2D copies of several small arrays in one launch: view k owns
+// blocks [block0[k], block0[k + 1]) and strides over its rows * cols elements.
+template <typename E>
+__global__ __launch_bounds__(256) void copy2d_many_kernel(Copy2dMany p) {
+    const int b = blockIdx.x;
+    int k = 0;
+    while (k + 1 < p.count && p.block0[k + 1] <= b) ++k;
+    const int nb = p.block0[k + 1] - p.block0[k];
+    const int cols = p.cols[k];
+    const int64_t n = (int64_t)p.rows[k] * cols;
+    const E *src = static_cast<const E *>(p.src[k]);
+    E *dst = static_cast<E *>(p.dst[k]);
+    for (int64_t i = (int64_t)(b - p.block0[k]) * 256 + threadIdx.x; i < n; i += (int64_t)nb * 256) {
+        const int64_t r = i / cols, c = i - r * cols;
+        dst[r * p.dst_rs[k] + c * p.dst_cs[k]] = src[r * p.src_rs[k] + c * p.src_cs[k]];
+    }
+}
+
 inline int elt_grid(int64_t n8) {
     const int64_t blocks = (n8 + 255) / 256;
     return (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
@@ -372,6 +390,21 @@ hipError_t launch_adamw_many(AdamwMany p, int dtype, hipStream_t s) {
         hipLaunchKernelGGL((adamw_many_kernel<bf16>), grid, block, 0, s, p);
     else
         hipLaunchKernelGGL((adamw_many_kernel<float>), grid, block, 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy2d_many(Copy2dMany p, int elt_bytes, hipStream_t s) {
+    int blocks = 0;
+    for (int k = 0; k < p.count; ++k) {
+        p.block0[k] = blocks;
+        const int64_t nb = ((int64_t)p.rows[k] * p.cols[k] + 255) / 256;
+        blocks += (int)(nb < 256 ? nb : 256);
+    }
+    p.block0[p.count] = blocks;
+    if (elt_bytes == 2)
+        hipLaunchKernelGGL(copy2d_many_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(copy2d_many_kernel<uint32_t>, dim3(blocks), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -1054,6 +1054,42 @@ fa_status fa_adamw_step(const fa_adamw_args *a, void *stream) {
     return ok();
 }
 
+fa_status fa_copy2d_many(const fa_copy2d_args *args, int32_t count, void *stream) {
+    if (!args || count < 1) return fail(FA_ERR_INVALID_ARG, "args is NULL or count < 1");
+    for (int32_t i = 0; i < count; ++i) {
+        const fa_copy2d_args &a = args[i];
+        if (a.dtype != FA_DTYPE_BF16 && a.dtype != FA_DTYPE_F32)
+            return fail(FA_ERR_INVALID_ARG, "view %d: unknown dtype %d", i, a.dtype);
+        if (a.dtype != args[0].dtype) return fail(FA_ERR_INVALID_ARG, "view %d: dtype differs from view 0's", i);
+        if (a.rows < 1 || a.cols < 1) return fail(FA_ERR_INVALID_ARG, "view %d: rows and cols must be >= 1", i);
+        if (a.src_rs < 0 || a.src_cs < 0 || a.dst_rs < 0 || a.dst_cs < 0)
+            return fail(FA_ERR_INVALID_ARG, "view %d: strides must be >= 0", i);
+        const size_t eb = dtype_bytes(a.dtype);
+        if (!a.src || !a.dst || !aligned(a.src, eb) || !aligned(a.dst, eb))
+            return fail(FA_ERR_INVALID_ARG, "view %d: src or dst is NULL or misaligned", i);
+    }
+    FA_TRY(init_current());
+    for (int32_t k0 = 0; k0 < count; k0 += fa::kCopyMany) {
+        fa::Copy2dMany p{};
+        p.count = count - k0 < fa::kCopyMany ? count - k0 : fa::kCopyMany;
+        for (int k = 0; k < p.count; ++k) {
+            const fa_copy2d_args &a = args[k0 + k];
+            p.src[k] = a.src;
+            p.dst[k] = a.dst;
+            p.src_rs[k] = a.src_rs;
+            p.src_cs[k] = a.src_cs;
+            p.dst_rs[k] = a.dst_rs;
+            p.dst_cs[k] = a.dst_cs;
+            p.rows[k] = a.rows;
+            p.cols[k] = a.cols;
+        }
+        const hipError_t e = fa::launch_copy2d_many(p, (int)dtype_bytes(args[0].dtype),
+                                                    static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail(e, "copy launch");
+    }
+    return ok();
+}
+
 fa_status fa_adamw_step_many(const fa_adamw_args *args, int32_t count, void *stream) {
     if (!args || count < 1) return fail(FA_ERR_INVALID_ARG, "args is NULL or count < 1");
     for (int32_t i = 0; i < count; ++i) {

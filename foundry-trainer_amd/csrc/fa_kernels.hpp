@@ -190,6 +190,19 @@ struct AdamwParams {
 };
 hipError_t launch_adamw(const AdamwParams &p, int dtype, hipStream_t s);
 
+// Up to kCopyMany strided 2D views copied in one launch (strides in
+// elements); block0 is filled by the launcher.
+constexpr int kCopyMany = 32;
+struct Copy2dMany {
+    const void *src[kCopyMany];
+    void *dst[kCopyMany];
+    int64_t src_rs[kCopyMany], src_cs[kCopyMany], dst_rs[kCopyMany], dst_cs[kCopyMany];
+    int rows[kCopyMany], cols[kCopyMany];
+    int block0[kCopyMany + 1];
+    int count;
+};
+hipError_t launch_copy2d_many(Copy2dMany p, int elt_bytes, hipStream_t s);
+
 // Up to kAdamwMany tensors of one step (shared hyperparameters); block0 is
 // filled by the launcher.
 constexpr int kAdamwMany = 32;

@@ -28,7 +28,7 @@ EXPORTED = [
     "fa_lora_fwd", "fa_lora_bwd_workspace_size", "fa_lora_bwd",
     # include/foundry_block.h
     "fa_ln_mod_fwd", "fa_ln_mod_bwd", "fa_gated_residual", "fa_gelu_fwd", "fa_gelu_bwd", "fa_silu",
-    "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step", "fa_adamw_step_many",
+    "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step", "fa_adamw_step_many", "fa_copy2d_many",
     "fa_lora_down", "fa_lora_up", "fa_lora_grad", "fa_lora_grad_workspace_size",
     "fa_lora_grad_many", "fa_lora_grad_many_workspace_size",
 ]
@@ -178,6 +178,14 @@ class AdamwArgs(ctypes.Structure):
     ]
 
 
+class Copy2dArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+        ("src", ctypes.c_void_p), ("src_rs", ctypes.c_int64), ("src_cs", ctypes.c_int64),
+        ("dst", ctypes.c_void_p), ("dst_rs", ctypes.c_int64), ("dst_cs", ctypes.c_int64),
+    ]
+
+
 _lib = None
 
 
@@ -210,6 +218,8 @@ def lib() -> ctypes.CDLL:
     L.fa_qk_prologue_bwd_multi.argtypes = [ctypes.POINTER(QkPrologueBwdArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_adamw_step_many.restype = ctypes.c_int
     L.fa_adamw_step_many.argtypes = [ctypes.POINTER(AdamwArgs), ctypes.c_int32, ctypes.c_void_p]
+    L.fa_copy2d_many.restype = ctypes.c_int
+    L.fa_copy2d_many.argtypes = [ctypes.POINTER(Copy2dArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_attn_bwd_phase.restype = ctypes.c_int
     L.fa_attn_bwd_phase.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_int32, ctypes.c_void_p]
     L.fa_attn_fwd_workspace_size.restype = ctypes.c_size_t

@@ -207,6 +207,31 @@ def adamw_step_many(items, step: int, lr: float = 1e-3, betas=(0.9, 0.999), eps:
     check(lib().fa_adamw_step_many(arr, len(items), _stream(items[0][0])))
 
 
+def copy2d_many(pairs):
+    """dst.copy_(src) for several (src, dst) pairs of 2-D views of one dtype
+    (any strides, no overlaps) in one launch per 32 views (fa_copy2d_many)."""
+    pairs = list(pairs)
+    if not pairs:
+        return
+    dev = pairs[0][1].device
+    if dev.type == "cpu":
+        # a block built in host memory only to read or write adapter files
+        # (its compute ops refuse host tensors): plain host copies
+        for src, dst in pairs:
+            dst.copy_(src)
+        return
+    arr = (_abi.Copy2dArgs * len(pairs))()
+    for i, (src, dst) in enumerate(pairs):
+        if src.dim() != 2 or src.shape != dst.shape or src.dtype != dst.dtype or src.device != dev \
+                or dst.device != dev:
+            raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG, "copy2d_many: pairs of equal-shape 2-D views "
+                                                            "of one dtype on one device")
+        arr[i] = _abi.Copy2dArgs(dtype=_dtype_code(src), rows=src.shape[0], cols=src.shape[1], src=_ptr(src),
+                                 src_rs=src.stride(0), src_cs=src.stride(1), dst=_ptr(dst), dst_rs=dst.stride(0),
+                                 dst_cs=dst.stride(1))
+    check(lib().fa_copy2d_many(arr, len(pairs), _stream(pairs[0][1])))
+
+
 # ---------------------------------------------------------------------------
 # the block
 # ---------------------------------------------------------------------------
@@ -216,7 +241,12 @@ STREAMS = ("txt", "img")  # joint order: txt first (throughput.rs:545-547)
 # Host issue order of the two streams' ops between the joint attention calls:
 # img's rows (8x txt's at c4) are the critical path, so its launches go first
 # and the GPU starts on them while the host issues txt's on the side stream.
+# Under HIP-graph capture there is no host issue time to hide, and the graph
+# dispatches its nodes in capture order: txt's short ops go first there, so
+# that img's long GEMMs do not hold every CU while txt's wait (measured at c4:
+# about 30 us per replay).
 ISSUE_ORDER = ("img", "txt")
+CAPTURE_ORDER = ("txt", "img")
 
 
 @dataclass
@@ -297,7 +327,11 @@ class DoubleBlockLoRA:
         projections).  Backward with the input gradient: dY [W_qkv | B_blk | 0]
         = [dY W_qkv | t | 0], t_j = dY_j B_j, in one GEMM (no separate
         t_j products).  Each output is one f32 sum rounded once, where the
-        unfolded path rounds the base product and the adapter sum apart."""
+        unfolded path rounds the base product and the adapter sum apart.
+        With out adapters on both streams the out projection folds the same
+        way: a [W_out; A_out; 0]^T = [out | u | 0] (then out += s u B_out^T),
+        and [dout | s dout B_out | 0] [W_out; A_out; 0] = dout W_out + du A_out
+        gives dO."""
         if mlp not in ("gelu", "swiglu"):
             raise ValueError(f"mlp must be 'gelu' or 'swiglu', not {mlp!r}")
         self.w = weights
@@ -375,6 +409,17 @@ class DoubleBlockLoRA:
                     ext_t = torch.zeros((C + P, 3 * C), **kw)
                     self._qkv_ext_t[name] = ext_t
                     self._bview_t[name] = ext_t.as_strided((3, C, r), (3 * C * r + C, 1, 3 * C), 3 * C * C)
+        self._fold_out = self._fold and all("out" in weights[name].lora_a for name in STREAMS)
+        if self._fold_out:
+            C, r, P = self.C, self.rank, ADAPTER_PAD
+            kw = dict(dtype=self.dtype, device=self.device)
+            self._out_ext, self._out_ext_t, self._b_out_t, self._b_out_ext = {}, {}, {}, {}
+            for name in STREAMS:
+                self._out_ext[name] = torch.zeros((C + P, C), **kw)   # [W_out; A_out; 0]
+                if self._wt is not None:
+                    self._out_ext_t[name] = torch.zeros((C, C + P), **kw)
+                self._b_out_t[name] = torch.empty((r, C), **kw)       # B_out^T: du = s dout B_out
+                self._b_out_ext[name] = None if weights[name].b_out is None else torch.zeros(C + P, **kw)
         self.refresh_frozen()
         if self._batched:
             self.refresh_adapters()
@@ -384,15 +429,23 @@ class DoubleBlockLoRA:
         dx_weights_t), in place."""
         C = self.C
         for name in STREAMS:
+            w = self.w[name]
             if self._fold:
-                self._qkv_ext[name][:, :C].copy_(self.w[name].w_qkv)
+                self._qkv_ext[name][:, :C].copy_(w.w_qkv)
                 if self._wt is not None:
-                    self._qkv_ext_t[name][:C].copy_(self.w[name].w_qkv.t())
+                    self._qkv_ext_t[name][:C].copy_(w.w_qkv.t())
+            if self._fold_out:
+                self._out_ext[name][:C].copy_(w.w_out)
+                if self._wt is not None:
+                    self._out_ext_t[name][:, :C].copy_(w.w_out.t())
+                if w.b_out is not None:
+                    self._b_out_ext[name][:C].copy_(w.b_out)
         if self._wt is None:
             return
+        folded = (("w_qkv",) if self._fold else ()) + (("w_out",) if self._fold_out else ())
         for name in STREAMS:
             w = self.w[name]
-            for key in ("w_out", "w1", "w2") if self._fold else ("w_qkv", "w_out", "w1", "w2"):
+            for key in (k for k in ("w_qkv", "w_out", "w1", "w2") if k not in folded):
                 src = getattr(w, key)
                 dst = self._wt[name].get(key)
                 if dst is None or dst.shape != (src.shape[1], src.shape[0]):
@@ -408,14 +461,17 @@ class DoubleBlockLoRA:
 
     def refresh_adapters(self) -> None:
         """Re-derive what the batched adapter products read from the LoRA
-        factors: the stacked A_qkv and B_qkv, A_qkv^T (for dh += s t A_qkv)
-        and the B_j^T (for t_j = dy_j B_j), two copies per stream.
+        factors: the stacked A_qkv and B_qkv, A_qkv^T (for dh += s t A_qkv),
+        the B_j^T (for t_j = dy_j B_j) and, with folded adapters, the factor
+        columns of the qkv and out GEMM operands (and their transposes) -- in
+        one fa_copy2d_many launch for both streams.
         apply_adamw calls it; call it after changing lora_a / lora_b any other
         way (loading a LoRA file: a tensor assigned to lora_a[t] or lora_b[t]
         is copied into its stack and replaced by its view)."""
         if not self._batched:
             return
         r = self.rank
+        pairs = []
         for name in STREAMS:
             w, a, b = self.w[name], self._a_qkv[name], self._b_qkv[name]
             for j, t in enumerate(QKV):
@@ -426,12 +482,20 @@ class DoubleBlockLoRA:
                 if w.lora_b[t].data_ptr() != b[j].data_ptr():
                     b[j].copy_(w.lora_b[t])
                     w.lora_b[t] = b[j]
-            self._a_qkv_t[name].copy_(a.t())
-            self._b_qkv_t[name].copy_(b.transpose(1, 2))
-            if self._fold:
-                self._bview[name].copy_(b)
+            pairs.append((a.t(), self._a_qkv_t[name]))
+            for j in range(len(QKV)):
+                pairs.append((b[j].t(), self._b_qkv_t[name][j]))
+                if self._fold:
+                    pairs.append((b[j], self._bview[name][j]))
+                    if self._wt is not None:
+                        pairs.append((b[j], self._bview_t[name][j]))
+            if self._fold_out:
+                C = self.C
+                pairs.append((w.lora_a["out"], self._out_ext[name][C:C + r]))
                 if self._wt is not None:
-                    self._bview_t[name].copy_(b)
+                    pairs.append((w.lora_a["out"].t(), self._out_ext_t[name][:, C:C + r]))
+                pairs.append((w.lora_b["out"].t(), self._b_out_t[name]))
+        copy2d_many(pairs)  # one launch for every derived operand of both streams
 
     # -- conditioning: computed once per run (throughput.rs:936-938) -------
     def set_conditioning(self, c: torch.Tensor) -> None:
@@ -466,6 +530,9 @@ class DoubleBlockLoRA:
                     # [h | s u | 0]: the padding columns stay zero
                     b[f"hx.{name}"] = torch.zeros((n, C + ADAPTER_PAD), **kw)
                     b[f"dhx.{name}"] = torch.empty((n, C + ADAPTER_PAD), **kw)
+                if self._fold_out:
+                    b[f"ox.{name}"] = torch.empty((n, C + ADAPTER_PAD), **kw)   # [out | u | 0]
+                    b[f"dox.{name}"] = torch.zeros((n, C + ADAPTER_PAD), **kw)  # [dout | du | 0]
             self._buf = b
         return self._buf
 
@@ -571,8 +638,14 @@ class DoubleBlockLoRA:
         w, off, n = self.w[name], self.offset[name], self.rows[name]
         sh2, sc2, g1, g2 = w.mod[3], w.mod[4], w.mod[2], w.mod[5]
         a = o_t[0, off:off + n].reshape(n, C)
-        out = _linear(a, w.w_out, w.b_out, B[f"out.{name}"])
-        u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s) if "out" in w.lora_a else None
+        if self._fold_out:
+            ox, r = B[f"ox.{name}"], self.rank
+            _linear(a, self._out_ext[name], self._b_out_ext[name], ox)  # [out | u | 0]
+            out, u_out = ox[:, :C], ox[:, C:C + r]
+            lora_up(u_out, w.lora_b["out"], out, s)
+        else:
+            out = _linear(a, w.w_out, w.b_out, B[f"out.{name}"])
+            u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s) if "out" in w.lora_a else None
         x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
         h2, mean2, rstd2 = ln_mod_fwd(x1, sh2, sc2, self.eps, out=B[f"h2.{name}"], stats=True)
         pre = _linear(h2, w.w1, w.b1, B[f"pre.{name}"])
@@ -598,8 +671,17 @@ class DoubleBlockLoRA:
             dpre = gelu_bwd(dact, pre, out=dact)
         dh2 = torch.mm(dpre, self._dx_weight(name, "w1"), out=B[f"t2.{name}"])
         dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
-        dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
         do_rows = B["do"][0, off:off + n].reshape(n, C)
+        if self._fold_out:
+            dox, r = B[f"dox.{name}"], self.rank
+            dout = gated_residual(None, g1, dx1, out=dox[:, :C])
+            du = lora_down(dout, self._b_out_t[name], s, out=dox[:, C:C + r])  # s dout B_out
+            rhs = self._out_ext_t[name].t() if self._wt is not None else self._out_ext[name]
+            torch.mm(dox, rhs, out=do_rows)  # dout W_out + du A_out
+            # dA_out = du^T a, dB_out = s dout^T u
+            saved[(name, "out", "grad")] = tuple(lora_grad_many([(du, a, 1.0, False), (u_out, dout, s, True)]))
+            return
+        dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
         torch.mm(dout, self._dx_weight(name, "w_out"), out=do_rows)
         if u_out is not None:
             saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,
@@ -655,8 +737,9 @@ class DoubleBlockLoRA:
         C, S, H, D = self.C, self.S, self.H, self.D
         main = torch.cuda.current_stream(self.device)
         saved, y, grads = {}, {}, {}
+        order = CAPTURE_ORDER if torch.cuda.is_current_stream_capturing() else ISSUE_ORDER
         self._fork()
-        for name in ISSUE_ORDER:
+        for name in order:
             with self._on(name):
                 self._qkv_phase(name, x, saved)
         self._join()
@@ -671,7 +754,7 @@ class DoubleBlockLoRA:
             self.capture["attn_in.q"], self.capture["attn_in.k"] = B["q"][0].clone(), B["k"][0].clone()
             self.capture["attn_in.v"], self.capture["attn"] = v[0].clone(), o_t[0].clone()
         self._fork()
-        for name in ISSUE_ORDER:
+        for name in order:
             with self._on(name):
                 self._out_phase(name, x, dy, o_t, y, saved)
         self._join()
@@ -686,7 +769,7 @@ class DoubleBlockLoRA:
                 self.capture[key] = t[0].clone()
         qk_prologue_bwd_multi(self._prologue_segments(True), self.eps)
         self._fork()
-        for name in ISSUE_ORDER:
+        for name in order:
             with self._on(name):
                 self._qkv_bwd_phase(name, x, want_dx, saved, grads)
         self._join()
@@ -845,11 +928,9 @@ class SingleBlockLoRA:
         if not self.fused:
             return
         C, r, w = self.C, self.r, self.w
-        self.w_in_ext[:, C:C + r].copy_(w.lora_b["to_in"])
-        self.w_out_ext[C:C + r].copy_(w.lora_a["to_out"])
-        # copied in place: a captured step (GraphedTrainStep) reads these addresses
-        self.a_in_t.copy_(w.lora_a["to_in"].t())
-        self.b_out_t.copy_(w.lora_b["to_out"].t())
+        # copied in place, one launch: a captured step (GraphedTrainStep) reads these addresses
+        copy2d_many([(w.lora_b["to_in"], self.w_in_ext[:, C:C + r]), (w.lora_a["to_out"], self.w_out_ext[C:C + r]),
+                     (w.lora_a["to_in"].t(), self.a_in_t), (w.lora_b["to_out"].t(), self.b_out_t)])
 
     def set_conditioning(self, c: torch.Tensor) -> None:
         """Modulation parts chunk3(silu(c) W_mod^T) (the Mod3 of throughput.rs:284-288)."""

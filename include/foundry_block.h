@@ -152,6 +152,23 @@ fa_status fa_adamw_step(const fa_adamw_args *args, void *stream);
  * throughput.rs:787-803). */
 fa_status fa_adamw_step_many(const fa_adamw_args *args, int32_t count, void *stream);
 
+typedef struct fa_copy2d_args {
+    int32_t dtype;            /* fa_dtype of src and dst                         */
+    int32_t rows, cols;       /* >= 1                                            */
+    const void *src;          /* element (r, c) at src[r * src_rs + c * src_cs]  */
+    int64_t src_rs, src_cs;   /* strides in elements, >= 0                       */
+    void *dst;                /* element (r, c) at dst[r * dst_rs + c * dst_cs]  */
+    int64_t dst_rs, dst_cs;
+} fa_copy2d_args;
+
+/* dst[r, c] = src[r, c] over each of `count` 2D views, in as few launches as
+ * possible (up to 32 views each).  No view's destination may overlap another
+ * view's source or destination.  No counterpart in the reference, which
+ * applies each LoRA factor where it is stored (lib.rs:270-287): the blocks
+ * here keep copies of the factors inside the frozen GEMMs' operands and
+ * transposed, and refresh them after each AdamW step with one such call. */
+fa_status fa_copy2d_many(const fa_copy2d_args *args, int32_t count, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -378,6 +378,27 @@ def test_lora_pieces_validate_before_device_work():
     assert L.fa_lora_grad_many(arr, 3, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
 
 
+def test_copy2d_many_validates_before_device_work():
+    """fa_copy2d_many refuses bad views before touching a device."""
+    L = _abi.lib()
+    good = _abi.Copy2dArgs(dtype=0, rows=16, cols=3072, src=_FAKE, src_rs=3072, src_cs=1, dst=_FAKE + 4096,
+                           dst_rs=1, dst_cs=16)
+    assert L.fa_copy2d_many(None, 1, None) == _abi.FA_ERR_INVALID_ARG
+    arr = (_abi.Copy2dArgs * 2)(good, good)
+    assert L.fa_copy2d_many(arr, 0, None) == _abi.FA_ERR_INVALID_ARG
+    for field, val in (("dtype", 7), ("rows", 0), ("cols", -1), ("src_rs", -1), ("dst_cs", -2), ("src", 0),
+                       ("dst", _FAKE + 1)):
+        bad = _abi.Copy2dArgs.from_buffer_copy(good)
+        setattr(bad, field, val)
+        arr = (_abi.Copy2dArgs * 2)(good, bad)
+        assert L.fa_copy2d_many(arr, 2, None) == _abi.FA_ERR_INVALID_ARG, field
+        assert b"view 1" in L.fa_last_error(), field
+    mixed = _abi.Copy2dArgs.from_buffer_copy(good)
+    mixed.dtype = 1
+    arr = (_abi.Copy2dArgs * 2)(good, mixed)
+    assert L.fa_copy2d_many(arr, 2, None) == _abi.FA_ERR_INVALID_ARG
+
+
 def test_public_headers_are_plain_c():
     """include/*.h compile as C99 on their own (no C++ or HIP types cross the
     boundary), as a Rust bindgen or cgo consumer would read them."""

@@ -418,6 +418,31 @@ def test_klein_single_block_step_properties():
             assert torch.isfinite(a).all() and float(a.abs().max()) > 0 and torch.equal(a, b), t
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_copy2d_many_matches_torch_copies(dtype):
+    """fa_copy2d_many over 40 views (two launches): transposed sources,
+    strided destinations inside wider buffers, column blocks -- every
+    destination equals torch's copy_, and the bytes around it are untouched."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    pairs, want, bufs = [], [], []
+    for i in range(40):
+        r, c = 1 + (7 * i) % 48, 16 + (37 * i) % 300
+        src = torch.randn(c, r, device="cuda", generator=g).to(dtype).t() if i % 3 == 0 else \
+            torch.randn(r, c, device="cuda", generator=g).to(dtype)
+        buf = torch.full((r + 3, c + 9), -7.0, device="cuda", dtype=dtype)
+        dst = buf[1:1 + r, 4:4 + c] if i % 2 else buf[:c, :r].t() if c + 3 <= r else buf[2:2 + r, :c]
+        ref = buf.clone()
+        ref_dst = ref[1:1 + r, 4:4 + c] if i % 2 else ref[:c, :r].t() if c + 3 <= r else ref[2:2 + r, :c]
+        ref_dst.copy_(src)
+        pairs.append((src, dst))
+        want.append(ref)
+        bufs.append(buf)
+    fb.copy2d_many(pairs)
+    torch.cuda.synchronize()
+    for i, (b, w) in enumerate(zip(bufs, want)):
+        assert torch.equal(b, w), i
+
+
 def _flat(y, grads):
     """Copies of a block step's outputs as a name -> tensor dict."""
     out = {}
