@@ -6,7 +6,7 @@ The frozen base linears of the double and single blocks are library GEMMs
 hipBLASLt or rocBLAS solution as measured on the GPU itself.
 ``gemm_tuning_gfx950.csv`` holds that choice for every GEMM shape of the c4
 double block and the klein single block (forward, dX, both streams, with the
-single block's adapter-carrying K / N extensions), measured on an MI355X.
+adapter-carrying K / N extensions of both blocks), measured on an MI355X.
 Its Validator rows name the PyTorch, HIP, hipBLASLt and rocBLAS versions it
 was measured with.
 
@@ -18,7 +18,9 @@ its own way (then it changes nothing):
   libraries, which leaves the default path in place.
 
 Measured on one box: the single block step 3.73 -> 3.41 ms, the double block
-3.92 -> 3.87 ms.  This switches TunableOp on for the whole process (read-only),
+3.92 -> 3.87 ms; after the double block's adapters moved into its GEMMs, the
+rows for those extended shapes took its graph-replayed step from about
+3.35 to 3.2 ms.  This switches TunableOp on for the whole process (read-only),
 which affects only GEMM shapes listed in the file.
 """
 from __future__ import annotations
