@@ -886,7 +886,10 @@ class SingleBlockLoRA:
     def __init__(self, weights: SingleWeights, heads: int, head_dim: int, txt_tokens: int, img_rows: int,
                  img_cols: int, axes: Sequence[int] = (32, 32, 32, 32), theta: float = 2000.0,
                  lora_scale: float = 1.0, eps: float = 1e-6, fuse_adapters: bool = True,
-                 tuned_gemms: bool = True):
+                 tuned_gemms: bool = True, dx_weights_t: bool = True):
+        """dx_weights_t (with fused adapters): keep transposed copies of the two
+        adapter-carrying GEMM operands, so that the backward's dX products read
+        them with the contraction dimension contiguous (as the forward does)."""
         self.w = weights
         self.H, self.D = heads, head_dim
         self.C = heads * head_dim
@@ -919,6 +922,9 @@ class SingleBlockLoRA:
             self.w_out_ext[:C] = weights.w_out
             self.a_in_t = torch.empty((C, self.r), **kw)    # A_in^T: the dx term's "B"
             self.b_out_t = torch.empty((self.r, C), **kw)   # B_out^T: du_out = s dout B_out
+            # [C + P, 3C + 2M] and [C + M, C + P]: the dX products' right operands, transposed
+            self.w_in_ext_t = self.w_in_ext.t().contiguous() if dx_weights_t else None
+            self.w_out_ext_t = self.w_out_ext.t().contiguous() if dx_weights_t else None
             self.refresh_adapters()
 
     def refresh_adapters(self) -> None:
@@ -929,8 +935,12 @@ class SingleBlockLoRA:
             return
         C, r, w = self.C, self.r, self.w
         # copied in place, one launch: a captured step (GraphedTrainStep) reads these addresses
-        copy2d_many([(w.lora_b["to_in"], self.w_in_ext[:, C:C + r]), (w.lora_a["to_out"], self.w_out_ext[C:C + r]),
-                     (w.lora_a["to_in"].t(), self.a_in_t), (w.lora_b["to_out"].t(), self.b_out_t)])
+        pairs = [(w.lora_b["to_in"], self.w_in_ext[:, C:C + r]), (w.lora_a["to_out"], self.w_out_ext[C:C + r]),
+                 (w.lora_a["to_in"].t(), self.a_in_t), (w.lora_b["to_out"].t(), self.b_out_t)]
+        if self.w_in_ext_t is not None:
+            pairs += [(w.lora_b["to_in"].t(), self.w_in_ext_t[C:C + r]),
+                      (w.lora_a["to_out"].t(), self.w_out_ext_t[:, C:C + r])]
+        copy2d_many(pairs)
 
     def set_conditioning(self, c: torch.Tensor) -> None:
         """Modulation parts chunk3(silu(c) W_mod^T) (the Mod3 of throughput.rs:284-288)."""
@@ -1024,7 +1034,7 @@ class SingleBlockLoRA:
             dout_ext = B["dout_ext"]
             dout = gated_residual(None, g, dy, out=dout_ext[:, :C])
             du_out = lora_down(dout, self.b_out_t, s, out=dout_ext[:, C:C + r])
-            torch.mm(dout_ext, self.w_out_ext, out=djoined)
+            torch.mm(dout_ext, self.w_out_ext if self.w_out_ext_t is None else self.w_out_ext_t.t(), out=djoined)
             grads = {"to_out": tuple(lora_grad_many([(du_out, joined, 1.0, False), (u_out, dout, s, True)]))}
         else:
             dout = gated_residual(None, g, dy, out=B["dout"])
@@ -1042,7 +1052,7 @@ class SingleBlockLoRA:
             if want_dx:
                 # dfused [W_in | B_in | 0] = [dfused W_in | dfused B_in | 0]
                 dnh_ext = B["dnh_ext"]
-                torch.mm(dfused, self.w_in_ext, out=dnh_ext)
+                torch.mm(dfused, self.w_in_ext if self.w_in_ext_t is None else self.w_in_ext_t.t(), out=dnh_ext)
                 dnh, t_in = dnh_ext[:, :C], dnh_ext[:, C:C + r]
                 lora_up(t_in, self.a_in_t, dnh, s)  # + s (dfused B_in) A_in
             else:
