@@ -207,6 +207,17 @@ def adamw_step_many(items, step: int, lr: float = 1e-3, betas=(0.9, 0.999), eps:
     check(lib().fa_adamw_step_many(arr, len(items), _stream(items[0][0])))
 
 
+def _set_mod(old, parts):
+    """New modulation parts, written into the old tensors when their shapes
+    match (a captured GraphedTrainStep reads those addresses)."""
+    parts = [t.contiguous() for t in parts]
+    if len(old) == len(parts) and all(o.shape == p.shape and o.dtype == p.dtype for o, p in zip(old, parts)):
+        for o, p in zip(old, parts):
+            o.copy_(p)
+        return old
+    return tuple(parts)
+
+
 def copy2d_many(pairs):
     """dst.copy_(src) for several (src, dst) pairs of 2-D views of one dtype
     (any strides, no overlaps) in one launch per 32 views (fa_copy2d_many)."""
@@ -308,7 +319,7 @@ class DoubleBlockLoRA:
                  lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
                  tuned_gemms: bool = True, batch_qkv_adapters: bool = True, mlp: str = "gelu",
                  positions: Optional[np.ndarray] = None, dx_weights_t: bool = True,
-                 fold_qkv_adapters: bool = True):
+                 fold_qkv_adapters: bool = True, fold_mlp_gate: bool = True):
         """positions: [S, n_axes] RoPE position ids of the joint sequence (txt
         rows first); None gives txt (l, 0, 0), img (0, r, c).
 
@@ -331,7 +342,13 @@ class DoubleBlockLoRA:
         With out adapters on both streams the out projection folds the same
         way: a [W_out; A_out; 0]^T = [out | u | 0] (then out += s u B_out^T),
         and [dout | s dout B_out | 0] [W_out; A_out; 0] = dout W_out + du A_out
-        gives dO."""
+        gives dO.
+
+        fold_mlp_gate (no MLP output bias): the MLP's gate g2 (a per-channel
+        modulation, fixed by set_conditioning) scales the rows of W2 once,
+        W2g = diag(g2) W2.  Then y = x1 + act W2g^T is one GEMM with x1 as its
+        accumulator input, and the backward's dact = (g2 * dy) W2 = dy W2g
+        needs no separate g2 * dy pass."""
         if mlp not in ("gelu", "swiglu"):
             raise ValueError(f"mlp must be 'gelu' or 'swiglu', not {mlp!r}")
         self.w = weights
@@ -368,6 +385,8 @@ class DoubleBlockLoRA:
         self._buf = None
         self._side = torch.cuda.Stream(device=self.device) if overlap_streams else None
         self._wt = {name: {} for name in STREAMS} if dx_weights_t else None
+        self._fold_g2 = fold_mlp_gate and all(weights[name].b2 is None for name in STREAMS)
+        self._w2g, self._w2g_t = {}, {}
         if tuned_gemms and self.dtype == torch.bfloat16:
             gemm_tuning.enable()
         ranks = {int(a.shape[0]) for w in weights.values() for a in w.lora_a.values()}
@@ -442,7 +461,9 @@ class DoubleBlockLoRA:
                     self._b_out_ext[name][:C].copy_(w.b_out)
         if self._wt is None:
             return
-        folded = (("w_qkv",) if self._fold else ()) + (("w_out",) if self._fold_out else ())
+        self._refresh_w2g()
+        folded = (("w_qkv",) if self._fold else ()) + (("w_out",) if self._fold_out else ()) + \
+            (("w2",) if self._fold_g2 else ())
         for name in STREAMS:
             w = self.w[name]
             for key in (k for k in ("w_qkv", "w_out", "w1", "w2") if k not in folded):
@@ -452,6 +473,26 @@ class DoubleBlockLoRA:
                     self._wt[name][key] = src.t().contiguous()
                 else:
                     dst.copy_(src.t())
+
+    def _refresh_w2g(self) -> None:
+        """W2g = diag(g2) W2 per stream (and its transpose with dx_weights_t),
+        once the modulation is known; rounded once from the f32 product."""
+        if not self._fold_g2:
+            return
+        for name in STREAMS:
+            w = self.w[name]
+            if len(w.mod) < 6:
+                continue
+            w2g = (w.w2.float() * w.mod[5].float()[:, None]).to(self.dtype)
+            if name in self._w2g and self._w2g[name].shape == w2g.shape:
+                self._w2g[name].copy_(w2g)  # in place: a captured step reads this address
+            else:
+                self._w2g[name] = w2g
+            if self._wt is not None:
+                if name in self._w2g_t and self._w2g_t[name].shape == (w2g.shape[1], w2g.shape[0]):
+                    self._w2g_t[name].copy_(w2g.t())
+                else:
+                    self._w2g_t[name] = w2g.t().contiguous()
 
     def _dx_weight(self, name: str, key: str) -> torch.Tensor:
         """W of stream `name` as the right operand of dX = dY W."""
@@ -505,7 +546,8 @@ class DoubleBlockLoRA:
             w = self.w[name]
             m = torch.empty((1, w.w_mod.shape[0]), dtype=self.dtype, device=self.device)
             _linear(sc, w.w_mod, w.b_mod, m)
-            w.mod = tuple(t.contiguous() for t in m.reshape(-1).split(self.C))
+            w.mod = _set_mod(w.mod, m.reshape(-1).split(self.C))
+        self._refresh_w2g()
 
     def _buffers(self):
         if self._buf is None:
@@ -654,16 +696,23 @@ class DoubleBlockLoRA:
             act = swiglu(pre[:, :M], pre[:, M:], out=B[f"act.{name}"])
         else:
             act = gelu(pre, out=B[f"act.{name}"])
-        mlp = _linear(act, w.w2, w.b2, B[f"mlp.{name}"])
-        y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
+        if self._fold_g2:
+            y[name] = torch.addmm(x1, act, self._w2g[name].t(), out=B[f"y.{name}"])  # x1 + act W2g^T
+        else:
+            mlp = _linear(act, w.w2, w.b2, B[f"mlp.{name}"])
+            y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
         if self.capture is not None:
             self.capture[f"{name}_post_attn"] = x1.clone()
             self.capture[f"{name}_out"] = y[name].clone()
         if dy is None:
             return
         # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
-        dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
-        dact = torch.mm(dmlp, self._dx_weight(name, "w2"), out=B[f"dact.{name}"])
+        if self._fold_g2:  # (g2 * dy) W2 = dy W2g
+            w2g = self._w2g[name] if self._wt is None else self._w2g_t[name].t()
+            dact = torch.mm(dy[name], w2g, out=B[f"dact.{name}"])
+        else:
+            dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
+            dact = torch.mm(dmlp, self._dx_weight(name, "w2"), out=B[f"dact.{name}"])
         if self.mlp == "swiglu":
             dpre = B[f"dpre.{name}"]
             swiglu_bwd(dact, pre[:, :M], pre[:, M:], dgate=dpre[:, :M], dup=dpre[:, M:])
@@ -945,7 +994,7 @@ class SingleBlockLoRA:
     def set_conditioning(self, c: torch.Tensor) -> None:
         """Modulation parts chunk3(silu(c) W_mod^T) (the Mod3 of throughput.rs:284-288)."""
         m = torch.mm(silu(c.reshape(1, -1)), self.w.w_mod.t()).reshape(-1)
-        self.w.mod = tuple(t.contiguous() for t in m.split(self.C))
+        self.w.mod = _set_mod(self.w.mod, m.split(self.C))
 
     def _buffers(self):
         if self._buf is None:
@@ -1121,7 +1170,8 @@ class GraphedTrainStep:
       overwritten by the next call.
     - AdamW and the adapter refresh run eagerly after each replay: their bias
       corrections change with the step count.  They update the LoRA factors
-      in place, at the addresses the graph reads.
+      in place, at the addresses the graph reads; so do set_conditioning,
+      refresh_adapters and refresh_frozen.
     - The captured ops record no memset: the step's kernels and hipBLASLt
       GEMMs write every element they later read.
     """

@@ -456,12 +456,12 @@ def _flat(y, grads):
 
 @pytest.mark.parametrize("kind", ["double", "single"])
 def test_graphed_train_step_replays_match_eager(kind):
-    """GraphedTrainStep (forward + backward captured in one HIP graph): three
+    """GraphedTrainStep (forward + backward captured in one HIP graph): four
     replays with an AdamW step between them (the LoRA factors and the
-    adapter operands the graph reads change every step) each give the bits
-    of an eager forward_backward on the same factors, run right after the
-    replay with a synchronisation between; calling the step replays and
-    applies AdamW."""
+    adapter operands the graph reads change every step; before the last, the
+    conditioning changes too) each give the bits of an eager forward_backward
+    on the same state, run right after the replay with a synchronisation
+    between; calling the step replays and applies AdamW."""
     bf = torch.bfloat16
     if kind == "double":
         case = oracle_mods(make_case(C=256, H=2, T=16, rows=4, cols=8, r=4, bf16=True, seed=5))
@@ -472,8 +472,11 @@ def test_graphed_train_step_replays_match_eager(kind):
         sc = single_oracle_mods(make_single_case(C=256, H=2, T=40, rows=8, cols=12, r=4, bf16=True, seed=9))
         blk = device_single_block(sc, bf)
         x, dy = dev(sc["x"], bf), dev(sc["dy"], bf)
+    c = case["c"] if kind == "double" else sc["c"]
     gs = fb.GraphedTrainStep(blk, x, dy, want_dx=True)
-    for i in range(3):
+    for i in range(4):
+        if i == 3:  # new conditioning: the modulation (and diag(g2) W2) change in place
+            blk.set_conditioning(dev(0.5 * c, bf))
         gs.graph.replay()
         torch.cuda.synchronize()
         got = _flat(gs.y, gs.grads)
