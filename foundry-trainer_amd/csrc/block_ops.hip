@@ -45,10 +45,21 @@ __device__ __forceinline__ void store8(float *p, const float v[8]) {
     *reinterpret_cast<f32x4 *>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
 }
 
+// Sum over the wave, the same value in every lane: within each 16-lane row by
+// DPP (partners lane^1, lane^2, then the mirrors within 8 and within 16 lanes;
+// each step adds a disjoint group's partial, so every lane of a row ends with
+// the same sum), then rows by lane^16 and lane^32 exchanges.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float s) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    return s;
+    s += dpp_f32<0xB1>(s);   // quad_perm [1,0,3,2]
+    s += dpp_f32<0x4E>(s);   // quad_perm [2,3,0,1]
+    s += dpp_f32<0x141>(s);  // row_half_mirror
+    s += dpp_f32<0x140>(s);  // row_mirror
+    s += __shfl_xor(s, 16, 64);
+    return sum_xor32(s);
 }
 
 // One wave per row; lane l holds elements k*512 + 8*l .. +8 for k < MAXCH.
@@ -85,6 +96,7 @@ __global__ __launch_bounds__(256) void ln_mod_fwd_kernel(LnModParams p) {
     }
     const float var = wave_sum(q) / (float)C;
     const float den = sqrtf(var + p.eps);
+    const float inv = 1.f / den;
     const T *shift = static_cast<const T *>(p.shift), *scale = static_cast<const T *>(p.scale);
     T *y = static_cast<T *>(p.y) + row * p.ldy;
 #pragma unroll
@@ -95,7 +107,7 @@ __global__ __launch_bounds__(256) void ln_mod_fwd_kernel(LnModParams p) {
             load8(shift + e, sh);
             load8(scale + e, sc);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = (v[k][j] - mean) / den * (sc[j] + 1.f) + sh[j];
+            for (int j = 0; j < 8; ++j) o[j] = (v[k][j] - mean) * inv * (sc[j] + 1.f) + sh[j];
             store8(y + e, o);
         }
     }
@@ -317,11 +329,16 @@ inline int elt_grid(int64_t n8) {
 
 }  // namespace
 
+// MAXCH (512-element chunks per row): 2 up to C = 1024, 6 up to 3072 (the
+// blocks' width: fewer registers, so a whole 4608-row grid is resident in one
+// round), 8 up to 4096.
 template <typename T>
 static hipError_t ln_fwd_t(const LnModParams &p, hipStream_t s) {
     const dim3 grid((unsigned)((p.N + 3) / 4)), block(256);
     if (p.C <= 1024)
         hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 2>), grid, block, 0, s, p);
+    else if (p.C <= 3072)
+        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 6>), grid, block, 0, s, p);
     else
         hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 8>), grid, block, 0, s, p);
     return hipGetLastError();
@@ -331,6 +348,8 @@ static hipError_t ln_bwd_t(const LnModParams &p, hipStream_t s) {
     const dim3 grid((unsigned)((p.N + 3) / 4)), block(256);
     if (p.C <= 1024)
         hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 2>), grid, block, 0, s, p);
+    else if (p.C <= 3072)
+        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 6>), grid, block, 0, s, p);
     else
         hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 8>), grid, block, 0, s, p);
     return hipGetLastError();

@@ -27,7 +27,7 @@ def host(t):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("C", [256, 3072])
+@pytest.mark.parametrize("C", [256, 3072, 4096])
 def test_block_ops_match_oracle(dtype, C):
     bf = dtype == torch.bfloat16
     rng = np.random.default_rng(C)
