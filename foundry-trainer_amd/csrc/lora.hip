@@ -482,28 +482,38 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
         acc[r] = 0.f;
         acc2[r] = 0.f;
     }
-    auto stage = [&](const char *tile, int t0) {
+    // A stage's U^T fragments are loaded before the next stage's DMA is
+    // issued: memory operations complete in issue order, so waiting for them
+    // then leaves that DMA in flight during this stage's MFMAs.
+    constexpr int KS = kCsRows / 16;
+    auto loadu = [&](int t0, bf16x8 (&b)[2 * KS]) {
 #pragma unroll
-        for (int ks = 0; ks < kCsRows / 16; ++ks) {
-            const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
-                                               col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
-            const bf16x8 b = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
-            acc = mfma_32x32x16(a, b, acc);
-            if (two) {
-                const bf16x8 b2 = as_bf16x8(ld_global_16(ub2 + t0 + ks * 16));
-                acc2 = mfma_32x32x16(a, b2, acc2);
-            }
+        for (int ks = 0; ks < KS; ++ks) {
+            b[ks] = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
+            if (two) b[KS + ks] = as_bf16x8(ld_global_16(ub2 + t0 + ks * 16));
         }
     };
+    auto stage = [&](const char *tile, const bf16x8 (&b)[2 * KS]) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
+                                               col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
+            acc = mfma_32x32x16(a, b[ks], acc);
+            if (two) acc2 = mfma_32x32x16(a, b[KS + ks], acc2);
+        }
+    };
+    bf16x8 bu[2 * KS];
     issue(t_begin, st0);
     for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
         barrier_keep_dma<0>();
+        loadu(t0, bu);
         if (t0 + kCsRows < t_end) issue(t0 + kCsRows, st1);
-        stage(st0, t0);
+        stage(st0, bu);
         if (t0 + kCsRows < t_end) {
             barrier_keep_dma<0>();
+            loadu(t0 + kCsRows, bu);
             if (t0 + 2 * kCsRows < t_end) issue(t0 + 2 * kCsRows, st0);
-            stage(st1, t0 + kCsRows);
+            stage(st1, bu);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
