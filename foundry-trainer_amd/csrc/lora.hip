@@ -368,24 +368,33 @@ __global__ __launch_bounds__(256) void lora_colsum_mfma_kernel(const bf16 *__res
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    auto stage = [&](const char *tile, int t0) {
+    // a stage's U^T fragments are loaded before the next stage's DMA, so that
+    // waiting for them leaves that DMA in flight (in-order completion)
+    constexpr int KS = kCsRows / 16;
+    auto loadu = [&](int t0, bf16x8 (&b)[KS]) {
 #pragma unroll
-        for (int ks = 0; ks < kCsRows / 16; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) b[ks] = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
+    };
+    auto stage = [&](const char *tile, const bf16x8 (&b)[KS]) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
             const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
                                                col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
-            const bf16x8 b = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
-            acc = mfma_32x32x16(a, b, acc);
+            acc = mfma_32x32x16(a, b[ks], acc);
         }
     };
+    bf16x8 bu[KS];
     issue(t_begin, st0);
     for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
         barrier_keep_dma<0>();
+        loadu(t0, bu);
         if (t0 + kCsRows < t_end) issue(t0 + kCsRows, st1);
-        stage(st0, t0);
+        stage(st0, bu);
         if (t0 + kCsRows < t_end) {
             barrier_keep_dma<0>();
+            loadu(t0 + kCsRows, bu);
             if (t0 + 2 * kCsRows < t_end) issue(t0 + 2 * kCsRows, st0);
-            stage(st1, t0 + kCsRows);
+            stage(st1, bu);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
