@@ -21,12 +21,16 @@ Compute path: the memory-bound ops (layer_norm_mod and its backward, gated
 residuals, GELU, the fused QK-RMSNorm + RoPE prologue, the LoRA adapters,
 AdamW) and the joint attention run as libfoundry_attn.so kernels; the frozen
 base linears are plain library GEMMs (torch.mm -> hipBLASLt), bf16 in, f32
-accumulation, bf16 out.
+accumulation, bf16 out.  In bf16 the adapters ride in those GEMMs as extra
+K or N columns (DoubleBlockLoRA's fold options, SingleBlockLoRA's fused
+adapters), and GraphedTrainStep captures either block's forward and
+backward in one HIP graph.
 
-The backward forms exactly the gradients Candle's autograd needs for the
-LoRA factors: nothing flows into the first layer_norm_mod (its output feeds
-only frozen weights and the adapters), so no dX is formed for the frozen qkv
-projection.
+With want_dx=False the backward forms exactly the gradients Candle's
+autograd needs for the LoRA factors: nothing flows into the first
+layer_norm_mod (its output feeds only frozen weights and the adapters), so no
+dX is formed for the frozen qkv projection.  want_dx=True also forms the
+block-input gradient, as a block inside a stack needs.
 """
 from __future__ import annotations
 
@@ -307,11 +311,11 @@ class DoubleBlockLoRA:
     read the same h, so their A factors are stacked into one [3r, C] tensor
     (lora_a[t] become row views of it) and every product that contracts or
     expands over h runs once at rank 3r -- s u = s h A^T, dh += s t A_qkv
-    and dA = s t^T h -- while the block-diagonal ones (the three up
-    projections, t_j = dy_j B_j and dB_j) stay per adapter.  Same arithmetic
-    as the adapter pieces of the single block (u and t rounded to bf16 as the
-    reference's bf16 matmuls round them); a third of the launches and one
-    pass over h and dh instead of three.
+    and dA = s t^T h.  The block-diagonal ones (the three up projections and
+    t_j = dy_j B_j) ride in the qkv GEMMs with fold_qkv_adapters (see
+    __init__), or stay per adapter without; the dB_j are formed with dA in
+    one grouped launch set.  u and t are rounded to bf16 as the reference's
+    bf16 matmuls round them.
     """
 
     def __init__(self, weights: Dict[str, StreamWeights], heads: int, head_dim: int, txt_tokens: int,
