@@ -407,6 +407,23 @@ __global__ __launch_bounds__(256) void lora_colsum_mfma_kernel(const bf16 *__res
     }
 }
 
+// sum_sp p[sp * stride] for sp = 0, 1, ..., n - 1, added in that order; the
+// loads go out eight at a time, so a thread waits for memory once per eight
+// splits rather than once per split.
+__device__ __forceinline__ float sum_splits(const float *p, int64_t stride, int n) {
+    float acc = 0.f;
+    int sp = 0;
+    for (; sp + 8 <= n; sp += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = p[(int64_t)(sp + i) * stride];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += v[i];
+    }
+    for (; sp < n; ++sp) acc += p[(int64_t)sp * stride];
+    return acc;
+}
+
 // out[j * os_j + c * os_c] = s * sum_sp part[sp][c][j] (fixed order), j < R.
 __global__ void lora_colsum_reduce_kernel(const float *__restrict__ part, float *out, int64_t os_j,
                                           int64_t os_c, int C, int R, int splits, float s) {
@@ -414,9 +431,7 @@ __global__ void lora_colsum_reduce_kernel(const float *__restrict__ part, float 
     if (e >= (int64_t)C * 32) return;
     const int c = (int)(e >> 5), j = (int)(e & 31);
     if (j >= R) return;
-    float acc = 0.f;
-    for (int sp = 0; sp < splits; ++sp) acc += part[(int64_t)sp * C * 32 + e];
-    out[j * os_j + (int64_t)c * os_c] = s * acc;
+    out[j * os_j + (int64_t)c * os_c] = s * sum_splits(part + e, (int64_t)C * 32, splits);
 }
 
 // ---- colsum over several products in one set of launches -----------------
@@ -546,9 +561,7 @@ __global__ void lora_colsum_reduce_many_kernel(GradMany g) {
     if (e >= (int64_t)q.C * q.rw) return;
     const int c = (int)(e / q.rw), j = (int)(e - (int64_t)c * q.rw);
     if (j >= q.R) return;
-    float acc = 0.f;
-    for (int sp = 0; sp < q.splits; ++sp) acc += q.part[(int64_t)sp * q.C * q.rw + e];
-    q.out[j * q.os_j + (int64_t)c * q.os_c] = q.s * acc;
+    q.out[j * q.os_j + (int64_t)c * q.os_c] = q.s * sum_splits(q.part + e, (int64_t)q.C * q.rw, q.splits);
 }
 
 // Small transpose [R][C] -> [C][R] (dtype).
