@@ -45,6 +45,12 @@ __device__ __forceinline__ void store8(float *p, const float v[8]) {
     *reinterpret_cast<f32x4 *>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
 }
 
+// x rounded to the storage type T, back in f32
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+    return (float)(T)x;
+}
+
 // Sum over the wave, the same value in every lane: within each 16-lane row by
 // DPP (partners lane^1, lane^2, then the mirrors within 8 and within 16 lanes;
 // each step adds a disjoint group's partial, so every lane of a row ends with
@@ -63,7 +69,11 @@ __device__ __forceinline__ float wave_sum(float s) {
 }
 
 // One wave per row; lane l holds elements k*512 + 8*l .. +8 for k < MAXCH.
-template <typename T, int MAXCH>
+// GATED: the row is first the gated residual x + g * b, rounded to T as the
+// gated-residual op rounds it (the same fma), stored to sum (and sum2), and
+// the statistics are those of the rounded sum: the bits of the gated
+// residual followed by this kernel on its output.
+template <typename T, int MAXCH, bool GATED>
 __global__ __launch_bounds__(256) void ln_mod_fwd_kernel(LnModParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -77,6 +87,15 @@ __global__ __launch_bounds__(256) void ln_mod_fwd_kernel(LnModParams p) {
         const int e = k * 512 + lane * 8;
         if (e < C) {
             load8(x + e, v[k]);
+            if constexpr (GATED) {
+                float gv[8], bv[8];
+                load8(static_cast<const T *>(p.g) + e, gv);
+                load8(static_cast<const T *>(p.b) + row * p.ldb + e, bv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[k][j] = round_to<T>(__builtin_fmaf(gv[j], bv[j], v[k][j]));
+                store8(static_cast<T *>(p.sum) + row * p.ldsum + e, v[k]);
+                if (p.sum2) store8(static_cast<T *>(p.sum2) + row * p.ldsum2 + e, v[k]);
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) s += v[k][j];
         }
@@ -117,7 +136,10 @@ __global__ __launch_bounds__(256) void ln_mod_fwd_kernel(LnModParams p) {
     }
 }
 
-template <typename T, int MAXCH>
+// GATE_OUT: also gdx = g * dx, from dx as rounded to T (the same fma as the
+// gated-residual op with no x), the gradient through a gated branch whose
+// output fed this layer norm's input.
+template <typename T, int MAXCH, bool GATE_OUT>
 __global__ __launch_bounds__(256) void ln_mod_bwd_kernel(LnModParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -163,6 +185,13 @@ __global__ __launch_bounds__(256) void ln_mod_bwd_kernel(LnModParams p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = r[j] + rstd * (dn[k][j] - ma - n[k][j] * mb);
             store8(dx + e, o);
+            if constexpr (GATE_OUT) {
+                float gv[8], go[8];
+                load8(static_cast<const T *>(p.g) + e, gv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) go[j] = __builtin_fmaf(gv[j], round_to<T>(o[j]), 0.f);
+                store8(static_cast<T *>(p.gdx) + row * p.ldgdx + e, go);
+            }
         }
     }
 }
@@ -204,7 +233,7 @@ __global__ __launch_bounds__(kEltLanes) void elementwise_kernel(EltParams p) {
                 for (int j = 0; j < 8; ++j) xv[j] = 0.f;
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = xv[j] + gv[j] * bv[j];
+            for (int j = 0; j < 8; ++j) o[j] = __builtin_fmaf(gv[j], bv[j], xv[j]);
         } else if constexpr (OP == 1) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = bv[j] * gelu_sigmoid(bv[j]);
@@ -229,11 +258,6 @@ __global__ __launch_bounds__(kEltLanes) void elementwise_kernel(EltParams p) {
 // SwiGLU over [N, C] views, 8 elements per thread.  Forward: y = T(T(silu(g))
 // * u).  Backward: du = T(dy * T(silu(g))), dg = T(T(dy * u) * silu'(g)) with
 // silu'(g) = s (1 + g (1 - s)), s = 1 / (1 + e^-g); T() = round to storage.
-template <typename T>
-__device__ __forceinline__ float round_to(float x) {
-    return (float)(T)x;
-}
-
 template <typename T, bool BWD>
 __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams p) {
     const int64_t per_row = p.C / 8;
@@ -332,27 +356,35 @@ inline int elt_grid(int64_t n8) {
 // MAXCH (512-element chunks per row): 2 up to C = 1024, 6 up to 3072 (the
 // blocks' width: fewer registers, so a whole 4608-row grid is resident in one
 // round), 8 up to 4096.
-template <typename T>
+template <typename T, bool F>
 static hipError_t ln_fwd_t(const LnModParams &p, hipStream_t s) {
     const dim3 grid((unsigned)((p.N + 3) / 4)), block(256);
     if (p.C <= 1024)
-        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 2>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 2, F>), grid, block, 0, s, p);
     else if (p.C <= 3072)
-        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 6>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 6, F>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 8>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((ln_mod_fwd_kernel<T, 8, F>), grid, block, 0, s, p);
     return hipGetLastError();
 }
-template <typename T>
+template <typename T, bool F>
 static hipError_t ln_bwd_t(const LnModParams &p, hipStream_t s) {
     const dim3 grid((unsigned)((p.N + 3) / 4)), block(256);
     if (p.C <= 1024)
-        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 2>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 2, F>), grid, block, 0, s, p);
     else if (p.C <= 3072)
-        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 6>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 6, F>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 8>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((ln_mod_bwd_kernel<T, 8, F>), grid, block, 0, s, p);
     return hipGetLastError();
+}
+template <typename T>
+static hipError_t ln_fwd_t(const LnModParams &p, hipStream_t s) {
+    return p.b ? ln_fwd_t<T, true>(p, s) : ln_fwd_t<T, false>(p, s);
+}
+template <typename T>
+static hipError_t ln_bwd_t(const LnModParams &p, hipStream_t s) {
+    return p.gdx ? ln_bwd_t<T, true>(p, s) : ln_bwd_t<T, false>(p, s);
 }
 
 hipError_t launch_ln_mod_fwd(const LnModParams &p, int dtype, hipStream_t s) {

@@ -947,6 +947,60 @@ fa_status fa_ln_mod_bwd(const fa_ln_mod_bwd_args *a, void *stream) {
     return ok();
 }
 
+fa_status fa_gated_ln_mod_fwd(const fa_gated_ln_mod_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    const fa_ln_mod_args *l = &a->ln;
+    FA_TRY(check_ln(l));
+    FA_TRY(check_row_view("y", l->y, l->ldy, l->cols, l->dtype));
+    if ((l->mean == nullptr) != (l->rstd == nullptr))
+        return fail(FA_ERR_INVALID_ARG, "mean and rstd must both be given or both NULL");
+    if (l->mean && (!aligned(l->mean, 4) || !aligned(l->rstd, 4)))
+        return fail(FA_ERR_INVALID_ARG, "mean/rstd misaligned");
+    FA_TRY(check_vec("g", a->g));
+    FA_TRY(check_row_view("b", a->b, a->ldb, l->cols, l->dtype));
+    FA_TRY(check_row_view("sum", a->sum, a->ldsum, l->cols, l->dtype));
+    if (a->sum2) FA_TRY(check_row_view("sum2", a->sum2, a->ldsum2, l->cols, l->dtype));
+    FA_TRY(init_current());
+    fa::LnModParams p = ln_params(l);
+    p.g = a->g;
+    p.b = a->b;
+    p.ldb = a->ldb;
+    p.sum = a->sum;
+    p.ldsum = a->ldsum;
+    p.sum2 = a->sum2;
+    p.ldsum2 = a->ldsum2;
+    const hipError_t e = fa::launch_ln_mod_fwd(p, l->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "gated layer-norm-mod launch");
+    return ok();
+}
+
+fa_status fa_ln_mod_bwd_gate(const fa_ln_mod_bwd_gate_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    const fa_ln_mod_bwd_args *w = &a->bwd;
+    FA_TRY(check_ln(&w->fwd));
+    if (!w->fwd.mean || !w->fwd.rstd || !aligned(w->fwd.mean, 4) || !aligned(w->fwd.rstd, 4))
+        return fail(FA_ERR_INVALID_ARG, "mean and rstd (from the forward) are required");
+    FA_TRY(check_row_view("dy", w->dy, w->lddy, w->fwd.cols, w->fwd.dtype));
+    FA_TRY(check_row_view("dx", w->dx, w->lddx, w->fwd.cols, w->fwd.dtype));
+    if (w->dres) FA_TRY(check_row_view("dres", w->dres, w->ldres, w->fwd.cols, w->fwd.dtype));
+    FA_TRY(check_vec("g", a->g));
+    FA_TRY(check_row_view("gdx", a->gdx, a->ldgdx, w->fwd.cols, w->fwd.dtype));
+    FA_TRY(init_current());
+    fa::LnModParams p = ln_params(&w->fwd);
+    p.dy = w->dy;
+    p.lddy = w->lddy;
+    p.dres = w->dres;
+    p.ldres = w->ldres;
+    p.dx = w->dx;
+    p.lddx = w->lddx;
+    p.g = a->g;
+    p.gdx = a->gdx;
+    p.ldgdx = a->ldgdx;
+    const hipError_t e = fa::launch_ln_mod_bwd(p, w->fwd.dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "layer-norm-mod backward launch");
+    return ok();
+}
+
 fa_status fa_gated_residual(const fa_rows_args *a, void *stream) { return rows_op(a, 0, stream); }
 fa_status fa_gelu_fwd(const fa_rows_args *a, void *stream) { return rows_op(a, 1, stream); }
 fa_status fa_gelu_bwd(const fa_rows_args *a, void *stream) { return rows_op(a, 2, stream); }

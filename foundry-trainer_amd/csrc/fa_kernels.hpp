@@ -148,6 +148,16 @@ struct LnModParams {
     int64_t lddx;
     int N, C;
     float eps;
+    const void *g;  // [C] gate: fwd with b, the gated residual x + g * b in
+                    // front of the norm; bwd with gdx, g * dx after it
+    const void *b;  // fwd: [N, C] gated branch, or null (plain layer norm)
+    int64_t ldb;
+    void *sum;      // fwd with b: [N, C] output x + g * b (the norm's input)
+    int64_t ldsum;
+    void *sum2;     // fwd with b: optional second copy of the sum
+    int64_t ldsum2;
+    void *gdx;      // bwd: [N, C] output g * dx, or null
+    int64_t ldgdx;
 };
 hipError_t launch_ln_mod_fwd(const LnModParams &p, int dtype, hipStream_t s);
 hipError_t launch_ln_mod_bwd(const LnModParams &p, int dtype, hipStream_t s);

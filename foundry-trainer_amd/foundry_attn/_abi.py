@@ -31,6 +31,7 @@ EXPORTED = [
     "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step", "fa_adamw_step_many", "fa_copy2d_many",
     "fa_lora_down", "fa_lora_up", "fa_lora_grad", "fa_lora_grad_workspace_size",
     "fa_lora_grad_many", "fa_lora_grad_many_workspace_size",
+    "fa_gated_ln_mod_fwd", "fa_ln_mod_bwd_gate",
 ]
 
 
@@ -120,6 +121,16 @@ class LnModBwdArgs(ctypes.Structure):
     _fields_ = [("fwd", LnModArgs), ("dy", ctypes.c_void_p), ("lddy", ctypes.c_int64),
                 ("dres", ctypes.c_void_p), ("ldres", ctypes.c_int64), ("dx", ctypes.c_void_p),
                 ("lddx", ctypes.c_int64)]
+
+
+class GatedLnModArgs(ctypes.Structure):
+    _fields_ = [("ln", LnModArgs), ("g", ctypes.c_void_p), ("b", ctypes.c_void_p), ("ldb", ctypes.c_int64),
+                ("sum", ctypes.c_void_p), ("ldsum", ctypes.c_int64), ("sum2", ctypes.c_void_p),
+                ("ldsum2", ctypes.c_int64)]
+
+
+class LnModBwdGateArgs(ctypes.Structure):
+    _fields_ = [("bwd", LnModBwdArgs), ("g", ctypes.c_void_p), ("gdx", ctypes.c_void_p), ("ldgdx", ctypes.c_int64)]
 
 
 class RowsArgs(ctypes.Structure):
@@ -229,6 +240,7 @@ def lib() -> ctypes.CDLL:
     L.fa_lora_bwd_workspace_size.restype = ctypes.c_size_t
     L.fa_lora_bwd_workspace_size.argtypes = [ctypes.POINTER(LoraBwdArgs)]
     for name, st in (("fa_ln_mod_fwd", LnModArgs), ("fa_ln_mod_bwd", LnModBwdArgs),
+                     ("fa_gated_ln_mod_fwd", GatedLnModArgs), ("fa_ln_mod_bwd_gate", LnModBwdGateArgs),
                      ("fa_gated_residual", RowsArgs), ("fa_gelu_fwd", RowsArgs),
                      ("fa_gelu_bwd", RowsArgs), ("fa_silu", RowsArgs), ("fa_adamw_step", AdamwArgs),
                      ("fa_swiglu_fwd", SwigluArgs), ("fa_swiglu_bwd", SwigluBwdArgs),

@@ -108,6 +108,49 @@ def ln_mod_bwd(x, dy, scale, mean, rstd, eps: float = 1e-6, dres=None, out=None)
     return dx
 
 
+def gated_ln_mod_fwd(x, g, b, shift, scale, eps: float = 1e-6, out=None, sum_out=None, sum_copy=None):
+    """The gated residual s = x + g * b and layer_norm_mod(s) in one pass
+    (throughput.rs:552-566): returns (s, y, mean, rstd), the bits of
+    gated_residual followed by ln_mod_fwd(stats=True) on its output.
+    sum_copy, when given, receives a second copy of s."""
+    x = _rows(x, "x")
+    N, C = x.shape
+    b = _like(b, x, "b")
+    s = _like(sum_out, x, "sum_out")
+    y = _like(out, x)
+    if sum_copy is not None:
+        _like(sum_copy, x, "sum_copy")
+    mean = torch.empty(N, dtype=torch.float32, device=x.device)
+    rstd = torch.empty(N, dtype=torch.float32, device=x.device)
+    ln = _abi.LnModArgs(dtype=_dtype_code(x), rows=N, cols=C, eps=float(eps), x=_ptr(x), ldx=x.stride(0),
+                        shift=_ptr(_vec(shift, C, x, "shift")), scale=_ptr(_vec(scale, C, x, "scale")),
+                        y=_ptr(y), ldy=y.stride(0), mean=_ptr(mean), rstd=_ptr(rstd))
+    a = _abi.GatedLnModArgs(ln=ln, g=_ptr(_vec(g, C, x, "g")), b=_ptr(b), ldb=b.stride(0), sum=_ptr(s),
+                            ldsum=s.stride(0), sum2=_ptr(sum_copy),
+                            ldsum2=0 if sum_copy is None else sum_copy.stride(0))
+    check(lib().fa_gated_ln_mod_fwd(ctypes.byref(a), _stream(x)))
+    return s, y, mean, rstd
+
+
+def ln_mod_bwd_gate(x, dy, scale, mean, rstd, g, eps: float = 1e-6, dres=None, out=None, gated_out=None):
+    """ln_mod_bwd's dx and g * dx in one pass: returns (dx, g * dx), the bits
+    of ln_mod_bwd followed by gated_residual(None, g, dx)."""
+    x, dy = _rows(x, "x"), _rows(dy, "dy")
+    N, C = x.shape
+    dx = _like(out, x)
+    gdx = _like(gated_out, x, "gated_out")
+    if dres is not None:
+        _rows(dres, "dres")
+    fwd = _abi.LnModArgs(dtype=_dtype_code(x), rows=N, cols=C, eps=float(eps), x=_ptr(x), ldx=x.stride(0),
+                         shift=_ptr(_vec(scale, C, x, "scale")), scale=_ptr(_vec(scale, C, x, "scale")),
+                         mean=_ptr(mean), rstd=_ptr(rstd))
+    bw = _abi.LnModBwdArgs(fwd=fwd, dy=_ptr(dy), lddy=dy.stride(0), dres=_ptr(dres),
+                           ldres=0 if dres is None else dres.stride(0), dx=_ptr(dx), lddx=dx.stride(0))
+    a = _abi.LnModBwdGateArgs(bwd=bw, g=_ptr(_vec(g, C, x, "g")), gdx=_ptr(gdx), ldgdx=gdx.stride(0))
+    check(lib().fa_ln_mod_bwd_gate(ctypes.byref(a), _stream(x)))
+    return dx, gdx
+
+
 def _rows_op(fn, x, g, b, out):
     b = _rows(b, "b")
     N, C = b.shape
@@ -692,8 +735,12 @@ class DoubleBlockLoRA:
         else:
             out = _linear(a, w.w_out, w.b_out, B[f"out.{name}"])
             u_out = lora_fwd(a, w.lora_a["out"], w.lora_b["out"], out, s) if "out" in w.lora_a else None
-        x1 = gated_residual(x[name], g1, out, out=B[f"x1.{name}"])
-        h2, mean2, rstd2 = ln_mod_fwd(x1, sh2, sc2, self.eps, out=B[f"h2.{name}"], stats=True)
+        # the gated residual and the second layer norm in one pass; with the
+        # MLP gate folded into W2, x1 also lands in y, which the W2 GEMM then
+        # accumulates into in place (no separate copy of x1)
+        yb = B[f"y.{name}"]
+        x1, h2, mean2, rstd2 = gated_ln_mod_fwd(x[name], g1, out, sh2, sc2, self.eps, out=B[f"h2.{name}"],
+                                                sum_out=B[f"x1.{name}"], sum_copy=yb if self._fold_g2 else None)
         pre = _linear(h2, w.w1, w.b1, B[f"pre.{name}"])
         M = w.w2.shape[1]
         if self.mlp == "swiglu":
@@ -701,7 +748,7 @@ class DoubleBlockLoRA:
         else:
             act = gelu(pre, out=B[f"act.{name}"])
         if self._fold_g2:
-            y[name] = torch.addmm(x1, act, self._w2g[name].t(), out=B[f"y.{name}"])  # x1 + act W2g^T
+            y[name] = yb.addmm_(act, self._w2g[name].t())  # x1 + act W2g^T
         else:
             mlp = _linear(act, w.w2, w.b2, B[f"mlp.{name}"])
             y[name] = gated_residual(x1, g2, mlp, out=B[f"y.{name}"])
@@ -723,18 +770,19 @@ class DoubleBlockLoRA:
         else:
             dpre = gelu_bwd(dact, pre, out=dact)
         dh2 = torch.mm(dpre, self._dx_weight(name, "w1"), out=B[f"t2.{name}"])
-        dx1 = ln_mod_bwd(x1, dh2, sc2, mean2, rstd2, self.eps, dres=dy[name], out=B[f"dx1.{name}"])
+        # dx1 and dout = g1 * dx1 (the out projection's gradient) in one pass
+        dox = B[f"dox.{name}"] if self._fold_out else None
+        dx1, dout = ln_mod_bwd_gate(x1, dh2, sc2, mean2, rstd2, g1, self.eps, dres=dy[name], out=B[f"dx1.{name}"],
+                                    gated_out=dox[:, :C] if self._fold_out else B[f"t1.{name}"])
         do_rows = B["do"][0, off:off + n].reshape(n, C)
         if self._fold_out:
-            dox, r = B[f"dox.{name}"], self.rank
-            dout = gated_residual(None, g1, dx1, out=dox[:, :C])
+            r = self.rank
             du = lora_down(dout, self._b_out_t[name], s, out=dox[:, C:C + r])  # s dout B_out
             rhs = self._out_ext_t[name].t() if self._wt is not None else self._out_ext[name]
             torch.mm(dox, rhs, out=do_rows)  # dout W_out + du A_out
             # dA_out = du^T a, dB_out = s dout^T u
             saved[(name, "out", "grad")] = tuple(lora_grad_many([(du, a, 1.0, False), (u_out, dout, s, True)]))
             return
-        dout = gated_residual(None, g1, dx1, out=B[f"t1.{name}"])
         torch.mm(dout, self._dx_weight(name, "w_out"), out=do_rows)
         if u_out is not None:
             saved[(name, "out", "grad")] = lora_bwd(a, w.lora_a["out"], w.lora_b["out"], u_out, dout, s,

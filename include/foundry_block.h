@@ -6,6 +6,8 @@
  * linears and its attention (crates/foundry-spike/src/bin/throughput.rs:
  * 480-574, the fixture-sized lib.rs:301-392):
  *   layer_norm_mod   lib.rs:60-71        fa_ln_mod_fwd / fa_ln_mod_bwd
+ *   gated residual + layer_norm_mod   throughput.rs:552-566
+ *                                        fa_gated_ln_mod_fwd / fa_ln_mod_bwd_gate
  *   gated residual   throughput.rs:552-572   fa_gated_residual
  *   MLP activation   (c4 block: tanh-GELU; the reference block's SwiGLU,
  *                    lib.rs:293-297, has no tanh-GELU counterpart)
@@ -63,6 +65,40 @@ typedef struct fa_ln_mod_bwd_args {
  * dn = dy * (1 + scale): the gradient Candle's autograd forms through
  * layer_norm_mod (shift and scale are frozen, so no gradient for them). */
 fa_status fa_ln_mod_bwd(const fa_ln_mod_bwd_args *args, void *stream);
+
+typedef struct fa_gated_ln_mod_args {
+    fa_ln_mod_args ln;    /* x: the residual stream; y, mean, rstd: layer_norm_mod
+                             of the sum below (ln.x is not normalised itself)   */
+    const void *g;        /* [C] gate                                            */
+    const void *b;        /* [N, C] gated branch                                 */
+    int64_t ldb;
+    void *sum;            /* [N, C] output: x + g * b, the norm's input          */
+    int64_t ldsum;
+    void *sum2;           /* [N, C] or NULL: a second copy of the sum            */
+    int64_t ldsum2;
+} fa_gated_ln_mod_args;
+
+/* sum = x + g * b (as fa_gated_residual), then y = layer_norm_mod(sum), in one
+ * pass: the gated residual and the layer_norm_mod that follows it in the
+ * double block (throughput.rs:552-566, lib.rs:60-71), with the bits of
+ * fa_gated_residual followed by fa_ln_mod_fwd on its output.  sum may alias
+ * x or b element for element; y, sum2 and the statistics must not overlap
+ * any other view. */
+fa_status fa_gated_ln_mod_fwd(const fa_gated_ln_mod_args *args, void *stream);
+
+typedef struct fa_ln_mod_bwd_gate_args {
+    fa_ln_mod_bwd_args bwd; /* as for fa_ln_mod_bwd                              */
+    const void *g;        /* [C] gate                                            */
+    void *gdx;            /* [N, C] output: g * dx                               */
+    int64_t ldgdx;
+} fa_ln_mod_bwd_gate_args;
+
+/* dx as fa_ln_mod_bwd, and gdx = g * dx (dx as rounded to the dtype) in the
+ * same pass: the gradient through the gated branch whose sum fed the norm
+ * (Candle's autograd through throughput.rs:552-566), with the bits of
+ * fa_ln_mod_bwd followed by fa_gated_residual (x NULL) on its dx.  gdx must
+ * not overlap dx. */
+fa_status fa_ln_mod_bwd_gate(const fa_ln_mod_bwd_gate_args *args, void *stream);
 
 typedef struct fa_rows_args {
     int32_t dtype;        /* fa_dtype of every view                              */

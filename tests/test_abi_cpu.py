@@ -52,7 +52,8 @@ def test_struct_layouts_match_header(tmp_path):
                "fa_ln_mod_bwd_args": _abi.LnModBwdArgs, "fa_rows_args": _abi.RowsArgs,
                "fa_adamw_args": _abi.AdamwArgs, "fa_swiglu_args": _abi.SwigluArgs,
                "fa_swiglu_bwd_args": _abi.SwigluBwdArgs, "fa_lora_down_args": _abi.LoraDownArgs,
-               "fa_lora_up_args": _abi.LoraUpArgs, "fa_lora_grad_args": _abi.LoraGradArgs}
+               "fa_lora_up_args": _abi.LoraUpArgs, "fa_lora_grad_args": _abi.LoraGradArgs,
+               "fa_gated_ln_mod_args": _abi.GatedLnModArgs, "fa_ln_mod_bwd_gate_args": _abi.LnModBwdGateArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{BLOCK_HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -255,6 +256,50 @@ _FAKE = 1 << 20  # aligned non-null placeholder; validation fails before any use
 
 def _status_name(st):
     return _abi.STATUS_NAMES[st]
+
+
+def test_fused_gated_ln_mod_validates_before_device_work():
+    """fa_gated_ln_mod_fwd and fa_ln_mod_bwd_gate check the layer-norm
+    arguments as their plain forms do, plus the gate, the branch and the
+    extra outputs, before touching a device."""
+    L = lib()
+    ok_dev = _abi.FA_OK if gpu_available() else _abi.FA_ERR_NO_DEVICE
+    ln = _abi.LnModArgs(dtype=0, rows=4, cols=3072, eps=1e-6, x=_FAKE, ldx=3072, shift=_FAKE, scale=_FAKE,
+                        y=_FAKE, ldy=3072)
+    fw = _abi.GatedLnModArgs(ln=ln, g=_FAKE, b=_FAKE, ldb=3072, sum=_FAKE, ldsum=3072)
+    if not gpu_available():
+        assert L.fa_gated_ln_mod_fwd(ctypes.byref(fw), None) == ok_dev
+        fw2 = _abi.GatedLnModArgs.from_buffer_copy(fw)
+        fw2.sum2, fw2.ldsum2 = _FAKE, 3072
+        assert L.fa_gated_ln_mod_fwd(ctypes.byref(fw2), None) == ok_dev
+    for field, val in (("g", 0), ("g", _FAKE + 2), ("b", 0), ("ldb", 3071), ("sum", 0), ("ldsum", 3000),
+                       ("sum2", _FAKE + 8)):
+        bad = _abi.GatedLnModArgs.from_buffer_copy(fw)
+        setattr(bad, field, val)
+        if field == "sum2":
+            bad.ldsum2 = 3072
+        assert L.fa_gated_ln_mod_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+    bad = _abi.GatedLnModArgs.from_buffer_copy(fw)
+    bad.ln.cols = 3070
+    assert L.fa_gated_ln_mod_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.GatedLnModArgs.from_buffer_copy(fw)
+    bad.ln.mean = _FAKE
+    assert L.fa_gated_ln_mod_fwd(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+
+    stats = _abi.LnModArgs.from_buffer_copy(ln)
+    stats.mean, stats.rstd = _FAKE, _FAKE + 256
+    bw = _abi.LnModBwdGateArgs(bwd=_abi.LnModBwdArgs(fwd=stats, dy=_FAKE, lddy=3072, dx=_FAKE, lddx=3072),
+                               g=_FAKE, gdx=_FAKE, ldgdx=3072)
+    if not gpu_available():
+        assert L.fa_ln_mod_bwd_gate(ctypes.byref(bw), None) == ok_dev
+    for field, val in (("g", 0), ("gdx", 0), ("gdx", _FAKE + 4), ("ldgdx", 3071)):
+        bad = _abi.LnModBwdGateArgs.from_buffer_copy(bw)
+        setattr(bad, field, val)
+        assert L.fa_ln_mod_bwd_gate(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG, field
+    bad = _abi.LnModBwdGateArgs.from_buffer_copy(bw)
+    bad.bwd.fwd.mean = 0
+    assert L.fa_ln_mod_bwd_gate(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    assert b"mean and rstd" in L.fa_last_error()
 
 
 def test_block_ops_validate_before_device_work():

@@ -66,6 +66,53 @@ def test_block_ops_match_oracle(dtype, C):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("C", [256, 3072, 4096])
+def test_fused_gated_ln_mod_matches_separate_ops(dtype, C):
+    """gated_ln_mod_fwd gives the bits of gated_residual followed by
+    ln_mod_fwd, and ln_mod_bwd_gate those of ln_mod_bwd followed by
+    gated_residual(None, g, dx): on row views with padded strides (the double
+    block's [dout | du | 0] operand), with the sum written in place over x,
+    and against the oracle."""
+    bf = dtype == torch.bfloat16
+    rng = np.random.default_rng(7 + C)
+    rnd = (lambda a: oracle.bf16_round(a.astype(np.float32))) if bf else (lambda a: a.astype(np.float32))
+    N = 300
+    x, b, dy, dres = (rnd(rng.standard_normal((N, C))) for _ in range(4))
+    sh, sc, g = (rnd(0.1 * rng.standard_normal(C)) for _ in range(3))
+    X, DY, DRES = dev(x, dtype), dev(dy, dtype), dev(dres, dtype)
+    SH, SC, G = dev(sh, dtype), dev(sc, dtype), dev(g, dtype)
+    wide = torch.zeros((N, C + 64), dtype=dtype, device="cuda")
+    wide[:, :C] = dev(b, dtype)
+    Bv = wide[:, :C]  # a strided branch view
+
+    s_ref = fb.gated_residual(X, G, Bv)
+    y_ref, m_ref, r_ref = fb.ln_mod_fwd(s_ref, SH, SC, 1e-6, stats=True)
+    copy = torch.full((N, C + 64), 7.0, dtype=dtype, device="cuda")
+    s, y, m, r = fb.gated_ln_mod_fwd(X, G, Bv, SH, SC, 1e-6, sum_copy=copy[:, :C])
+    torch.cuda.synchronize()
+    for name, got, want in (("sum", s, s_ref), ("y", y, y_ref), ("mean", m, m_ref), ("rstd", r, r_ref),
+                            ("sum_copy", copy[:, :C], s_ref)):
+        assert torch.equal(got, want), name
+    assert bool((copy[:, C:] == 7.0).all()), "sum_copy wrote past its view"
+    inplace = X.clone()
+    s2, y2, _, _ = fb.gated_ln_mod_fwd(inplace, G, Bv, SH, SC, 1e-6, sum_out=inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(inplace, s_ref) and torch.equal(y2, y_ref)
+    ws = oracle.gated_residual(x, g, b, bf16=bf)
+    wy, _, _ = oracle.ln_mod_fwd(ws, sh, sc, 1e-6, bf16=bf)
+    tol = 2e-2 if bf else 1e-4
+    assert rel_l2(host(y), wy) <= tol
+
+    dx_ref = fb.ln_mod_bwd(s_ref, DY, SC, m_ref, r_ref, 1e-6, dres=DRES)
+    gd_ref = fb.gated_residual(None, G, dx_ref)
+    gwide = torch.full((N, C + 64), 7.0, dtype=dtype, device="cuda")
+    dx, gd = fb.ln_mod_bwd_gate(s, DY, SC, m, r, G, 1e-6, dres=DRES, gated_out=gwide[:, :C])
+    torch.cuda.synchronize()
+    assert torch.equal(dx, dx_ref) and torch.equal(gd, gd_ref)
+    assert bool((gwide[:, C:] == 7.0).all()), "gated_out wrote past its view"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_swiglu_fused_views_match_oracle(dtype):
     """silu(gate) * up and its gradients with gate and up read as column
     slices of one fused projection output [N, 3C + 2M] (the single block's
