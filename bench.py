@@ -67,8 +67,9 @@ def parse():
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c5"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample (0 = skip)")
-    ap.add_argument("--block-steps", type=int, default=10,
-                    help="timed c4 LoRA block steps (0 = skip the block measurement)")
+    ap.add_argument("--block-steps", type=int, default=30,
+                    help="timed c4 LoRA block steps (0 = skip the block measurement); the block "
+                         "sections warm up for a third as many steps (at least 2)")
     ap.add_argument("--settle-s", type=float, default=0.3,
                     help="untimed seconds of steps before the warm-up steps (clock ramp)")
     ap.add_argument("--only-headline", action="store_true",
@@ -566,9 +567,9 @@ def main():
         rec["memory_bound"] = memory_bound_bench(torch, fa, cfg)
         rec["ulysses_shards"] = shard_bench(torch, fa, cfg)
         if args.block_steps > 0:
-            rec["block"] = block_bench(torch, args.block_steps, max(2, args.warmup // 4))
-            rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.warmup // 4))
-            rec["checkpointed_stack"] = stack_bench(torch, args.block_steps, max(2, args.warmup // 4))
+            rec["block"] = block_bench(torch, args.block_steps, max(2, args.block_steps // 3))
+            rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.block_steps // 3))
+            rec["checkpointed_stack"] = stack_bench(torch, args.block_steps, max(2, args.block_steps // 3))
     rec["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds) if args.cpu_seconds > 0 and not args.only_headline \
         else None
     print(json.dumps(rec), flush=True)
