@@ -517,7 +517,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build is single-GPU; --gpus {args.gpus} is not supported "
-              "(the attention path shards over (B, H) across GPUs by design, see DESIGN.md)",
+              "(the attention path would shard over heads, one process per GPU, with an all-to-all "
+              "before and after attention; only one GPU's share is measured here)",
               file=sys.stderr)
         return 2
     import torch
