@@ -160,6 +160,26 @@ def _graph_ms(torch, fn, reps: int = 20, replays: int = 5) -> float:
     return ms
 
 
+def box_reference(torch):
+    """Rates of two library operations on this box, measured right after the
+    headline (clocks already up), so that runs on different boxes of the pool
+    can be compared: an 8192^3 bf16 torch.mm and a 1 GiB device-to-device
+    copy, each over 10 timed calls after 3 warm-up calls."""
+    n = 8192
+    a = torch.randn((n, n), device="cuda", dtype=torch.bfloat16)
+    b = torch.randn((n, n), device="cuda", dtype=torch.bfloat16)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    gemm_ms = _event_ms(torch, lambda: torch.mm(a, b), 10)
+    copy_ms = _event_ms(torch, lambda: dst.copy_(src), 10)
+    del a, b, src, dst
+    torch.cuda.empty_cache()
+    return {"bf16_gemm_8192_tflops": round(2 * n ** 3 / (gemm_ms * 1e-3) / 1e12, 1),
+            "copy_1gib_gbs": round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
+            "note": "library GEMM and device copy rates on this box, for comparing runs across boxes; "
+                    "not part of the metric"}
+
+
 def memory_bound_bench(torch, fa, cfg):
     """Achieved HBM rates of the memory-bound kernels around the attention,
     from algorithmic bytes (each tensor read or written once) over HIP-event
@@ -564,6 +584,7 @@ def main():
         "kernels": r["kernels"],
     }
     if not args.only_headline:
+        rec["box_reference"] = box_reference(torch)
         rec["configs"] = configs_bench(torch, fa, args.steps, args.warmup, args.settle_s)
         rec["memory_bound"] = memory_bound_bench(torch, fa, cfg)
         rec["ulysses_shards"] = shard_bench(torch, fa, cfg)
