@@ -114,3 +114,49 @@ def test_saved_lse_is_keyed_on_the_forward_call():
     assert op._saved_lse(q, k.clone(), v, res) is None    # different storage for k
     q.add_(1.0)                                           # q modified in place
     assert op._saved_lse(q, k, v, res) is None
+
+
+@pytest.mark.parametrize("case", ["b_shape", "b_dtype", "g_len", "shift_dtype", "sum_shape", "copy_col_stride",
+                                  "x_col_stride"])
+def test_gated_ln_mod_fwd_rejects(case):
+    """The fused gated residual + layer_norm_mod refuses views that do not
+    match x before anything is launched."""
+    from foundry_attn import block as fb
+    x, b = _x(), _x()
+    g, sh, sc = (torch.zeros(128, dtype=bf) for _ in range(3))
+    kw = {}
+    if case == "b_shape":
+        b = _x(K=96)
+    elif case == "b_dtype":
+        b = _x(dtype=torch.float32)
+    elif case == "g_len":
+        g = torch.zeros(96, dtype=bf)
+    elif case == "shift_dtype":
+        sh = torch.zeros(128, dtype=torch.float32)
+    elif case == "sum_shape":
+        kw["sum_out"] = _x(N=32)
+    elif case == "copy_col_stride":
+        kw["sum_copy"] = torch.zeros(128, 64, dtype=bf).t()
+    else:
+        x = torch.zeros(128, 64, dtype=bf).t()
+    with pytest.raises(FoundryAttnError):
+        fb.gated_ln_mod_fwd(x, g, b, sh, sc, 1e-6, **kw)
+
+
+@pytest.mark.parametrize("case", ["gated_out_shape", "gated_out_dtype", "g_len", "dy_col_stride"])
+def test_ln_mod_bwd_gate_rejects(case):
+    from foundry_attn import block as fb
+    x, dy = _x(), _x()
+    sc, g = torch.zeros(128, dtype=bf), torch.zeros(128, dtype=bf)
+    mean, rstd = torch.zeros(64), torch.ones(64)
+    kw = {}
+    if case == "gated_out_shape":
+        kw["gated_out"] = _x(K=64)
+    elif case == "gated_out_dtype":
+        kw["gated_out"] = _x(dtype=torch.float32)
+    elif case == "g_len":
+        g = torch.zeros(64, dtype=bf)
+    else:
+        dy = torch.zeros(128, 64, dtype=bf).t()
+    with pytest.raises(FoundryAttnError):
+        fb.ln_mod_bwd_gate(x, dy, sc, mean, rstd, g, 1e-6, **kw)
