@@ -19,7 +19,7 @@
 // Every GPU holds its own copy for the life of the process, and every call on
 // one GPU shares it.  On the host `scratch` names a host-side stand-in, not
 // device memory: kernels and copies get the per-device address that
-// init_device looks up (g_scratch), never the array's name.
+// setup_scratch_locked looks up (g_scratch), never the array's name.
 static __device__ __align__(256) unsigned char scratch[FA_BWD_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -70,20 +70,6 @@ fa_status init_device(int device) {
                         device, prop.gcnArchName);
     }
     if (g_dev_state[device] < 0) return fail(FA_ERR_LOAD_FAILED, "device %d is not gfx950", device);
-    if (!g_scratch[device]) {
-        // the symbol's address is per device: look it up with `device` current
-        int cur = 0;
-        hipError_t e = hipGetDevice(&cur);
-        if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-        if (cur != device && (e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
-        void *ptr = nullptr;
-        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        const hipError_t e2 = cur != device ? hipSetDevice(cur) : hipSuccess;
-        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-        if (e2 != hipSuccess) return hip_fail(e2, "hipSetDevice (restore)");
-        if (!ptr || !aligned_ptr(ptr, 256)) return fail(FA_ERR_HIP, "no-allocation scratch is misaligned");
-        g_scratch[device] = ptr;
-    }
     if (!g_prepared) {
         hipError_t e = fa::prepare_attn_kernels();
         if (e != hipSuccess) return hip_fail(e, "kernel attribute setup");
@@ -103,15 +89,36 @@ fa_status init_current() {
 
 bool aligned(const void *p, size_t a) { return aligned_ptr(p, a); }
 
-// Device address of the no-allocation scratch on the current device (set up
-// by init_current, which the caller has run).
+// Looks up, once per device, the device address of the no-allocation scratch
+// (each GPU holds its own copy of `scratch` at its own address) with `device`
+// current; only fa_init and fa_attn_bwd_noalloc need it.  Caller holds
+// g_init_mu.
+fa_status setup_scratch_locked(int device) {
+    if (g_scratch[device]) return FA_OK;
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (cur != device && (e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t e2 = cur != device ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (e2 != hipSuccess) return hip_fail(e2, "hipSetDevice (restore)");
+    if (!ptr || !aligned_ptr(ptr, 256)) return fail(FA_ERR_HIP, "no-allocation scratch is misaligned");
+    g_scratch[device] = ptr;
+    return FA_OK;
+}
+
+// Device address of the no-allocation scratch on the current device, looked
+// up on first use there unless fa_init(device) already did.
 fa_status scratch_for_current(char **out) {
     int dev = 0;
     const hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(FA_ERR_INVALID_ARG, "device %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_init_mu);
-    if (dev < 0 || dev >= kMaxDevices || !g_scratch[dev])
-        return fail(FA_ERR_HIP, "no-allocation scratch of device %d is not set up", dev);
+    const fa_status st = setup_scratch_locked(dev);
+    if (st != FA_OK) return st;
     *out = static_cast<char *>(g_scratch[dev]);
     return FA_OK;
 }
@@ -217,6 +224,10 @@ const char *fa_op_name(void) { return "foundry-attn-bwd"; }
 
 fa_status fa_init(int device) {
     FA_TRY(init_device(device));
+    {
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        FA_TRY(setup_scratch_locked(device));
+    }
     return ok();
 }
 
@@ -477,6 +488,11 @@ static fa_status check_prologue(const fa_qk_prologue_args *a) {
         return fail(FA_ERR_INVALID_ARG, "batch/tokens/heads must be >= 1");
     if ((int64_t)a->tokens * a->heads >= (int64_t(1) << 31) || a->batch > 65535)
         return fail(FA_ERR_UNSUPPORTED, "tokens * heads must be < 2^31 and batch <= 65535");
+    // the kernels form a row's token and head with 24-bit products and an f32
+    // quotient estimate that is exact for heads <= 1024
+    if (a->tokens >= (1 << 24) || a->heads > 1024)
+        return fail(FA_ERR_UNSUPPORTED, "tokens %d, heads %d: this build needs tokens < 2^24 and heads <= 1024",
+                    a->tokens, a->heads);
     if (a->head_dim != 64 && a->head_dim != 128)
         return fail(FA_ERR_UNSUPPORTED, "head_dim %d: this build implements 64 and 128", a->head_dim);
     if (!(a->eps >= 0.f) || !isfinite(a->eps)) return fail(FA_ERR_INVALID_ARG, "eps must be finite, >= 0");

@@ -491,9 +491,11 @@ class DoubleBlockLoRA:
             self.refresh_adapters()
 
     def refresh_frozen(self) -> None:
-        """Re-derive the transposed frozen weights the backward reads (with
-        dx_weights_t), in place."""
+        """Re-derive, in place, every operand formed from the frozen weights:
+        the extended (adapter-carrying) GEMM operands, the gate-folded W2g,
+        and the transposed copies the backward reads (with dx_weights_t)."""
         C = self.C
+        self._refresh_w2g()
         for name in STREAMS:
             w = self.w[name]
             if self._fold:
@@ -508,7 +510,6 @@ class DoubleBlockLoRA:
                     self._b_out_ext[name][:C].copy_(w.b_out)
         if self._wt is None:
             return
-        self._refresh_w2g()
         folded = (("w_qkv",) if self._fold else ()) + (("w_out",) if self._fold_out else ()) + \
             (("w2",) if self._fold_g2 else ())
         for name in STREAMS:

@@ -68,9 +68,10 @@ const char *fa_last_error(void);
 const char *fa_op_name(void);
 
 /* Checks that `device` is a gfx950 GPU and prepares the kernels for it
- * (LDS limits).  Idempotent and thread-safe; the attention entry points call
- * it for the current device on first use.  Replaces the CUDA device/NVRTC
- * setup the reference does through cudarc (src/main.rs:16-38). */
+ * (LDS limits), and looks up the device address of fa_attn_bwd_noalloc's
+ * scratch on it.  Idempotent and thread-safe; the attention entry points call
+ * the device part for the current device on first use.  Replaces the CUDA
+ * device/NVRTC setup the reference does through cudarc (src/main.rs:16-38). */
 fa_status fa_init(int device);
 
 /* ------------------------------------------------------------------------- */
@@ -188,7 +189,11 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *args, int32_t phase, void *s
  * gradients).  All calls on one GPU share its scratch, and every call
  * overwrites all the scratch rows it reads before reading them, so nothing
  * carries over from an earlier call; calls that overlap on one GPU (two
- * streams, or two host threads, at once) race on it. */
+ * streams, or two host threads, at once) race on it.
+ * Graph capture: the first call on a device queries the device and looks up
+ * its scratch address, which must not happen inside a capture.  Call
+ * fa_init(device) (or this function once, eagerly) before capturing; the
+ * calls captured afterwards make only kernel launches on `stream`. */
 fa_status fa_attn_bwd_noalloc(const fa_attn_bwd_args *args, void *stream);
 
 /* ------------------------------------------------------------------------- */
@@ -221,8 +226,8 @@ typedef struct fa_qk_prologue_args {
  * * weight in dtype; rotation in f32, cast back).  Fuses lib.rs:45-58,
  * lib.rs:122-129 and the txt||img concatenation lib.rs:363-365.
  * Views of x, y (and dx): token and head strides below 2^24 elements, and a
- * batch item's rows within 2^31 elements of its first (FA_ERR_UNSUPPORTED
- * otherwise). */
+ * batch item's rows within 2^31 elements of its first; tokens < 2^24 and
+ * heads <= 1024 (FA_ERR_UNSUPPORTED otherwise). */
 fa_status fa_qk_prologue_fwd(const fa_qk_prologue_args *args, void *stream);
 
 typedef struct fa_qk_prologue_bwd_args {

@@ -178,7 +178,21 @@ def test_prologue_validation():
     a.tokens, a.y_stride = 1 << 20, _abi.Strides(0, 3072, 128)  # (2^20 - 1) * 3072 + ... >= 2^31
     assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
     assert b"2^31" in lib().fa_last_error()
-    a.tokens = 4
+    # a row's token and head come from 24-bit products and an f32 quotient
+    # exact for heads <= 1024: 2^24 + 1 tokens of stride 64 span only ~2^30
+    # elements, and 1025 heads of stride 128 fit too, yet both are refused
+    a.tokens, a.heads = (1 << 24) + 1, 1
+    a.x_stride = a.y_stride = _abi.Strides(0, 64, 64)
+    a.head_dim, a.axes[0], a.axes[1], a.axes[2] = 64, 16, 24, 24
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"2^24" in lib().fa_last_error()
+    a.tokens, a.heads = 4, 1025
+    a.x_stride = a.y_stride = _abi.Strides(0, 1025 * 64, 64)
+    assert lib().fa_qk_prologue_fwd(ctypes.byref(a), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"1024" in lib().fa_last_error()
+    a.head_dim, a.axes[0], a.axes[1], a.axes[2] = 128, 16, 56, 56
+    a.x_stride = a.y_stride = st
+    a.tokens, a.heads = 4, 24
     b = _abi.QkPrologueBwdArgs(fwd=a, dy=fake, dx=fake, dx_stride=_abi.Strides(0, 3072, 1 << 24))
     assert lib().fa_qk_prologue_bwd(ctypes.byref(b), None) == _abi.FA_ERR_UNSUPPORTED
     assert b"dx" in lib().fa_last_error()

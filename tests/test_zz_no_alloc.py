@@ -26,11 +26,9 @@ def _inputs(B, S, H, D, dtype, seed, device):
     return mk(), mk(), mk(), mk()
 
 
-def _noalloc_call(q, k, v, o, do, lse, keep, scale):
-    """dq, dk, dv from fa_attn_bwd_noalloc (outputs come from the caller)."""
+def _noalloc_args(q, k, v, o, do, lse, keep, scale, dq, dk, dv):
     B, S, H, D = q.shape
-    dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
-    a = _abi.AttnBwdArgs(dtype=ops._dtype_code(q), batch=B, seq=S, heads=H, head_dim=D, scale=scale,
+    return _abi.AttnBwdArgs(dtype=ops._dtype_code(q), batch=B, seq=S, heads=H, head_dim=D, scale=scale,
                          q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), o=o.data_ptr(),
                          dout=do.data_ptr(), lse=lse.data_ptr(),
                          key_keep=0 if keep is None else keep.data_ptr(),
@@ -39,6 +37,12 @@ def _noalloc_call(q, k, v, o, do, lse, keep, scale):
                          o_stride=ops._strides(o), do_stride=ops._strides(do),
                          dq_stride=ops._strides(dq), dk_stride=ops._strides(dk),
                          dv_stride=ops._strides(dv))
+
+
+def _noalloc_call(q, k, v, o, do, lse, keep, scale):
+    """dq, dk, dv from fa_attn_bwd_noalloc (outputs come from the caller)."""
+    dq, dk, dv = (torch.empty_like(t) for t in (q, k, v))
+    a = _noalloc_args(q, k, v, o, do, lse, keep, scale, dq, dk, dv)
     check(lib().fa_attn_bwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream))
     return dq, dk, dv
 
@@ -91,3 +95,37 @@ def test_noalloc_rejects_rows_past_scratch(device):
                          dk_stride=_abi.Strides(0, 64, 64), dv_stride=_abi.Strides(0, 64, 64))
     assert lib().fa_attn_bwd_noalloc(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
     assert b"2097152 rows" in lib().fa_last_error()
+
+
+def test_noalloc_replays_under_graph_capture(device):
+    """fa_attn_bwd_noalloc captured in a HIP graph, after fa_init on the
+    device (the first call's device query and scratch lookup stay outside the
+    capture): four replays, each after eager work that overwrites the outputs
+    with NaN and the shared scratch with another call's rows, all give the
+    eager call's bits."""
+    assert lib().fa_init(torch.cuda.current_device()) == _abi.FA_OK
+    B, S, H, D = 1, 1000, 4, 128
+    q, k, v, do = _inputs(B, S, H, D, torch.bfloat16, 300, device)
+    keep = torch.ones((B, S), dtype=torch.uint8)
+    keep[:, 100:260] = 0
+    keep = keep.to(device)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.attn_fwd(q, k, v, key_keep=keep, split=False)
+    want = _noalloc_call(q, k, v, o, do, lse, keep, scale)
+    other = _inputs(1, 600, 3, 64, torch.bfloat16, 301, device)
+    o2, lse2 = ops.attn_fwd(*other[:3], split=False)
+    out = tuple(torch.empty_like(t) for t in (q, k, v))
+    a = _noalloc_args(q, k, v, o, do, lse, keep, scale, *out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        check(lib().fa_attn_bwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream))
+    for rep in range(4):
+        for t in out:
+            t.fill_(float("nan"))
+        _noalloc_call(*other[:3], o2, other[3], lse2, None, 0.125)  # rewrites the scratch rows
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for name, got, w in zip(("dq", "dk", "dv"), out, want):
+            assert torch.equal(got, w), (rep, name)
