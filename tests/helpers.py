@@ -24,6 +24,21 @@ def max_abs(a, b) -> float:
     return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
 
 
+def check_gate(label: str, got, want, bf16: bool) -> None:
+    """The north-star gate for one tensor: bf16 rel-L2 <= 1e-2 and max-abs
+    <= 2e-2 x max(1, max|want|) (bf16's spacing is relative, so above unit
+    magnitude the bound scales with the tensor's peak); f32 rel-L2 <= 1e-4.
+    Prints the measured values, peak-relative max-abs included."""
+    r, m = rel_l2(got, want), max_abs(got, want)
+    peak = float(np.max(np.abs(np.asarray(want, np.float64)))) if np.size(want) else 0.0
+    print(f"  {label}: rel_l2={r:.2e} max_abs={m:.2e} max_abs/peak={m / (peak + 1e-30):.2e}", flush=True)
+    if bf16:
+        assert r <= BF16_REL_L2, (label, r)
+        assert m <= BF16_MAX_ABS * max(1.0, peak), (label, m, peak)
+    else:
+        assert r <= F32_REL_L2, (label, r)
+
+
 def cosine(a, b) -> float:
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()

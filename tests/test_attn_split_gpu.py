@@ -81,9 +81,10 @@ def shard_run():
 
 
 def test_ulysses_shard_parity(shard_run):
+    """All 3 heads of the shard against the oracle."""
     cfg, x, g = shard_run
     assert _splits(1, cfg.seq, cfg.heads, cfg.head_dim)[0] > 0
-    compare(g, x["q"], x["k"], x["v"], x["do"], cfg.scale, None, True, (1, 2))
+    compare(g, x["q"], x["k"], x["v"], x["do"], cfg.scale, None, True, (0, cfg.heads))
 
 
 def test_ulysses_shard_properties(shard_run):

@@ -18,9 +18,10 @@ block and the MSE seed after it supplies it, gen_block.py:300-360) and is
 compared at grad/attn/double.{out,q,k,v}, grad/double.img.to_{q,v}.lora_{a,b}
 and grad/inputs/{img,txt}; then one AdamW step against opt1/*.
 
-Gates: the reference's own for these comparisons, cos >= 0.999 and
-rel-L2 <= 2e-2 (lib.rs:28-29), for bf16; rel-L2 <= 1e-4 (the f32 bar) and
-cos >= 0.99999 for fp32."""
+Gates: for bf16, the reference's cos >= 0.999 (lib.rs:28-29) with the
+north-star rel-L2 <= 1e-2 (tighter than the reference's 2e-2); for fp32,
+rel-L2 <= 1e-4 (the reference's fp32 policy, docs/TESTING.md:15) and
+cos >= 0.99999."""
 import numpy as np
 import pytest
 import torch
@@ -31,7 +32,7 @@ from helpers import cosine, load_pipeline_golden, rel_l2
 
 pytestmark = pytest.mark.gpu
 
-GATES = {"fp32": (0.99999, 1e-4), "bf16": (0.999, 2e-2)}
+GATES = {"fp32": (0.99999, 1e-4), "bf16": (0.999, 1e-2)}
 
 
 def build(f, dtype, device):

@@ -2,9 +2,9 @@
 CPU oracle.  Every block op goes through libfoundry_attn.so; the frozen base
 linears are library GEMMs.  Gates: the ops at bf16 max-abs / rel-L2 from the
 attention gates (2e-2 / 1e-2), f32 rel-L2 1e-4 (ln-mod backward 1e-3); the
-whole block step (outputs, LoRA gradients, updated LoRA factors) at the
-reference's own block thresholds, rel-L2 <= 2e-2 in bf16
-(tools/fixtures/PROVENANCE.md:49-53), 1e-3 in f32."""
+whole block step (outputs, input gradients, LoRA gradients) at the same gate
+as attention: bf16 rel-L2 <= 1e-2 with max-abs <= 2e-2 x max(1, peak), f32
+rel-L2 <= 1e-4 (the reference's fp32 policy, docs/TESTING.md:15)."""
 import numpy as np
 import pytest
 import torch
@@ -13,7 +13,7 @@ import block_ref  # noqa: E402  (oracle/ on sys.path via conftest)
 import oracle
 from block_case import make_case, make_single_case, oracle_mods, single_oracle_mods
 from foundry_attn import block as fb
-from helpers import max_abs, rel_l2
+from helpers import check_gate, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -194,7 +194,7 @@ def test_adamw_many_matches_separate_steps(dtype):
             assert torch.equal(x, y)
 
 
-def device_block(case, dtype):
+def device_block(case, dtype, **kw):
     ws = {}
     for name in ("txt", "img"):
         w = case["W"][name]
@@ -209,7 +209,7 @@ def device_block(case, dtype):
                 sw.v[f"{t}.{part}"] = torch.zeros(P.shape, dtype=torch.float32, device="cuda")
         ws[name] = sw
     blk = fb.DoubleBlockLoRA(ws, case["H"], case["D"], case["T"], case["rows"], case["cols"], axes=case["axes"],
-                             lora_scale=case["scale"])
+                             lora_scale=case["scale"], **kw)
     blk.set_conditioning(dev(case["c"], dtype))
     return blk
 
@@ -230,23 +230,17 @@ def test_block_step_matches_oracle(dtype, want_dx):
     torch.cuda.synchronize()
     wy, wgrads, wupd = block_ref.block_step(case["x"], case["dy"], case["W"], case["H"], case["D"], case["cos"],
                                             case["sin"], case["axes"], case["scale"], bf16=bf, want_dx=want_dx)
-    gate = 2e-2 if bf else 1e-3
     for name in ("txt", "img"):
-        r = rel_l2(host(y[name]), wy[name])
-        print(f"  y.{name}: rel_l2={r:.2e}", flush=True)
-        assert r <= gate
+        check_gate(f"y.{name}", host(y[name]), wy[name], bf)
         if want_dx:
-            r = rel_l2(host(grads[(name, "x")]), wgrads[(name, "x")])
-            print(f"  dx.{name}: rel_l2={r:.2e}", flush=True)
-            assert r <= gate
+            check_gate(f"dx.{name}", host(grads[(name, "x")]), wgrads[(name, "x")], bf)
     for key, g in wgrads.items():
         if key[1] == "x":
             continue
         wa, wb = g
         da, db = grads[key]
-        ra, rb = rel_l2(host(da), wa), rel_l2(host(db), wb)
-        print(f"  grad {key}: dA {ra:.2e} dB {rb:.2e}", flush=True)
-        assert ra <= gate and rb <= gate, key
+        check_gate(f"grad {key} dA", host(da), wa, bf)
+        check_gate(f"grad {key} dB", host(db), wb, bf)
         a1, b1 = wupd[key]
         w = blk.w[key[0]]
         # one AdamW step moves each factor by ~lr * sign(g): compare the step
@@ -313,6 +307,41 @@ def test_refresh_adapters_after_changing_factors():
             assert torch.equal(a, b), key
 
 
+@pytest.mark.parametrize("dx_weights_t", [False, True], ids=["strided_dx", "transposed_dx"])
+def test_refresh_frozen_after_changing_weights(dx_weights_t):
+    """Frozen weights changed in place (w_qkv, w_out, w1, w2 of both streams)
+    followed by refresh_frozen() give the bits of a block built from the
+    changed weights: the adapter-carrying qkv / out operands, the gate-folded
+    W2g = diag(g2) W2 and (with dx_weights_t) the transposed copies all follow
+    the new weights."""
+    import copy
+    bf = torch.bfloat16
+    rng = np.random.default_rng(78)
+    case = oracle_mods(make_case(C=256, H=2, T=16, rows=4, cols=8, r=4, bf16=True, seed=8))
+    case2 = copy.deepcopy(case)
+    blk = device_block(case, bf, dx_weights_t=dx_weights_t)
+    assert blk._fold_g2
+    for name in ("txt", "img"):
+        for key in ("w_qkv", "w_out", "w1", "w2"):
+            W = case2["W"][name][key]
+            case2["W"][name][key] = oracle.bf16_round(W + 0.02 * rng.standard_normal(W.shape).astype(np.float32))
+            getattr(blk.w[name], key).copy_(dev(case2["W"][name][key], bf))
+    blk.refresh_frozen()
+    ref = device_block(case2, bf, dx_weights_t=dx_weights_t)
+    x = {k: dev(v, bf) for k, v in case["x"].items()}
+    dy = {k: dev(v, bf) for k, v in case["dy"].items()}
+    (y1, g1), (y2, g2) = (b.forward_backward(x, dy, want_dx=True) for b in (blk, ref))
+    torch.cuda.synchronize()
+    for name in ("txt", "img"):
+        assert torch.equal(y1[name], y2[name]), name
+    assert g1.keys() == g2.keys()
+    for key in g1:
+        parts = (g1[key],) if key[1] == "x" else g1[key]
+        want = (g2[key],) if key[1] == "x" else g2[key]
+        for a, b in zip(parts, want):
+            assert torch.equal(a, b), key
+
+
 def test_c4_block_step_properties():
     """The full c4 block (4096 img + 512 txt tokens, dim 3072): one step gives
     finite outputs, nonzero finite LoRA gradients that repeat bit for bit, and
@@ -350,10 +379,22 @@ def test_c4_full_size_step_matches_oracle():
     """Config c4 at full size (img 4096 = 64 x 64 + txt 512 tokens, dim 3072,
     24 x 128 heads, MLP 4x, LoRA r16 alpha 16 on q/k/v/out of both streams,
     A ~ N(0, 1/r^2), B ~ N(0, 1e-3^2)): one bf16 block step with the
-    block-input gradient against the composed CPU restatement (block_ref),
-    both block outputs, both dX and all 8 adapters' dA/dB at the block gate
-    (rel-L2 <= 2e-2, the reference's threshold), as the reference's block
-    test compares its gradients (block_backward.rs:34-136)."""
+    block-input gradient against the composed CPU restatement (block_ref) of
+    the reference's bf16 algorithm, as the reference's block test compares
+    its gradients (block_backward.rs:34-136).
+
+    Gate: both block outputs, both dX and the v / out adapters' dA / dB at the
+    bf16 gate (rel-L2 <= 1e-2, max-abs <= 2e-2 x max(1, peak)).  The q and k
+    adapters' gradients sit at the bf16 noise floor of this shape and are
+    held to rel-L2 <= 1.5e-2 instead: q and k are RMS-normalised, so the
+    scores have a standard deviation near 11 and the softmax amplifies a
+    one-ulp difference in q or k, and the kernels round dS to bf16 for the
+    dQ / dK MFMAs where the reference runs those two products in f32.  The
+    reference's own bf16 algorithm is as far from exact: every tensor is also
+    compared with the same restatement run in f32, where the bf16 restatement
+    measures 0.46-0.88e-2 rel-L2 and this path 0.46-1.22e-2 (seed 41).  This
+    path must stay within 1.5e-2 of the f32 result for every tensor."""
+    import copy
     case = make_case(C=3072, H=24, T=512, rows=64, cols=64, r=16, alpha=16.0, bf16=True, seed=41)
     for name in ("txt", "img"):
         for t in fb.LORA_TARGETS:
@@ -369,20 +410,42 @@ def test_c4_full_size_step_matches_oracle():
     grads = {k: (host(v) if k[1] == "x" else tuple(host(t) for t in v)) for k, v in grads.items()}
     wy, wgrads, _ = block_ref.block_step(case["x"], case["dy"], case["W"], case["H"], case["D"], case["cos"],
                                          case["sin"], case["axes"], case["scale"], bf16=True, want_dx=True)
-    gate = 2e-2
+    # the same restatement in f32 on the same (bf16-valued) inputs
+    c32 = copy.deepcopy(case)
+    c32["bf16"] = False
+    c32 = oracle_mods(c32)
+    T, I = case["T"], case["rows"] * case["cols"]
+    pos = np.zeros((T + I, 3), np.float32)
+    pos[:T, 0] = np.arange(T)
+    rr, cc = np.meshgrid(np.arange(case["rows"]), np.arange(case["cols"]), indexing="ij")
+    pos[T:, 1], pos[T:, 2] = rr.ravel(), cc.ravel()
+    cos, sin = oracle.rope_tables(pos, case["axes"], 1e4, bf16=False)
+    fy, fgrads, _ = block_ref.block_step(c32["x"], c32["dy"], c32["W"], c32["H"], c32["D"],
+                                         {"txt": cos[:T], "img": cos[T:]}, {"txt": sin[:T], "img": sin[T:]},
+                                         c32["axes"], c32["scale"], bf16=False, want_dx=True)
+
+    def both(label, got, want, want32, noise_floor=False):
+        r32, o32 = rel_l2(got, want32), rel_l2(want, want32)
+        print(f"  {label}: vs f32 restatement {r32:.2e} (bf16 restatement vs f32: {o32:.2e})", flush=True)
+        assert r32 <= 1.5e-2, (label, r32)
+        if not noise_floor:
+            check_gate(label, got, want, True)
+            return
+        r, m = rel_l2(got, want), max_abs(got, want)
+        print(f"  {label}: rel_l2={r:.2e} max_abs={m:.2e} (q/k adapter: rel-L2 gate 1.5e-2)", flush=True)
+        assert r <= 1.5e-2 and m <= 2e-2 * max(1.0, float(np.abs(want).max())), (label, r, m)
+
     for name in ("txt", "img"):
-        for label, got, want in (("y", y[name], wy[name]), ("dx", grads[(name, "x")], wgrads[(name, "x")])):
-            r = rel_l2(got, want)
-            print(f"  {label}.{name}: rel_l2={r:.2e}", flush=True)
-            assert r <= gate, (label, name, r)
+        both(f"y.{name}", y[name], wy[name], fy[name])
+        both(f"dx.{name}", grads[(name, "x")], wgrads[(name, "x")], fgrads[(name, "x")])
     n_adapters = 0
     for key, g in wgrads.items():
         if key[1] == "x":
             continue
-        (wa, wb), (da, db) = g, grads[key]
-        ra, rb = rel_l2(da, wa), rel_l2(db, wb)
-        print(f"  grad {key}: dA {ra:.2e} dB {rb:.2e}", flush=True)
-        assert ra <= gate and rb <= gate, key
+        (wa, wb), (da, db), (fa_, fb_) = g, grads[key], fgrads[key]
+        floor = key[1] in ("q", "k")
+        both(f"grad {key} dA", da, wa, fa_, floor)
+        both(f"grad {key} dB", db, wb, fb_, floor)
         n_adapters += 1
     assert n_adapters == 8
 
@@ -421,16 +484,12 @@ def test_single_block_step_matches_oracle(dtype):
     wy, wgrads, wupd, wdx = block_ref.single_block_step(case["x"], case["dy"], case["W"], case["H"], case["D"],
                                                         case["cos"], case["sin"], case["axes"], case["scale"],
                                                         bf16=bf)
-    gate = 2e-2 if bf else 1e-3
     for name, got, want in (("y", host(y), wy), ("dx", host(grads["x"]), wdx)):
-        r = rel_l2(got, want)
-        print(f"  {name}: rel_l2={r:.2e}", flush=True)
-        assert r <= gate, name
+        check_gate(name, got, want, bf)
     for t in fb.SINGLE_LORA_TARGETS:
         (da, db), (wa, wb) = grads[t], wgrads[t]
-        ra, rb = rel_l2(host(da), wa), rel_l2(host(db), wb)
-        print(f"  grad {t}: dA {ra:.2e} dB {rb:.2e}", flush=True)
-        assert ra <= gate and rb <= gate, t
+        check_gate(f"grad {t} dA", host(da), wa, bf)
+        check_gate(f"grad {t} dB", host(db), wb, bf)
         a1, b1 = wupd[t]
         step_a = host(blk.w.lora_a[t]) - case["W"]["lora_a"][t]
         step_b = host(blk.w.lora_b[t]) - case["W"]["lora_b"][t]

@@ -8,7 +8,8 @@ reference's MSE loss.
    attention forward.
 2. The stack's LoRA gradients and input gradients match the oracle composed
    from block_ref.block_step and block_ref.single_block_step (the same
-   chain rule run on the CPU), at the block-step gates.
+   chain rule run on the CPU), at the north-star gate (bf16 rel-L2 1e-2 and
+   max-abs 2e-2 x max(1, peak); f32 rel-L2 1e-4).
 """
 import numpy as np
 import pytest
@@ -18,7 +19,7 @@ import block_ref
 import oracle
 from block_case import make_case, make_single_case, oracle_mods, single_oracle_mods
 from foundry_attn import checkpoint as ck
-from helpers import rel_l2
+from helpers import check_gate
 from test_block_gpu import dev, device_block, device_single_block, host
 
 pytestmark = pytest.mark.gpu
@@ -91,20 +92,17 @@ def test_checkpointed_stack_matches_oracle(dtype):
     loss, in_grads, grads = ck.checkpointed_step(st, inputs, ck.mse_seed([dev(t, dtype) for t in targets]))
     torch.cuda.synchronize()
     wloss, wd, ws = oracle_stack(dcase, scase, targets, bf)
-    gate = 2e-2 if bf else 1e-3
-    assert abs(float(loss) - wloss) <= gate * wloss
+    rl = abs(float(loss) - wloss) / wloss
+    print(f"  loss: rel={rl:.2e}", flush=True)
+    assert rl <= (1e-2 if bf else 1e-4)
     for name, got in zip(("txt", "img"), in_grads):
-        r = rel_l2(host(got), wd[(name, "x")])
-        print(f"  dx.{name}: {r:.2e}", flush=True)
-        assert r <= gate, name
+        check_gate(f"dx.{name}", host(got), wd[(name, "x")], bf)
     for key, (da, db) in grads[0].items():
-        ra, rb = rel_l2(host(da), wd[key][0]), rel_l2(host(db), wd[key][1])
-        print(f"  double {key}: {ra:.2e} {rb:.2e}", flush=True)
-        assert ra <= gate and rb <= gate, key
+        check_gate(f"double {key} dA", host(da), wd[key][0], bf)
+        check_gate(f"double {key} dB", host(db), wd[key][1], bf)
     for t, (da, db) in grads[2].items():
-        ra, rb = rel_l2(host(da), ws[t][0]), rel_l2(host(db), ws[t][1])
-        print(f"  single {t}: {ra:.2e} {rb:.2e}", flush=True)
-        assert ra <= gate and rb <= gate, t
+        check_gate(f"single {t} dA", host(da), ws[t][0], bf)
+        check_gate(f"single {t} dB", host(db), ws[t][1], bf)
     ck.apply_adamw(st, grads)
     torch.cuda.synchronize()
     assert st[0].block.step_count == 1 and st[2].block.step_count == 1

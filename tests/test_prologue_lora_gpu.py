@@ -337,3 +337,52 @@ def test_prologue_multi_matches_separate_calls(dtype):
     torch.cuda.synchronize()
     for k in x:
         assert torch.equal(dsep[k], done[k]), k
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prologue_bwd_multi_c2_shape_matches_oracle(dtype):
+    """The backward the double block runs, at c2's shape: Q and K of the txt
+    (512 tokens) and img (64 x 64) streams, H = 24, D = 128, in one
+    fa_qk_prologue_bwd_multi launch.  x is the q or k slice of each stream's
+    packed [T, 3, H, D] projection output and dx is written into the same
+    slice of a packed gradient buffer (the block's strides); dy is the joint
+    [1, 4608, H, D] gradient read at each stream's offset.  Every segment
+    against the oracle's chain rule."""
+    from foundry_attn import qk_prologue_bwd_multi
+    bf = dtype == "bf16"
+    tdt = torch.bfloat16 if bf else torch.float32
+    rnd = oracle.bf16_round if bf else (lambda a: a.astype(np.float32))
+    rng = np.random.default_rng(24)
+    H, D, T_txt, S = C2.heads, C2.head_dim, C2.txt_len, C2.seq
+    lens = {"txt": T_txt, "img": S - T_txt}
+    off = {"txt": 0, "img": T_txt}
+    pos = C2.positions()
+    cos, sin = oracle.rope_tables(pos, C2.axes, C2.theta, bf16=bf)
+    tc, ts = rope_tables(pos, C2.axes, C2.theta, dtype=tdt)
+    tab = {n: (tc[off[n]:off[n] + lens[n]].contiguous(), ts[off[n]:off[n] + lens[n]].contiguous()) for n in lens}
+    qkv = {n: rnd(rng.standard_normal((lens[n], 3, H, D)).astype(np.float32)) for n in lens}
+    w = {t: rnd(1 + 0.02 * rng.standard_normal(D).astype(np.float32)) for t in "qk"}
+    dy = {t: rnd(rng.standard_normal((1, S, H, D)).astype(np.float32)) for t in "qk"}
+    tqkv = {n: dev(a, tdt) for n, a in qkv.items()}
+    tdq = {n: torch.full(a.shape, float("nan"), dtype=tdt, device="cuda") for n, a in qkv.items()}
+    tw, tdy = {t: dev(a, tdt) for t, a in w.items()}, {t: dev(a, tdt) for t, a in dy.items()}
+    segs = []
+    for i, t in enumerate("qk"):
+        for n in ("txt", "img"):
+            segs.append((tqkv[n][None, :, i], tw[t], *tab[n], C2.axes, tdy[t], off[n], tdq[n][None, :, i]))
+    qk_prologue_bwd_multi(segs)
+    torch.cuda.synchronize()
+    for i, t in enumerate("qk"):
+        for n in ("txt", "img"):
+            want = oracle.qk_prologue_bwd(qkv[n][:, i], w[t], cos[off[n]:off[n] + lens[n]],
+                                          sin[off[n]:off[n] + lens[n]], dy[t][0, off[n]:off[n] + lens[n]],
+                                          C2.axes)
+            got = host(tdq[n][:, i])
+            r, m = rel_l2(got, want), max_abs(got, want)
+            print(f"  d{t}.{n}: rel_l2={r:.2e} max_abs={m:.2e}", flush=True)
+            if bf:
+                assert r <= BF16_REL_L2 and m <= BF16_MAX_ABS * max(1.0, float(np.abs(want).max())), (t, n)
+            else:
+                assert r <= 1e-5, (t, n)
+    for n in lens:  # the v slices were never written
+        assert torch.isnan(tdq[n][:, 2]).all(), n
