@@ -135,6 +135,11 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
     const bf16 *dobase = static_cast<const bf16 *>(p.dout) + b * p.do_sb + h * p.do_sh;
     const int64_t row0 = ((int64_t)b * H + h) * S;
     const int kj = kt * kKT + wave * 32 + n;  // this lane's key
+    // keep byte of the workgroup's key tid (loaded first; unsplit with a mask)
+    const bool test_keys = !SPLIT && p.keep != nullptr;
+    const int tkey = kt * kKT + tid;
+    const uint32_t tkeep =
+        test_keys && tid < kKT ? (uint32_t)p.keep[(int64_t)b * S + min(tkey, S - 1)] & (tkey < S ? 0xffu : 0u) : 0u;
 
     // K and V rows of this lane's key (B operands): features kd*16 + g*8 .. +8
     bf16x8 kf[D / 16], vf[D / 16];
@@ -182,7 +187,17 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
         for (int r = 0; r < 16; ++r) dk[dt][r] = dv[dt][r] = 0.f;
     const float c = p.scale_log2;
 
+    // A workgroup whose keys are all excluded by the mask streams no queries:
+    // its dK and dV rows are stored as zero below (the unsplit kernel; a
+    // split range's partials are needed by the reduce).  The first stage is
+    // issued before the test, which rarely fails.
     issue(qb0, 0);
+    bool live = true;
+    if (test_keys) {
+        live = __syncthreads_or(tkeep != 0u) != 0;
+        if (!live) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stage lands before the exit
+    }
+    const int qend = live ? qb1 : qb0;
     auto stage = [&](auto par, int qb) {
         constexpr int P = decltype(par)::value;  // (qb - qb0) % 2
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -238,7 +253,7 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
                 }
         }
     };
-    for (int qb = qb0; qb < qb1; qb += 2) {
+    for (int qb = qb0; qb < qend; qb += 2) {
         stage(std::integral_constant<int, 0>{}, qb);
         if (qb + 1 < qb1) stage(std::integral_constant<int, 1>{}, qb + 1);
     }
@@ -343,6 +358,16 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     const uint8_t *keep = KEEP ? p.keep + (int64_t)b * S : nullptr;
     const int qi = qt * kQT + wave * 32 + n;
 
+    // KEEP: groups of four units (128 keys) with no kept key are not
+    // streamed.  Their keep bytes load first, beside the Q and dO rows.
+    __shared__ uint32_t live[KEEP ? kLiveWords : 1];
+    const int g1 = u1 >> 2;
+    const bool track = KEEP && g1 <= kLiveWords * 32;
+    constexpr int kLiveU = 64 / NW;  // groups per wave whose keep bytes load up front
+    uint32_t lv[kLiveU];
+    const __amdgpu_buffer_rsrc_t keep_rs = make_rsrc(keep, (uint32_t)S);
+    if (track) live_mask_issue<NW, 4 * kKU, kLiveU>(keep_rs, u0 >> 2, live, lv);
+
     // distinct LDS objects per buffer (see attn_fwd.hip: lets the compiler
     // keep the prefetch DMA in flight across reads of the other buffers)
     __shared__ __align__(16) char k0[T::BYTES], k1[T::BYTES], k2[T::BYTES], k3[T::BYTES];
@@ -439,11 +464,21 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     // and are fully masked).  Every unit issues its prefetch and its next
     // keep-byte load unconditionally, so each unit sees the same loads in
     // flight and the only waits are the explicit ones at the barriers.
+    // KEEP: ucur is the first unit of the group being processed, unext that
+    // of the next live group (u1 past the last), both set in the prologue;
+    // the j-th unit streamed sits in buffer j % 4.
+    auto next_group = [&](int ufrom) -> int {  // first unit of the first live group at or after ufrom
+        return track ? 4 * next_live_block(live, ufrom >> 2, g1) : ufrom;
+    };
+    int ucur = u0, unext = u0 + 4;
     // keep byte of this lane's key in unit u (clamped address; KEEP only)
     auto keep_byte = [&](int u) -> uint32_t { return KEEP ? keep[min(u * kKU + n, S - 1)] : 1u; };
-    uint32_t kbyte = keep_byte(u0);
-    auto unit = [&](auto par, int u, f32x16 &sc, f32x16 &dc, f32x16 &sn, f32x16 &dn) {
-        constexpr int P = decltype(par)::value;  // u % 4 (u0 is a multiple of 4)
+    uint32_t kbyte = 1u;
+    auto unit = [&](auto par, f32x16 &sc, f32x16 &dc, f32x16 &sn, f32x16 &dn) {
+        constexpr int P = decltype(par)::value;  // position in the group
+        const int u = ucur + P;
+        const int u_after = P < 3 ? u + 1 : unext;             // the unit streamed next
+        const int u_issue = P == 0 ? ucur + 3 : unext + P - 1;  // three units ahead
         // unit u+1 landed (unit u+2, 2*WI loads per wave, may still be in
         // flight, as may the keep byte issued after it); unit u-1 consumed
         barrier_keep_dma<2 * F::WI>();
@@ -454,8 +489,8 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
         if constexpr (KEEP) asm volatile("" : "+v"(kbyte));
         const int key = u * kKU + n;
         const uint64_t km = __ballot(key < S && kbyte != 0);
-        kbyte = keep_byte(u + 1);
-        issue(u + 3, kb_((P + 3) & 3), vb_((P + 3) & 3));
+        kbyte = keep_byte(u_after);
+        issue(u_issue, kb_((P + 3) & 3), vb_((P + 3) & 3));
         const char *kc = kb_(P), *kn = kb_((P + 1) & 3), *vn = vb_((P + 1) & 3);
 
 #pragma unroll
@@ -500,24 +535,48 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
         }
     };
 
-    // prologue: units u0..u0+2 issued, unit u0's scores computed
+    // prologue: the first live group's units 0..2 issued, unit 0's scores
+    // computed (a range with no live group skips everything: dQ = 0).  With
+    // a tracked mask, group u0 / 4 goes out before the live groups are known
+    // (it is live in most ranges), so its latency overlaps the keep bytes'.
     issue(u0, k0, v0);
     issue(u0 + 1, k1, v1);
     issue(u0 + 2, k2, v2);
-    barrier_keep_dma<0>();
-    f32x16 sa0, da0, sa1, da1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sa0[r] = da0[r] = 0.f;
-    sdp(k0, v0, sa0, da0, 0, D / 16);
-    for (int u = u0; u < u1; u += 4) {
-        unit(std::integral_constant<int, 0>{}, u, sa0, da0, sa1, da1);
-        unit(std::integral_constant<int, 1>{}, u + 1, sa1, da1, sa0, da0);
-        unit(std::integral_constant<int, 2>{}, u + 2, sa0, da0, sa1, da1);
-        unit(std::integral_constant<int, 3>{}, u + 3, sa1, da1, sa0, da0);
+    if (track) {
+        barrier_keep_dma<6 * F::WI>();  // zeroed words visible; keep bytes landed
+        live_mask_finish<NW, 4 * kKU, kLiveU>(keep_rs, u0 >> 2, g1, live, lv);
+        barrier_keep_dma<6 * F::WI>();  // live bits visible
+        ucur = next_group(u0);
+        if (ucur < u1) {
+            unext = next_group(ucur + 4);
+            if (ucur != u0) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // group u0's units landed, then are replaced
+                issue(ucur, k0, v0);
+                issue(ucur + 1, k1, v1);
+                issue(ucur + 2, k2, v2);
+            }
+        }
     }
-    // the last prefetches are still writing LDS: they must land before the
-    // workgroup can end
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ucur >= u1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the early DMA lands before the exit
+    if (ucur < u1) {
+        if (KEEP) kbyte = keep_byte(ucur);
+        barrier_keep_dma<0>();
+        f32x16 sa0, da0, sa1, da1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sa0[r] = da0[r] = 0.f;
+        sdp(k0, v0, sa0, da0, 0, D / 16);
+        while (ucur < u1) {
+            unit(std::integral_constant<int, 0>{}, sa0, da0, sa1, da1);
+            unit(std::integral_constant<int, 1>{}, sa1, da1, sa0, da0);
+            unit(std::integral_constant<int, 2>{}, sa0, da0, sa1, da1);
+            unit(std::integral_constant<int, 3>{}, sa1, da1, sa0, da0);
+            ucur = unext;
+            unext = next_group(unext + 4);
+        }
+        // the last prefetches are still writing LDS: they must land before
+        // the workgroup can end
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
 
     if constexpr (SPLIT) {
         if (qi < S) {

@@ -70,8 +70,9 @@ struct FwdState {
     float m_run, m_sc, l_run;
 };
 
-// Key blocks [kb0, kb1) of query tile t (t = (b*H + h)*nq + qt).
-template <int D, int NW>
+// Key blocks [kb0, kb1) of query tile t (t = (b*H + h)*nq + qt).  KEEP: a
+// key mask is given (p.keep); blocks with no kept key are not streamed.
+template <int D, int NW, bool KEEP>
 __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0, int kb1, FwdState<D> &st) {
     using F = FwdTile<D, NW>;
     constexpr int kBM = F::BM;
@@ -87,8 +88,22 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
     const bf16 *qbase = static_cast<const bf16 *>(p.q) + b * p.q_sb + h * p.q_sh;
     const bf16 *kbase = static_cast<const bf16 *>(p.k) + b * p.k_sb + h * p.k_sh;
     const bf16 *vbase = static_cast<const bf16 *>(p.v) + b * p.v_sb + h * p.v_sh;
-    const uint8_t *keep = p.keep ? p.keep + (int64_t)b * S : nullptr;
+    const uint8_t *keep = KEEP ? p.keep + (int64_t)b * S : nullptr;
     const int qi = qt * kBM + wave * 32 + n;  // this lane's query row
+
+    // KEEP: the live 64-key blocks of [kb0, kb1) (uniform over the
+    // workgroup).  The pipeline walks live blocks only: cur is the block
+    // being processed, nx1 and nx2 the next two live blocks (kb1 past the
+    // last); they are set in the prologue.  Without a mask every block is
+    // live.  The keep-byte loads go out first, beside the Q rows.
+    __shared__ uint32_t live[KEEP ? kLiveWords : 1];
+    const bool track = KEEP && kb1 <= kLiveWords * 32;
+    constexpr int kLiveU = 128 / NW;  // blocks per wave whose keep bytes load up front
+    uint32_t lv[kLiveU];
+    const __amdgpu_buffer_rsrc_t keep_rs = make_rsrc(keep, (uint32_t)S);
+    if (track) live_mask_issue<NW, kBN, kLiveU>(keep_rs, kb0, live, lv);
+    auto next_live = [&](int from) -> int { return track ? next_live_block(live, from, kb1) : from; };
+    int cur = kb0, nx1 = kb0 + 1, nx2 = kb0 + 2;
 
     // K and V tiles go straight from HBM/L2 into LDS; rows >= S read as zero
     const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(((S - 1) * p.k_ss + D) * 2));
@@ -194,21 +209,22 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
     // Keep byte of this lane's key in block kb, loaded one block ahead so its
     // latency hides behind a block of work: with one 8-wave workgroup per CU,
     // a load right after the barrier would stall every wave of the CU at once.
-    auto keep_byte = [&](int kb) -> uint32_t { return keep ? keep[min(kb * kBN + lane, S - 1)] : 1u; };
-    uint32_t kbyte = keep_byte(kb0);
+    auto keep_byte = [&](int kb) -> uint32_t { return KEEP ? keep[min(kb * kBN + lane, S - 1)] : 1u; };
+    uint32_t kbyte = 1u;
 
-    // One key block kb, a three-stage software pipeline with no dependency
-    // inside the block: the scores of block kb+1 (MFMA), P of block kb (VALU,
-    // from scores computed one block earlier) and O += P V for block kb-1
-    // (MFMA, with P kept in registers from the previous block) are
+    // One key block (cur), a three-stage software pipeline with no dependency
+    // inside the block: the scores of block nx1 (MFMA), P of block cur (VALU,
+    // from scores computed one block earlier) and O += P V for the previous
+    // block (MFMA, with P kept in registers from the previous block) are
     // interleaved slice by slice.  The reference check closes the block, so
-    // its body is one straight-line region.  K_j sits in ks[j%2] and V_j in
-    // vs[j%2] (relative to kb0); PAR = (kb - kb0) % 2 makes every LDS stage
-    // offset an immediate.  FIRST (kb == kb0) has no block kb-1.
-    auto block = [&](auto par, auto first, int kb, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1,
-                     u32x4 (&pw)[4]) {
+    // its body is one straight-line region.  The j-th block streamed has K in
+    // ks[j%2] and V in vs[j%2]; PAR = j % 2 makes every LDS stage offset an
+    // immediate.  FIRST (j == 0) has no previous block.  The block ends by
+    // advancing cur, nx1, nx2 to the next live blocks.
+    auto block = [&](auto par, auto first, f32x16 &c0, f32x16 &c1, f32x16 &n0, f32x16 &n1, u32x4 (&pw)[4]) {
         constexpr int P = decltype(par)::value;
         constexpr bool FIRST = decltype(first)::value;
+        const int kb = cur;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // K_{kb+1}, V_{kb-1} landed; K_kb and V_{kb-2} fully consumed
         const char *kn = P ? ks0 : ks1;  // K_{kb+1}
@@ -219,12 +235,12 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
         // empty asm keeps its use here (hoisted into the previous block, its
         // wait would also drain the DMA issued after the load).
         uint64_t km = ~0ull;
-        if (keep || (kb + 1) * kBN > S) {
-            if (keep) asm volatile("" : "+v"(kbyte));
+        if (KEEP || (kb + 1) * kBN > S) {
+            if (KEEP) asm volatile("" : "+v"(kbyte));
             const int key = kb * kBN + lane;
             km = __ballot(key < S && kbyte != 0);
         }
-        if (keep && kb + 1 < kb1) kbyte = keep_byte(kb + 1);
+        if (KEEP && nx1 < kb1) kbyte = keep_byte(nx1);
 #pragma unroll
         for (int r = 0; r < 16; ++r) n0[r] = n1[r] = 0.f;
         if (km != ~0ull) {
@@ -249,7 +265,7 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
             // second slice rather than in one burst at the barrier, where it
             // met every wave's first LDS reads (1% off the forward); both
             // buffers are free from the barrier on, and are read next block.
-            if (ks == 1 && kb + 2 < kb1) issue_k(kb + 2, P ? ks1 : ks0);
+            if (ks == 1 && nx2 < kb1) issue_k(nx2, P ? ks1 : ks0);
             if (ks == 2) issue_v(kb, P ? vs1 : vs0);
             make_p(c0, c1, pw, lp, ks);
             // The last block computes scores of a stale K tile that are never
@@ -266,30 +282,68 @@ __device__ __forceinline__ void fwd_tile(const AttnFwdParams &p, int t, int kb0,
             for (int ks = 0; ks < 4; ++ks) make_p(c0, c1, pw, lp, ks);
         }
         l_run += lp;
+        cur = nx1;
+        nx1 = nx2;
+        nx2 = next_live(nx2 + 1);
     };
 
-    // prologue: K_kb0 -> scores of block kb0; K_kb0+1 in flight
+    // prologue: K of the first live block -> its scores; the next live
+    // block's K in flight.  With a tracked mask, K of block kb0 goes out
+    // before the live blocks are known (kb0 is live in most ranges), so its
+    // latency overlaps the keep bytes'.
     f32x16 sa0, sa1, sb0, sb1;
     u32x4 pw[4];
-    issue_k(kb0, ks0);
+    if (track) {
+        issue_k(kb0, ks0);
+        barrier_keep_dma<F::WI>();  // zeroed words visible; keep bytes and Q rows landed
+        live_mask_finish<NW, kBN, kLiveU>(keep_rs, kb0, kb1, live, lv);
+        barrier_keep_dma<F::WI>();  // live bits visible
+        cur = next_live(kb0);
+        if (cur >= kb1) {  // no kept key in the range: O = 0, LSE = -inf
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the early DMA lands before the exit
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st.o[dt][r] = 0.f;
+            st.m_run = -INFINITY;
+            st.m_sc = 0.f;
+            st.l_run = 0.f;
+            return;
+        }
+        nx1 = next_live(cur + 1);
+        nx2 = next_live(nx1 + 1);
+        if (cur != kb0) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block kb0's tile landed, then is replaced
+            issue_k(cur, ks0);
+        }
+    } else {
+        issue_k(cur, ks0);
+    }
+    if (KEEP) kbyte = keep_byte(cur);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (kb0 + 1 < kb1) issue_k(kb0 + 1, ks1);
+    if (nx1 < kb1) issue_k(nx1, ks1);
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa0[r] = sa1[r] = 0.f;
     qk_part(ks0, sa0, sa1, 0, D / 16);
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    block(I0{}, std::true_type{}, kb0, sa0, sa1, sb0, sb1, pw);
-    for (int kb = kb0 + 1; kb < kb1; kb += 2) {
-        block(I1{}, std::false_type{}, kb, sb0, sb1, sa0, sa1, pw);
-        if (kb + 1 < kb1) block(I0{}, std::false_type{}, kb + 1, sa0, sa1, sb0, sb1, pw);
+    int nblk = 1;  // blocks streamed (KEEP; otherwise kb1 - kb0)
+    block(I0{}, std::true_type{}, sa0, sa1, sb0, sb1, pw);
+    while (cur < kb1) {
+        block(I1{}, std::false_type{}, sb0, sb1, sa0, sa1, pw);
+        ++nblk;
+        if (cur < kb1) {
+            block(I0{}, std::false_type{}, sa0, sa1, sb0, sb1, pw);
+            ++nblk;
+        }
     }
-    // epilogue: O += P V for the last block, V_{kb1-1} issued by that block
+    // epilogue: O += P V for the last block, whose V that block issued
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     {
-        const char *vl = ((kb1 - 1 - kb0) & 1) ? vs1 : vs0;
+        const int last = KEEP ? nblk - 1 : kb1 - 1 - kb0;
+        const char *vl = (last & 1) ? vs1 : vs0;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) pv_slice(vl, pw[ks], ks);
     }
@@ -365,8 +419,9 @@ __device__ __forceinline__ void fwd_store_part(const AttnFwdParams &p, int t, in
 }
 
 // One workgroup per NW*32-query tile; 2 waves per SIMD (<= 256 VGPRs).
-// SPLIT: p.split workgroups per tile, each over one key range.
-template <int D, int NW, bool SPLIT>
+// SPLIT: p.split workgroups per tile, each over one key range.  KEEP: a key
+// mask is given.
+template <int D, int NW, bool SPLIT, bool KEEP>
 __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
     const int nkb = (p.S + kBN - 1) / kBN;
     const int w = xcd_remap(blockIdx.x, gridDim.x);
@@ -379,10 +434,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_fwd_bf16_kernel(AttnFwdParams
         split_chunks(p.S, p.split, part, c0, c1);
         constexpr int kBPC = kSplitChunk / kBN;  // key blocks per chunk
         const int t = bh * nq + qt;
-        fwd_tile<D, NW>(p, t, c0 * kBPC, min(c1 * kBPC, nkb), st);
+        fwd_tile<D, NW, KEEP>(p, t, c0 * kBPC, min(c1 * kBPC, nkb), st);
         fwd_store_part<D, NW>(p, t, part, st);
     } else {
-        fwd_tile<D, NW>(p, w, 0, nkb, st);
+        fwd_tile<D, NW, KEEP>(p, w, 0, nkb, st);
         fwd_store<D, NW>(p, w, st);
     }
 }
@@ -589,10 +644,14 @@ hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s) {
     if (p.split > 1) {
         const int nq = (p.S + 255) / 256;
         const dim3 grid(p.B * p.H * nq * p.split), block(512);
-        if (D == 128)
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, true>), grid, block, 0, s, p);
+        if (D == 128 && p.keep)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, true, true>), grid, block, 0, s, p);
+        else if (D == 128)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, true, false>), grid, block, 0, s, p);
+        else if (p.keep)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, true, true>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, true>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, true, false>), grid, block, 0, s, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const int64_t threads = (int64_t)p.B * p.H * p.S * (D / 8);
@@ -607,14 +666,25 @@ hipError_t launch_attn_fwd_bf16(const AttnFwdParams &p, int D, hipStream_t s) {
     const int bm = nw * 32;
     const int nq = (p.S + bm - 1) / bm;
     const dim3 grid(p.B * p.H * nq), block(nw * 64);
-    if (D == 128 && nw == 8)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, false>), grid, block, 0, s, p);
-    else if (D == 128)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 4, false>), grid, block, 0, s, p);
-    else if (nw == 8)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, false>), grid, block, 0, s, p);
-    else
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 4, false>), grid, block, 0, s, p);
+    if (p.keep) {
+        if (D == 128 && nw == 8)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, false, true>), grid, block, 0, s, p);
+        else if (D == 128)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 4, false, true>), grid, block, 0, s, p);
+        else if (nw == 8)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, false, true>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 4, false, true>), grid, block, 0, s, p);
+    } else {
+        if (D == 128 && nw == 8)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 8, false, false>), grid, block, 0, s, p);
+        else if (D == 128)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 4, false, false>), grid, block, 0, s, p);
+        else if (nw == 8)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 8, false, false>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 4, false, false>), grid, block, 0, s, p);
+    }
     return hipGetLastError();
 }
 

@@ -33,6 +33,82 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
+// Live key blocks under a key-padding mask.  Bit kb of `words` is set when
+// block kb (keys [kb*BLK, kb*BLK + BLK) of one batch item) holds a kept key;
+// the kernels then stream only live blocks.  kLiveWords words track
+// kLiveWords*32 blocks; a range with more blocks is not tracked (every block
+// treated as live).  Built once per workgroup in two steps, so that the
+// keep-byte loads share their latency with the kernel's first loads:
+//   live_mask_issue: zero `words` and issue the keep-byte loads of the first
+//     batch: wave w takes the U consecutive blocks kb0 + w*U .. + U - 1, one
+//     byte per lane per load (BLK/64 loads per block) through a buffer
+//     resource over the row's S bytes, so keys past S read as zero;
+//   (the caller issues its own first loads, then a barrier that waits for
+//    LDS writes and for the keep bytes)
+//   live_mask_finish: one ballot per block, the wave's live bits gathered
+//     in a scalar register (blocks >= kb1 dropped) and ORed into at most two
+//     words; further batches of U*NW blocks when the range has more; the
+//     caller's next barrier publishes the words.
+constexpr int kLiveWords = 128;
+template <int BLK, int U>
+__device__ __forceinline__ void live_mask_load(__amdgpu_buffer_rsrc_t keep_rs, int first, uint32_t (&v)[U]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        v[u] = 0u;
+#pragma unroll
+        for (int j = 0; j < BLK; j += 64)
+            v[u] |= __builtin_amdgcn_raw_buffer_load_b8(keep_rs, (first + u) * BLK + j + lane, 0, 0);
+    }
+}
+
+template <int NW, int BLK, int U>
+__device__ __forceinline__ void live_mask_issue(__amdgpu_buffer_rsrc_t keep_rs, int kb0, uint32_t *words,
+                                                uint32_t (&v)[U]) {
+    static_assert(U <= 32, "a wave's blocks span at most two words");
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int i = tid; i < kLiveWords; i += NW * 64) words[i] = 0u;
+    live_mask_load<BLK, U>(keep_rs, kb0 + wave * U, v);
+}
+
+template <int NW, int BLK, int U>
+__device__ __forceinline__ void live_mask_finish(__amdgpu_buffer_rsrc_t keep_rs, int kb0, int kb1, uint32_t *words,
+                                                 uint32_t (&v)[U]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    for (int base = kb0;; base += U * NW) {
+        const int first = base + wave * U;
+        uint32_t m = 0u;  // bit u: block first + u is live (wave-uniform)
+#pragma unroll
+        for (int u = 0; u < U; ++u) m |= (__ballot(v[u] != 0u) != 0ull ? 1u : 0u) << u;
+        const int n = kb1 - first;  // blocks of this wave inside the range
+        m = n <= 0 ? 0u : n >= 32 ? m : m & ((1u << n) - 1u);
+        if (m != 0u && lane == 0) {
+            const uint64_t mm = (uint64_t)m << (first & 31);
+            atomicOr(&words[first >> 5], (uint32_t)mm);
+            if ((uint32_t)(mm >> 32)) atomicOr(&words[(first >> 5) + 1], (uint32_t)(mm >> 32));
+        }
+        if (base + U * NW >= kb1) break;
+        live_mask_load<BLK, U>(keep_rs, base + U * NW + wave * U, v);
+    }
+}
+
+// First live block >= from (wave-uniform), or `end` when blocks [from, end)
+// hold no kept key.  `words` as built by build_live_mask over [kb0, end).
+__device__ __forceinline__ int next_live_block(const uint32_t *words, int from, int end) {
+    if (from >= end) return end;
+    int w = from >> 5;
+    uint32_t bits = __builtin_amdgcn_readfirstlane(words[w]) & (~0u << (from & 31));
+    const int wend = (end + 31) >> 5;
+    while (bits == 0u) {
+        if (++w >= wend) return end;
+        bits = __builtin_amdgcn_readfirstlane(words[w]);
+    }
+    const int r = (w << 5) + __builtin_ctz(bits);
+    return r < end ? r : end;
+}
+
 // One wave-instruction: 16 bytes per lane from rsrc at (voff + soff) to
 // LDS[dst + 16*lane].  dst must be wave-uniform.
 __device__ __forceinline__ void buffer_to_lds_16(__amdgpu_buffer_rsrc_t rsrc, char *dst, uint32_t voff,

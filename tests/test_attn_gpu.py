@@ -196,6 +196,38 @@ def test_fully_masked_batch_item(dtype):
 
 
 @pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("H", [2, 6, 8], ids=["split", "four_wave", "eight_wave"])
+def test_dead_key_blocks_are_skipped(H, D):
+    """Masks whose excluded keys fill whole key blocks, which the kernels do
+    not stream (forward: 64-key blocks; dQ: 128-key groups; dK/dV: a
+    workgroup whose keys are all excluded).  B4 S3000 (47 forward blocks, so
+    the live-block words cross a 32-block boundary): a dead prefix (first
+    live block is block 10), a dead suffix (the last 31 blocks), every third
+    64-key block live, and one kept key (the last).  H picks the grid: 2 the
+    range-split kernels, 6 the 4-wave and 8 the 8-wave ones."""
+    from foundry_attn import attn_workspace_bytes
+    B, S = 4, 3000
+    rng = np.random.default_rng(H * 100 + D)
+    mk = lambda: oracle.bf16_round(rng.standard_normal((B, S, H, D)).astype(np.float32))
+    q, k, v, do = mk(), mk(), mk(), mk()
+    keep = np.ones((B, S), np.uint8)
+    keep[0, :700] = 0
+    keep[1, 1000:] = 0
+    keep[2] = ((np.arange(S) // 64) % 3 == 0).astype(np.uint8)
+    keep[3] = 0
+    keep[3, S - 1] = 1
+    fwd_ws = attn_workspace_bytes(torch.empty(B, S, H, D, dtype=torch.bfloat16, device="cuda"))[0]
+    assert (fwd_ws > 0) == (H == 2), "split policy changed for this case"
+    scale = D ** -0.5
+    g = run_gpu(q, k, v, do, torch.bfloat16, scale, keep)
+    compare(g, q, k, v, do, scale, keep, True, (0, 2))
+    pad = keep == 0
+    for b in range(B):
+        assert not np.any(g["dk"][b][pad[b]]) and not np.any(g["dv"][b][pad[b]]), b
+    assert np.all(np.isfinite(g["o"])) and np.all(np.isfinite(g["lse"]))
+
+
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("masked", [False, True])
 def test_wide_tiles_partial_last_tile(D, masked):
     """B=1, H=40, S=1400 runs the 8-wave (256-row) forward and dK/dV kernels
