@@ -46,17 +46,29 @@ sys.path.insert(0, os.path.join(ROOT, "foundry-trainer_amd"))
 METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at S=4608,D=128; LoRA block steps/s"  # block: rec["block"]
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-# HBM bytes per launch of a kernel: rocprofv3 FETCH_SIZE and WRITE_SIZE runs
-# of this script (--only-headline --calib-copy-mib 256), scaled by what the
-# same counters read for that 256 MiB copy (2.0 x FETCH_SIZE + 1.0 x
-# WRITE_SIZE, KiB).  Kept in profiles/attn_c2_pmc.md; None for a kernel or
-# workload not measured.
-TRAFFIC = {
-    ("c2", "attn_fwd"): int((2.0 * 50771.8 + 28748.9) * 1024),
-    ("c2", "attn_bwd_prepass"): int((2.0 * 29408.5 + 5760.5) * 1024),
-    ("c2", "attn_bwd_dkdv"): int((2.0 * 65710.3 + 56160.0) * 1024),
-    ("c2", "attn_bwd_dq"): int((2.0 * 65789.3 + 28364.9) * 1024),
-}
+# HBM bytes per launch of each attention kernel, per config: the table in
+# profiles/attn_traffic.md, made from rocprofv3 FETCH_SIZE and WRITE_SIZE runs
+# of this script (--only-headline --config <c> --calib-copy-mib 256), scaled
+# by what the same counters read for that 256 MiB copy.  A kernel or config
+# the table does not hold reports traffic null.
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "attn_traffic.md")
+
+
+def load_traffic(path: str = TRAFFIC_TABLE) -> dict:
+    """{(config, kernel): HBM bytes per launch} from the table rows
+    `| config | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes | ...`."""
+    out = {}
+    if not os.path.exists(path):
+        return out
+    with open(path) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 5 and cells[0] in ("c2", "c3", "c5") and cells[4].isdigit():
+                out[(cells[0], cells[1])] = int(cells[4])
+    return out
+
+
+TRAFFIC = load_traffic()
 
 
 def parse():
@@ -513,6 +525,16 @@ def attention_record(cfg, ms: float, kms: dict) -> dict:
     }
 
 
+def roofline(cfg, r: dict) -> dict:
+    """The roofline record of one attention measurement: its dominant
+    kernel's algorithmic rate against the bf16 MFMA peak, and that kernel's
+    HBM bytes per launch from the counter table (null when not measured)."""
+    dom_tf = r["dominant_tflops"]
+    return {"bound": "mfma", "kernel": r["dominant"], "achieved": round(dom_tf, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
+            "traffic": TRAFFIC.get((cfg.name, r["dominant"]))}
+
+
 def configs_bench(torch, fa, steps: int, warmup: int, settle_s: float):
     """c3 and c5 measured as the
     headline is: step time over `steps` timed fwd+bwd steps, then per-launch
@@ -528,7 +550,7 @@ def configs_bench(torch, fa, steps: int, warmup: int, settle_s: float):
                                  + (", key-padding mask (FLOPs count kept keys)" if masked else ""),
                      "ms_per_step": round(ms, 4), "tflops": round(r["value"], 2),
                      "pct_of_peak": round(100 * r["value"] / PEAK_BF16_TFLOPS, 2),
-                     "fwd": r["fwd"], "bwd": r["bwd"], "kernels": r["kernels"]}
+                     "fwd": r["fwd"], "bwd": r["bwd"], "roofline": roofline(cfg, r), "kernels": r["kernels"]}
         torch.cuda.empty_cache()
     return out
 
@@ -555,7 +577,7 @@ def main():
         del src, dst
     ms, kms, masked = attention_bench(torch, fa, cfg, args.steps, args.warmup, args.settle_s)
     r = attention_record(cfg, ms, kms)
-    value, dominant, dom_tf = r["value"], r["dominant"], r["dominant_tflops"]
+    value = r["value"]
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -577,10 +599,7 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "fwd": r["fwd"],
         "bwd": r["bwd"],
-        "roofline": {"bound": "mfma", "kernel": dominant,
-                     "achieved": round(dom_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
-                     "traffic": TRAFFIC.get((cfg.name, dominant))},
+        "roofline": roofline(cfg, r),
         "kernels": r["kernels"],
     }
     if not args.only_headline:
