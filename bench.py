@@ -240,6 +240,34 @@ def memory_bound_bench(torch, fa, cfg):
     return out
 
 
+def gemm_bench(torch):
+    """This build's bf16 GEMM (fa_gemm_bf16) against the tuned library GEMM
+    at the c4 block's W1 shape ([4096, 3072] x [12288, 3072]^T), plain and
+    with the fused GELU epilogue against the library GEMM followed by the
+    GELU kernel: HIP events over 20 calls after 3."""
+    from foundry_attn import block as fb
+    from foundry_attn import gemm_tuning
+    gemm_tuning.enable()
+    g = torch.Generator(device="cuda").manual_seed(11)
+    M, N, K = 4096, 12288, 3072
+    a = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn((N, K), device="cuda", generator=g)).to(torch.bfloat16)
+    c = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+    act = torch.empty_like(c)
+    lib_ms = _event_ms(torch, lambda: torch.mm(a, w.t(), out=c))
+    lib_gelu_ms = _event_ms(torch, lambda: (torch.mm(a, w.t(), out=c), fb.gelu(c, out=act)))
+    own_ms = _event_ms(torch, lambda: fb.gemm(a, w, out=c))
+    own_gelu_ms = _event_ms(torch, lambda: fb.gemm(a, w, "gelu", out=c, act_out=act))
+    tf = lambda ms: round(2 * M * N * K / (ms * 1e-3) / 1e12, 1)
+    del a, w, c, act
+    return {"shape": f"M={M} N={N} K={K} bf16 (c4 W1)",
+            "library_ms": round(lib_ms, 4), "library_tflops": tf(lib_ms),
+            "own_ms": round(own_ms, 4), "own_tflops": tf(own_ms),
+            "library_plus_gelu_ms": round(lib_gelu_ms, 4), "own_fused_gelu_ms": round(own_gelu_ms, 4),
+            "note": "the blocks keep the library GEMM: this GEMM is slower than the tuned library solution "
+                    "by more than the separate GELU pass costs"}
+
+
 def shard_bench(torch, fa, cfg):
     """Attention fwd+bwd at one GPU's share of cfg's heads under P-way
     sequence (Ulysses) parallelism, P = 2, 4, 8: the same kernels at
@@ -607,6 +635,7 @@ def main():
         rec["configs"] = configs_bench(torch, fa, args.steps, args.warmup, args.settle_s)
         rec["memory_bound"] = memory_bound_bench(torch, fa, cfg)
         rec["ulysses_shards"] = shard_bench(torch, fa, cfg)
+        rec["gemm_mlp"] = gemm_bench(torch)
         if args.block_steps > 0:
             rec["block"] = block_bench(torch, args.block_steps, max(2, args.block_steps // 3))
             rec["single_block"] = single_block_bench(torch, args.block_steps, max(2, args.block_steps // 3))

@@ -1017,6 +1017,31 @@ fa_status fa_ln_mod_bwd_gate(const fa_ln_mod_bwd_gate_args *a, void *stream) {
     return ok();
 }
 
+fa_status fa_gemm_bf16(const fa_gemm_args *a, void *stream) {
+    if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
+    if (a->epilogue < FA_GEMM_PLAIN || a->epilogue > FA_GEMM_DGELU)
+        return fail(FA_ERR_INVALID_ARG, "unknown epilogue %d", a->epilogue);
+    if (a->m < 256 || a->n < 256 || a->k < 64 || a->m % 256 || a->n % 256 || a->k % 64)
+        return fail(FA_ERR_UNSUPPORTED, "m %d, n %d, k %d: this build needs m, n multiples of 256 and k of 64",
+                    a->m, a->n, a->k);
+    FA_TRY(check_row_view("a", a->a, a->lda, a->k, FA_DTYPE_BF16));
+    FA_TRY(check_row_view("b", a->b, a->ldb, a->k, FA_DTYPE_BF16));
+    FA_TRY(check_row_view("c", a->c, a->ldc, a->n, FA_DTYPE_BF16));
+    if (a->epilogue == FA_GEMM_GELU) FA_TRY(check_row_view("c2", a->c2, a->ldc2, a->n, FA_DTYPE_BF16));
+    if (a->epilogue == FA_GEMM_DGELU) FA_TRY(check_row_view("aux", a->aux, a->ldaux, a->n, FA_DTYPE_BF16));
+    // buffer offsets within one 256-row block of a or b are 32-bit
+    if ((255 * a->lda + a->k) * 2 >= (int64_t(1) << 31) || (255 * a->ldb + a->k) * 2 >= (int64_t(1) << 31))
+        return fail(FA_ERR_UNSUPPORTED, "a 256-row block of a or b spans 2^31 bytes or more");
+    FA_TRY(init_current());
+    fa::GemmParams p{};
+    p.a = a->a; p.lda = a->lda; p.b = a->b; p.ldb = a->ldb;
+    p.c = a->c; p.ldc = a->ldc; p.c2 = a->c2; p.ldc2 = a->ldc2; p.aux = a->aux; p.ldaux = a->ldaux;
+    p.M = a->m; p.N = a->n; p.K = a->k; p.epi = a->epilogue;
+    const hipError_t e = fa::launch_gemm_tn_bf16(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "gemm launch");
+    return ok();
+}
+
 fa_status fa_gated_residual(const fa_rows_args *a, void *stream) { return rows_op(a, 0, stream); }
 fa_status fa_gelu_fwd(const fa_rows_args *a, void *stream) { return rows_op(a, 1, stream); }
 fa_status fa_gelu_bwd(const fa_rows_args *a, void *stream) { return rows_op(a, 2, stream); }

@@ -228,3 +228,18 @@ struct AdamwMany {
 hipError_t launch_adamw_many(AdamwMany p, int dtype, hipStream_t s);
 
 }  // namespace fa
+
+namespace fa {
+// C[M, N] = A[M, K] B[N, K]^T, bf16, with a fused epilogue (gemm.hip).
+// M and N multiples of 256, K a multiple of 64; rows 16-byte aligned.
+constexpr int kGemmNone = 0, kGemmGelu = 1, kGemmDgelu = 2;
+struct GemmParams {
+    const void *a, *b;  // A [M, K] (lda), B [N, K] (ldb)
+    void *c;            // C [M, N] (ldc): T(acc), pre (GELU) or the GELU gradient (DGELU)
+    void *c2;           // GELU: gelu(pre) [M, N] (ldc2)
+    const void *aux;    // DGELU: the saved pre-activation [M, N] (ldaux)
+    int64_t lda, ldb, ldc, ldc2, ldaux;
+    int M, N, K, epi;
+};
+hipError_t launch_gemm_tn_bf16(const GemmParams &p, hipStream_t s);
+}  // namespace fa

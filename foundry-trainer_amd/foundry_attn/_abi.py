@@ -31,7 +31,7 @@ EXPORTED = [
     "fa_swiglu_fwd", "fa_swiglu_bwd", "fa_adamw_step", "fa_adamw_step_many", "fa_copy2d_many",
     "fa_lora_down", "fa_lora_up", "fa_lora_grad", "fa_lora_grad_workspace_size",
     "fa_lora_grad_many", "fa_lora_grad_many_workspace_size",
-    "fa_gated_ln_mod_fwd", "fa_ln_mod_bwd_gate",
+    "fa_gated_ln_mod_fwd", "fa_ln_mod_bwd_gate", "fa_gemm_bf16",
 ]
 
 
@@ -197,6 +197,18 @@ class Copy2dArgs(ctypes.Structure):
     ]
 
 
+FA_GEMM_PLAIN, FA_GEMM_GELU, FA_GEMM_DGELU = 0, 1, 2
+
+
+class GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("epilogue", ctypes.c_int32), ("m", ctypes.c_int32), ("n", ctypes.c_int32), ("k", ctypes.c_int32),
+        ("a", ctypes.c_void_p), ("lda", ctypes.c_int64), ("b", ctypes.c_void_p), ("ldb", ctypes.c_int64),
+        ("c", ctypes.c_void_p), ("ldc", ctypes.c_int64), ("c2", ctypes.c_void_p), ("ldc2", ctypes.c_int64),
+        ("aux", ctypes.c_void_p), ("ldaux", ctypes.c_int64),
+    ]
+
+
 _lib = None
 
 
@@ -244,7 +256,8 @@ def lib() -> ctypes.CDLL:
                      ("fa_gated_residual", RowsArgs), ("fa_gelu_fwd", RowsArgs),
                      ("fa_gelu_bwd", RowsArgs), ("fa_silu", RowsArgs), ("fa_adamw_step", AdamwArgs),
                      ("fa_swiglu_fwd", SwigluArgs), ("fa_swiglu_bwd", SwigluBwdArgs),
-                     ("fa_lora_down", LoraDownArgs), ("fa_lora_up", LoraUpArgs), ("fa_lora_grad", LoraGradArgs)):
+                     ("fa_lora_down", LoraDownArgs), ("fa_lora_up", LoraUpArgs), ("fa_lora_grad", LoraGradArgs),
+                     ("fa_gemm_bf16", GemmArgs)):
         fn = getattr(L, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]

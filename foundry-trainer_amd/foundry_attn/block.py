@@ -182,6 +182,32 @@ def silu(b, out=None):
     return _rows_op("fa_silu", None, None, b, out)
 
 
+def gemm(a, w, epilogue: str = "plain", out=None, act_out=None, pre=None):
+    """a [M, K] @ w[N, K]^T in bf16 with f32 accumulation (fa_gemm_bf16), one
+    launch with a fused epilogue:
+      "plain": returns bf16(a w^T);
+      "gelu":  returns (pre, act), pre = bf16(a w^T), act = bf16(gelu(pre));
+      "dgelu": returns bf16(bf16(a w^T) * gelu'(pre)) for the saved `pre`.
+    M and N multiples of 256, K of 64; bf16 row views."""
+    epi = {"plain": _abi.FA_GEMM_PLAIN, "gelu": _abi.FA_GEMM_GELU, "dgelu": _abi.FA_GEMM_DGELU}[epilogue]
+    a, w = _rows(a, "a"), _rows(w, "w")
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K or a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("gemm: a [M, K] and w [N, K] must be bf16 with the same K")
+    c = out if out is not None else torch.empty((M, N), dtype=a.dtype, device=a.device)
+    c2 = None
+    if epi == _abi.FA_GEMM_GELU:
+        c2 = act_out if act_out is not None else torch.empty_like(c)
+    if epi == _abi.FA_GEMM_DGELU and pre is None:
+        raise ValueError("gemm: the dgelu epilogue needs the saved pre-activation")
+    args = _abi.GemmArgs(epilogue=epi, m=M, n=N, k=K, a=_ptr(a), lda=a.stride(0), b=_ptr(w), ldb=w.stride(0),
+                         c=_ptr(c), ldc=c.stride(0), c2=_ptr(c2), ldc2=0 if c2 is None else c2.stride(0),
+                         aux=_ptr(pre), ldaux=0 if pre is None else pre.stride(0))
+    check(lib().fa_gemm_bf16(ctypes.byref(args), _stream(a)))
+    return (c, c2) if epi == _abi.FA_GEMM_GELU else c
+
+
 def _same_rows(t: torch.Tensor, ref: torch.Tensor, name: str) -> torch.Tensor:
     _rows(t, name)
     if t.shape != ref.shape or t.dtype != ref.dtype or t.device != ref.device:

@@ -17,6 +17,10 @@
  *                                        fa_swiglu_fwd / fa_swiglu_bwd
  *   modulation input silu(temb)  throughput.rs:297-324     fa_silu
  *   adamw_step       lib.rs:477-510      fa_adamw_step, fa_adamw_step_many
+ *   MLP linear + activation  linear_scaled's base product lib.rs:270-287
+ *                    at throughput.rs:254-256, fused with the GELU that
+ *                    follows W1 or the GELU gradient after W2's dX
+ *                                        fa_gemm_bf16
  *
  * Row views: `rows` x `cols` elements, row r starting at base + r * ld
  * elements; cols % 8 == 0, ld >= cols, and base and ld keep every row
@@ -204,6 +208,41 @@ typedef struct fa_copy2d_args {
  * here keep copies of the factors inside the frozen GEMMs' operands and
  * transposed, and refresh them after each AdamW step with one such call. */
 fa_status fa_copy2d_many(const fa_copy2d_args *args, int32_t count, void *stream);
+
+/* Epilogues of fa_gemm_bf16. */
+typedef enum fa_gemm_epilogue {
+    FA_GEMM_PLAIN = 0,  /* c = bf16(acc)                                         */
+    FA_GEMM_GELU = 1,   /* c = pre = bf16(acc), c2 = bf16(gelu(pre))             */
+    FA_GEMM_DGELU = 2   /* c = bf16(bf16(acc) * gelu'(aux)), aux = the saved pre */
+} fa_gemm_epilogue;
+
+typedef struct fa_gemm_args {
+    int32_t epilogue;     /* fa_gemm_epilogue                                    */
+    int32_t m, n, k;      /* m, n multiples of 256; k a multiple of 64, >= 64    */
+    const void *a;        /* [m, k] bf16 (x), row stride lda                     */
+    int64_t lda;
+    const void *b;        /* [n, k] bf16 (W as stored by a linear), stride ldb   */
+    int64_t ldb;
+    void *c;              /* [m, n] bf16 output, stride ldc                      */
+    int64_t ldc;
+    void *c2;             /* FA_GEMM_GELU: [m, n] bf16 gelu(c), stride ldc2      */
+    int64_t ldc2;
+    const void *aux;      /* FA_GEMM_DGELU: [m, n] bf16 pre-activation, ldaux    */
+    int64_t ldaux;
+} fa_gemm_args;
+
+/* c = a b^T (bf16 in, f32 accumulation) with the epilogue, one launch.  The
+ * base product of linear_scaled (lib.rs:270-287) for the c4 block's MLP
+ * linears (throughput.rs:480-574), fused with the elementwise op after it:
+ * W1's forward with its GELU (FA_GEMM_GELU, c holds the pre-activation the
+ * backward needs), and W2's dX product with the GELU gradient (FA_GEMM_DGELU:
+ * the result is the gradient at W1's output).  The product is rounded to bf16
+ * before the epilogue, as the reference's bf16 matmul output is; gelu is the
+ * tanh form of fa_gelu_fwd / fa_gelu_bwd.  Views: 16-byte aligned bases, row
+ * strides multiples of 8 elements and >= k (a, b) or >= n (c, c2, aux);
+ * c and c2 must not overlap a, b or aux; a 256-row block of a or b must span
+ * fewer than 2^31 bytes. */
+fa_status fa_gemm_bf16(const fa_gemm_args *args, void *stream);
 
 #ifdef __cplusplus
 }

@@ -53,7 +53,8 @@ def test_struct_layouts_match_header(tmp_path):
                "fa_adamw_args": _abi.AdamwArgs, "fa_swiglu_args": _abi.SwigluArgs,
                "fa_swiglu_bwd_args": _abi.SwigluBwdArgs, "fa_lora_down_args": _abi.LoraDownArgs,
                "fa_lora_up_args": _abi.LoraUpArgs, "fa_lora_grad_args": _abi.LoraGradArgs,
-               "fa_gated_ln_mod_args": _abi.GatedLnModArgs, "fa_ln_mod_bwd_gate_args": _abi.LnModBwdGateArgs}
+               "fa_gated_ln_mod_args": _abi.GatedLnModArgs, "fa_ln_mod_bwd_gate_args": _abi.LnModBwdGateArgs,
+               "fa_gemm_args": _abi.GemmArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{BLOCK_HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -468,3 +469,34 @@ def test_public_headers_are_plain_c():
         r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-fsyntax-only",
                             "-I", inc, "-x", "c", "-"], input=src, capture_output=True, text=True)
         assert r.returncode == 0, (h, r.stderr)
+
+
+def test_gemm_validation():
+    """fa_gemm_bf16 refuses shapes off its 256 x 256 x 64 tiles, bad views,
+    unknown epilogues and a missing GELU input before any device work."""
+    fake = 1 << 20
+    a = _abi.GemmArgs(epilogue=0, m=512, n=256, k=128, a=fake, lda=128, b=fake, ldb=128, c=fake, ldc=256,
+                      c2=0, ldc2=0, aux=0, ldaux=0)
+    for field, value in (("m", 300), ("n", 128), ("k", 96), ("k", 0)):
+        bad = _abi.GemmArgs.from_buffer_copy(a)
+        setattr(bad, field, value)
+        assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_UNSUPPORTED, field
+    bad = _abi.GemmArgs.from_buffer_copy(a)
+    bad.epilogue = 3
+    assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.GemmArgs.from_buffer_copy(a)
+    bad.lda = 64  # < k
+    assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.GemmArgs.from_buffer_copy(a)
+    bad.a = fake + 2  # not 16-byte aligned
+    assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.GemmArgs.from_buffer_copy(a)
+    bad.epilogue = _abi.FA_GEMM_DGELU  # no aux
+    assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.GemmArgs.from_buffer_copy(a)
+    bad.epilogue = _abi.FA_GEMM_GELU  # no c2
+    assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_INVALID_ARG
+    bad = _abi.GemmArgs.from_buffer_copy(a)
+    bad.lda = bad.ldb = 1 << 23  # a 256-row block spans >= 2^31 bytes
+    assert lib().fa_gemm_bf16(ctypes.byref(bad), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"2^31" in lib().fa_last_error()
