@@ -240,6 +240,7 @@ struct GemmParams {
     const void *aux;    // DGELU: the saved pre-activation [M, N] (ldaux)
     int64_t lda, ldb, ldc, ldc2, ldaux;
     int M, N, K, epi;
+    int group_m;  // set by the launcher: M tiles per band of the tile order
 };
 hipError_t launch_gemm_tn_bf16(const GemmParams &p, hipStream_t s);
 }  // namespace fa
