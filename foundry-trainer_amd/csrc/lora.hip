@@ -99,10 +99,12 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(const float *__restric
 
 // ---- rowdot / expand, bf16 (MFMA) ---------------------------------------
 // rowdot: out[n][j] = s * sum_k X[n][k] W[j][k], R <= 16 * NT.  A workgroup
-// of 8 waves owns 16 rows; wave w takes k-steps (32 wide) w, w + 8, ..., four
-// at a time with all their loads issued before the MFMAs, and the 8 partial
-// tiles are summed in LDS in a fixed order (deterministic, no workspace).
-// Rows >= N and j >= R load from a clamped (valid) row and are zeroed.
+// of 8 waves owns 16 rows; wave w takes k-steps (32 wide) w, w + 8, ..., U
+// at a time with all their loads issued before the MFMAs (U = 12: at K = 3072
+// a wave's whole range), and the 8 partial tiles are summed in LDS in a fixed
+// order (deterministic, no workspace).  Rows >= N
+// and j >= R load from a clamped (valid) row: output element (n, j) depends
+// on row n of X and row j of W only, and those outputs are not stored.
 template <int NT, typename TO>
 __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restrict__ X, int64_t ldx,
                                                             const bf16 *__restrict__ W, TO *out, int64_t ldo,
@@ -112,50 +114,49 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, q = lane >> 4;
     const int row0 = blockIdx.x * 16;
-    const bool xin = row0 + m < N;
     const bf16 *xp = X + (int64_t)min(row0 + m, N - 1) * ldx + q * 8;
     const bf16 *wp[NT];
-    bool win[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        win[t] = t * 16 + m < R;
-        wp[t] = W + (int64_t)min(t * 16 + m, R - 1) * K + q * 8;
-    }
+    for (int t = 0; t < NT; ++t) wp[t] = W + (int64_t)min(t * 16 + m, R - 1) * K + q * 8;
     const u32x4 zero = {0, 0, 0, 0};
     f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    constexpr int U = NT <= 3 ? 12 : 6;  // VGPRs: 4 U (1 + NT) for the loads
     const int nfull = K / 32;
-    int i = wave;
-    for (; i + 24 < nfull; i += 32) {
-        u32x4 a[4], w[4][NT];
+    const int J = nfull > wave ? (nfull - wave + 7) / 8 : 0;  // this wave's k-steps
+    // k-steps j0 .. j0+U-1 of the wave (only those below J unless FULL)
+    auto group = [&](int j0, auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        u32x4 a[U], w[U][NT];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            a[u] = ld_global_16(xp + (i + 8 * u) * 32);
+        for (int u = 0; u < U; ++u)
+            if (FULL || j0 + u < J) {
+                const int off = (wave + 8 * (j0 + u)) * 32;
+                a[u] = ld_global_16(xp + off);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) w[u][t] = ld_global_16(wp[t] + (i + 8 * u) * 32);
-        }
+                for (int t = 0; t < NT; ++t) w[u][t] = ld_global_16(wp[t] + off);
+            }
+        // every load of the group goes out before the first MFMA waits (left
+        // to the scheduler, about 10 were in flight and the rest trickled out
+        // between the MFMAs, one latency per few loads)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
+            if (FULL || j0 + u < J)
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                acc[t] = mfma_16x16x32(as_bf16x8(xin ? a[u] : zero), as_bf16x8(win[t] ? w[u][t] : zero), acc[t]);
-    }
-    for (; i < nfull; i += 8) {
-        const u32x4 a = ld_global_16(xp + i * 32);
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-            acc[t] = mfma_16x16x32(as_bf16x8(xin ? a : zero),
-                                   as_bf16x8(win[t] ? ld_global_16(wp[t] + i * 32) : zero), acc[t]);
-    }
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_16x16x32(as_bf16x8(a[u]), as_bf16x8(w[u][t]), acc[t]);
+    };
+    int j0 = 0;
+    for (; j0 + U <= J; j0 += U) group(j0, std::true_type{});
+    if (j0 < J) group(j0, std::false_type{});
     if (K % 32 && wave == (nfull & 7)) {
         // K % 32 == 16: lanes q < 2 hold the last 16 columns, q >= 2 are past K
         const bool kin = q < 2;
         const u32x4 a = kin ? ld_global_16(xp + nfull * 32) : zero;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-            acc[t] = mfma_16x16x32(as_bf16x8(xin ? a : zero),
-                                   as_bf16x8(win[t] && kin ? ld_global_16(wp[t] + nfull * 32) : zero), acc[t]);
+            acc[t] = mfma_16x16x32(as_bf16x8(a), as_bf16x8(kin ? ld_global_16(wp[t] + nfull * 32) : zero), acc[t]);
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t)
