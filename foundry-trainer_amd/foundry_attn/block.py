@@ -392,7 +392,7 @@ class DoubleBlockLoRA:
                  lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
                  tuned_gemms: bool = True, batch_qkv_adapters: bool = True, mlp: str = "gelu",
                  positions: Optional[np.ndarray] = None, dx_weights_t: bool = True,
-                 fold_qkv_adapters: bool = True, fold_mlp_gate: bool = True):
+                 fold_qkv_adapters: bool = True, fold_mlp_gate: bool = True, fused_gelu: bool = False):
         """positions: [S, n_axes] RoPE position ids of the joint sequence (txt
         rows first); None gives txt (l, 0, 0), img (0, r, c).
 
@@ -421,7 +421,14 @@ class DoubleBlockLoRA:
         modulation, fixed by set_conditioning) scales the rows of W2 once,
         W2g = diag(g2) W2.  Then y = x1 + act W2g^T is one GEMM with x1 as its
         accumulator input, and the backward's dact = (g2 * dy) W2 = dy W2g
-        needs no separate g2 * dy pass."""
+        needs no separate g2 * dy pass.
+
+        fused_gelu (GELU MLP, bf16, no W1 bias, token and MLP widths multiples
+        of 256): W1's forward and W2's dX product run as this library's GEMM
+        (fa_gemm_bf16) with the GELU and GELU-gradient epilogues, in place of
+        the library GEMM followed by a separate GELU / GELU-backward pass.
+        The backward's operand is W2's (or W2g's) transposed copy, so it also
+        needs dx_weights_t."""
         if mlp not in ("gelu", "swiglu"):
             raise ValueError(f"mlp must be 'gelu' or 'swiglu', not {mlp!r}")
         self.w = weights
@@ -460,6 +467,7 @@ class DoubleBlockLoRA:
         self._wt = {name: {} for name in STREAMS} if dx_weights_t else None
         self._fold_g2 = fold_mlp_gate and all(weights[name].b2 is None for name in STREAMS)
         self._w2g, self._w2g_t = {}, {}
+        self._fused_gelu = fused_gelu
         if tuned_gemms and self.dtype == torch.bfloat16:
             gemm_tuning.enable()
         ranks = {int(a.shape[0]) for w in weights.values() for a in w.lora_a.values()}
@@ -567,6 +575,14 @@ class DoubleBlockLoRA:
                     self._w2g_t[name].copy_(w2g.t())
                 else:
                     self._w2g_t[name] = w2g.t().contiguous()
+
+    def _gelu_fused(self, name: str, backward: bool) -> bool:
+        """Whether stream `name`'s MLP runs W1 (forward) or W2's dX product
+        (backward) as fa_gemm_bf16 with the GELU epilogue."""
+        w = self.w[name]
+        ok = (self._fused_gelu and self.mlp == "gelu" and self.dtype == torch.bfloat16 and w.b1 is None
+              and self.rows[name] % 256 == 0 and w.w1.shape[0] % 256 == 0 and self.C % 64 == 0)
+        return ok and (not backward or self._wt is not None)
 
     def _dx_weight(self, name: str, key: str) -> torch.Tensor:
         """W of stream `name` as the right operand of dX = dY W."""
@@ -768,12 +784,15 @@ class DoubleBlockLoRA:
         yb = B[f"y.{name}"]
         x1, h2, mean2, rstd2 = gated_ln_mod_fwd(x[name], g1, out, sh2, sc2, self.eps, out=B[f"h2.{name}"],
                                                 sum_out=B[f"x1.{name}"], sum_copy=yb if self._fold_g2 else None)
-        pre = _linear(h2, w.w1, w.b1, B[f"pre.{name}"])
         M = w.w2.shape[1]
-        if self.mlp == "swiglu":
-            act = swiglu(pre[:, :M], pre[:, M:], out=B[f"act.{name}"])
+        if self._gelu_fused(name, backward=False):
+            pre, act = gemm(h2, w.w1, "gelu", out=B[f"pre.{name}"], act_out=B[f"act.{name}"])
         else:
-            act = gelu(pre, out=B[f"act.{name}"])
+            pre = _linear(h2, w.w1, w.b1, B[f"pre.{name}"])
+            if self.mlp == "swiglu":
+                act = swiglu(pre[:, :M], pre[:, M:], out=B[f"act.{name}"])
+            else:
+                act = gelu(pre, out=B[f"act.{name}"])
         if self._fold_g2:
             y[name] = yb.addmm_(act, self._w2g[name].t())  # x1 + act W2g^T
         else:
@@ -785,17 +804,22 @@ class DoubleBlockLoRA:
         if dy is None:
             return
         # backward: y = x1 + g2 * mlp(h2), h2 = ln_mod(x1), x1 = x + g1 * out(a)
-        if self._fold_g2:  # (g2 * dy) W2 = dy W2g
-            w2g = self._w2g[name] if self._wt is None else self._w2g_t[name].t()
-            dact = torch.mm(dy[name], w2g, out=B[f"dact.{name}"])
+        dmlp = dy[name] if self._fold_g2 else gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
+        if self._gelu_fused(name, backward=True):
+            # dpre = (dmlp W2) * gelu'(pre) in one GEMM; W2 (W2g) as [F, C]
+            w2t = self._w2g_t[name] if self._fold_g2 else self._wt[name]["w2"]
+            dpre = gemm(dmlp, w2t, "dgelu", out=B[f"dact.{name}"], pre=pre)
         else:
-            dmlp = gated_residual(None, g2, dy[name], out=B[f"t1.{name}"])
-            dact = torch.mm(dmlp, self._dx_weight(name, "w2"), out=B[f"dact.{name}"])
-        if self.mlp == "swiglu":
-            dpre = B[f"dpre.{name}"]
-            swiglu_bwd(dact, pre[:, :M], pre[:, M:], dgate=dpre[:, :M], dup=dpre[:, M:])
-        else:
-            dpre = gelu_bwd(dact, pre, out=dact)
+            if self._fold_g2:  # (g2 * dy) W2 = dy W2g
+                w2g = self._w2g[name] if self._wt is None else self._w2g_t[name].t()
+                dact = torch.mm(dmlp, w2g, out=B[f"dact.{name}"])
+            else:
+                dact = torch.mm(dmlp, self._dx_weight(name, "w2"), out=B[f"dact.{name}"])
+            if self.mlp == "swiglu":
+                dpre = B[f"dpre.{name}"]
+                swiglu_bwd(dact, pre[:, :M], pre[:, M:], dgate=dpre[:, :M], dup=dpre[:, M:])
+            else:
+                dpre = gelu_bwd(dact, pre, out=dact)
         dh2 = torch.mm(dpre, self._dx_weight(name, "w1"), out=B[f"t2.{name}"])
         # dx1 and dout = g1 * dx1 (the out projection's gradient) in one pass
         dox = B[f"dox.{name}"] if self._fold_out else None

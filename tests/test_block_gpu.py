@@ -253,6 +253,34 @@ def test_block_step_matches_oracle(dtype, want_dx):
         assert min(agree) >= (0.97 if bf else 0.999), key
 
 
+def test_fused_gelu_block_matches_oracle():
+    """fused_gelu: W1 and W2's dX product as fa_gemm_bf16 with the GELU /
+    GELU-gradient epilogues.  Widths multiples of 256 (512 tokens, MLP 1024)
+    so that both streams take the fused path; against the oracle, and against
+    the same block with the library GEMM and separate GELU passes."""
+    case = oracle_mods(make_case(C=256, H=2, T=256, rows=16, cols=16, r=4, bf16=True, seed=9))
+    x = {k: dev(v, torch.bfloat16) for k, v in case["x"].items()}
+    dy = {k: dev(v, torch.bfloat16) for k, v in case["dy"].items()}
+    out = {}
+    for fused in (False, True):
+        blk = device_block(case, torch.bfloat16, fused_gelu=fused)
+        assert all(blk._gelu_fused(n, b) == fused for n in ("txt", "img") for b in (False, True))
+        y, grads = blk.forward_backward(x, dy, want_dx=True)
+        torch.cuda.synchronize()
+        out[fused] = _flat(y, grads)
+    wy, wgrads, _ = block_ref.block_step(case["x"], case["dy"], case["W"], case["H"], case["D"], case["cos"],
+                                         case["sin"], case["axes"], case["scale"], bf16=True, want_dx=True)
+    for name in ("txt", "img"):
+        check_gate(f"y.{name}", host(out[True][("y", name)]), wy[name], True)
+        check_gate(f"dx.{name}", host(out[True][((name, "x"), 0)]), wgrads[(name, "x")], True)
+    for key, g in wgrads.items():
+        if key[1] != "x":
+            check_gate(f"grad {key} dA", host(out[True][(key, 0)]), g[0], True)
+            check_gate(f"grad {key} dB", host(out[True][(key, 1)]), g[1], True)
+    for k, t in out[False].items():
+        check_gate(f"fused vs library {k}", host(out[True][k]), host(t), True)
+
+
 def test_refresh_adapters_after_changing_factors():
     """LoRA factors changed outside apply_adamw -- a new tensor assigned to
     lora_a[t] (as a LoRA-file loader would), an in-place copy into
