@@ -153,6 +153,22 @@ __device__ __forceinline__ void barrier_keep_dma() {
 }
 #undef FA_WAIT_VM
 
+// Wait until at most VM of this wave's vector-memory loads are outstanding
+// (no barrier: for LDS a wave fills and reads itself).
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(VM >= 0 && VM <= 8, "vmcnt literal");
+    if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr (VM == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+    else if constexpr (VM == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if constexpr (VM == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if constexpr (VM == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else if constexpr (VM == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else if constexpr (VM == 7) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+}
+
 // Replace elements 4*half .. 4*half+3 of an MFMA operand with two packed words.
 __device__ __forceinline__ void set_half(bf16x8 &v, int half, u32x2 w) {
     u32x4 u = as_u32x4(v);

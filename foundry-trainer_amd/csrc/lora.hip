@@ -99,64 +99,112 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(const float *__restric
 
 // ---- rowdot / expand, bf16 (MFMA) ---------------------------------------
 // rowdot: out[n][j] = s * sum_k X[n][k] W[j][k], R <= 16 * NT.  A workgroup
-// of 8 waves owns 16 rows; wave w takes k-steps (32 wide) w, w + 8, ..., U
-// at a time with all their loads issued before the MFMAs (U = 12: at K = 3072
-// a wave's whole range), and the 8 partial tiles are summed in LDS in a fixed
-// order (deterministic, no workspace).  Rows >= N
-// and j >= R load from a clamped (valid) row: output element (n, j) depends
-// on row n of X and row j of W only, and those outputs are not stored.
+// of 8 waves owns 16 rows; wave w takes k-steps (32 wide) w, w + 8, ..., and
+// the 8 partial tiles are summed in LDS in a fixed order (deterministic, no
+// workspace).
+//
+// Loads: the MFMA operand order (lane = row + 16 * chunk) spreads each quad of
+// lanes over 4 rows, and loads in that order ran at half the rate of the same
+// bytes read with each quad in one 64-byte row segment (X and A of 4096 x
+// 3072, r 16: 6.6 against 3.4 us).  So each wave stages its own k-steps in a
+// private LDS region by buffer_load ... lds in the row-segment order (lane =
+// 4 * row + chunk, X rows then W rows, 1 KiB per 16 rows) and reads them back
+// in operand order.  Within a 64-byte row the chunk is XORed with (row / 4) %
+// 4, so that both the DMA (a quad still covers one segment) and the operand
+// reads (16 rows at one chunk hit 16 distinct bank groups) are conflict-free.
+// G k-steps per stage, two stages per wave in flight; no barrier (the
+// regions are private).  Rows >= N and j >= R load from a clamped (valid) row:
+// output element (n, j) depends on row n of X and row j of W only, and those
+// outputs are not stored.  K % 32 == 16 leaves a half k-step whose upper 16
+// columns are zeroed in the operand.
+template <int NT>
+struct RowdotStage {
+    static constexpr int G = NT <= 3 ? 2 : 1;          // k-steps per stage
+    static constexpr int STEP = 1024 * (1 + NT);       // LDS bytes per k-step: X, then NT W tiles
+    static constexpr int WAVE = G * STEP;              // one wave's stage
+    static constexpr int BYTES = 8 * WAVE;             // the workgroup's stage
+};
+
 template <int NT, typename TO>
 __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restrict__ X, int64_t ldx,
                                                             const bf16 *__restrict__ W, TO *out, int64_t ldo,
                                                             int N, int K, int R, float s) {
+    using RS = RowdotStage<NT>;
+    constexpr int G = RS::G;
+    // two distinct LDS objects: the compiler then tells the DMA into one
+    // stage from the reads of the other
+    __shared__ __align__(16) char sa[RS::BYTES], sb[RS::BYTES];
     __shared__ float part[8][NT][4][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, q = lane >> 4;
     const int row0 = blockIdx.x * 16;
-    const bf16 *xp = X + (int64_t)min(row0 + m, N - 1) * ldx + q * 8;
-    const bf16 *wp[NT];
+
+    // DMA source offsets: lane 4 r + p fetches chunk p ^ ((r / 4) % 4) of row
+    // r of a 16-row, 32-column k-step (the k-step itself goes in soffset)
+    const int r = lane >> 2, c = (lane & 3) ^ ((r >> 2) & 3);
+    const int xrows = min(16, N - row0);
+    const __amdgpu_buffer_rsrc_t xrs =
+        make_rsrc(X + (int64_t)row0 * ldx, (uint32_t)(((int64_t)(xrows - 1) * ldx + K) * 2));
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint32_t)((int64_t)R * K * 2));
+    const uint32_t xvo = (uint32_t)((min(r, xrows - 1) * ldx + c * 8) * 2);
+    uint32_t wvo[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) wp[t] = W + (int64_t)min(t * 16 + m, R - 1) * K + q * 8;
+    for (int t = 0; t < NT; ++t) wvo[t] = (uint32_t)((min(t * 16 + r, R - 1) * (int64_t)K + c * 8) * 2);
+    // operand reads: lane (m, q) takes chunk q of row m
+    const int rd = m * 64 + ((q ^ ((m >> 2) & 3)) << 4);
+
+    const int nks = (K + 31) / 32;                               // k-steps, the last maybe half
+    const int J = nks > wave ? (nks - wave + 7) / 8 : 0;         // this wave's k-steps
+    const bool half = K % 32 != 0;
+    // stage of k-steps j0 .. j0+G-1 of this wave into dst; past J it loads a
+    // clamped (valid) k-step that is never read, so every stage issues the
+    // same G (1 + NT) loads and the waits can count them
+    auto issue = [&](int j0, char *dst) {
+        char *d = dst + wave * RS::WAVE;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int ks = wave + 8 * min(j0 + g, J - 1);
+            buffer_to_lds_16(xrs, d + g * RS::STEP, xvo, (uint32_t)ks * 64);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) buffer_to_lds_16(wrs, d + g * RS::STEP + 1024 * (1 + t), wvo[t], (uint32_t)ks * 64);
+        }
+    };
     const u32x4 zero = {0, 0, 0, 0};
     f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    constexpr int U = NT <= 3 ? 12 : 6;  // VGPRs: 4 U (1 + NT) for the loads
-    const int nfull = K / 32;
-    const int J = nfull > wave ? (nfull - wave + 7) / 8 : 0;  // this wave's k-steps
-    // k-steps j0 .. j0+U-1 of the wave (only those below J unless FULL)
-    auto group = [&](int j0, auto full) {
-        constexpr bool FULL = decltype(full)::value;
-        u32x4 a[U], w[U][NT];
+    auto consume = [&](int j0, const char *src) {
+        const char *d = src + wave * RS::WAVE;
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (FULL || j0 + u < J) {
-                const int off = (wave + 8 * (j0 + u)) * 32;
-                a[u] = ld_global_16(xp + off);
+        for (int g = 0; g < G; ++g)
+            if (j0 + g < J) {
+                u32x4 a = ld_lds_16(d + g * RS::STEP, rd);
+                if (half && wave + 8 * (j0 + g) == nks - 1 && q >= 2) a = zero;  // columns past K
 #pragma unroll
-                for (int t = 0; t < NT; ++t) w[u][t] = ld_global_16(wp[t] + off);
+                for (int t = 0; t < NT; ++t)
+                    acc[t] = mfma_16x16x32(as_bf16x8(a), as_bf16x8(ld_lds_16(d + g * RS::STEP + 1024 * (1 + t), rd)),
+                                           acc[t]);
             }
-        // every load of the group goes out before the first MFMA waits (left
-        // to the scheduler, about 10 were in flight and the rest trickled out
-        // between the MFMAs, one latency per few loads)
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (FULL || j0 + u < J)
-#pragma unroll
-                for (int t = 0; t < NT; ++t) acc[t] = mfma_16x16x32(as_bf16x8(a[u]), as_bf16x8(w[u][t]), acc[t]);
     };
-    int j0 = 0;
-    for (; j0 + U <= J; j0 += U) group(j0, std::true_type{});
-    if (j0 < J) group(j0, std::false_type{});
-    if (K % 32 && wave == (nfull & 7)) {
-        // K % 32 == 16: lanes q < 2 hold the last 16 columns, q >= 2 are past K
-        const bool kin = q < 2;
-        const u32x4 a = kin ? ld_global_16(xp + nfull * 32) : zero;
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-            acc[t] = mfma_16x16x32(as_bf16x8(a), as_bf16x8(kin ? ld_global_16(wp[t] + nfull * 32) : zero), acc[t]);
+    if (J > 0) {
+        constexpr int VM = G * (1 + NT);  // loads per stage
+        issue(0, sa);
+        issue(G, sb);
+        // No exit between the halves: with one, the compiler's wait-count
+        // analysis sees a path from a refill of sa straight to the reads of
+        // sa and drains every load there.  A half past J reads nothing.
+        for (int j0 = 0; j0 < J; j0 += 2 * G) {
+            wait_vmcnt<VM>();  // stage j0 landed, the next one may stay in flight
+            consume(j0, sa);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the DMA refills sa
+            issue(j0 + 2 * G, sa);
+            wait_vmcnt<VM>();
+            consume(j0 + G, sb);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(j0 + 3 * G, sb);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stages issued past J land before LDS is reused
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t)
