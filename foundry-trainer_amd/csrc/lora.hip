@@ -369,18 +369,30 @@ __global__ __launch_bounds__(256) void lora_colsum_kernel(const float *__restric
 }
 
 // ---- colsum, bf16 (MFMA) ------------------------------------------------
-// U^T in the MFMA operand order: ut[j][n'] for j < 32, n' < npad (multiple of
-// 64), bf16.  Within each 16-token group the tokens are stored as
-// {0..3, 8..11, 4..7, 12..15}: lane half g of the B operand then reads its 8
-// values {4g..4g+3, 8+4g..8+4g+3} — the k order of the transpose-read A
-// operand — as one 16-byte chunk.  Rows j >= R and tokens >= N are zero.
+// U^T as MFMA B operands, fragment-major: for 32-row block h (j / 32),
+// 16-token step k and lane L = j % 32 + 32 g, the lane's 8 values are the 16
+// bytes at ((h * npad / 16 + k) * 64 + L) * 8, so a wave's operand load for
+// one step is 1 KiB in lane order (loads whose quads of lanes span 4 rows
+// ran at about half the rate).  Lane half g holds positions 16 k + 8 g ..
+// +7, and within each 16-token group the tokens are stored as {0..3, 8..11,
+// 4..7, 12..15}: lane half g then holds tokens {4g..4g+3, 8+4g..8+4g+3} —
+// the k order of the transpose-read A operand.  Rows j >= R and tokens >= N
+// are zero.  One thread per element, in storage order.
+__device__ __forceinline__ void ut_frag_coords(int64_t e, int npad, int &j, int &n) {
+    const int e8 = (int)(e & 7), L = (int)((e >> 3) & 63);
+    const int64_t rest = e >> 9;
+    const int nk = npad >> 4, h = (int)(rest / nk), k = (int)(rest % nk);
+    j = h * 32 + (L & 31);
+    const int p = k * 16 + (L >> 5) * 8 + e8;  // position within the padded token axis
+    const int q = p & 15;
+    n = (p >> 4) * 16 + ((q & 4) ? 8 : 0) + ((q & 8) ? 4 : 0) + (q & 3);
+}
 template <typename TU>
 __global__ void lora_ut_kernel(const TU *__restrict__ U, int64_t ldu, bf16 *ut, int N, int R, int npad) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= (int64_t)32 * npad) return;
-    const int j = (int)(e / npad), p = (int)(e % npad);
-    const int grp = p >> 4, q = p & 15;
-    const int n = grp * 16 + ((q & 4) ? 8 : 0) + ((q & 8) ? 4 : 0) + (q & 3);
+    int j, n;
+    ut_frag_coords(e, npad, j, n);
     ut[e] = j < R && n < N ? (bf16)U[(int64_t)n * ldu + j] : (bf16)0.f;
 }
 
@@ -397,7 +409,7 @@ __global__ __launch_bounds__(256) void lora_colsum_mfma_kernel(const bf16 *__res
     __shared__ __align__(16) char st0[T::BYTES], st1[T::BYTES];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = lane & 31, g = lane >> 5;
+    const int n = lane & 31;
     const int c0 = blockIdx.x * kCsCols;
     const int t_begin = blockIdx.y * chunk, t_end = min(t_begin + chunk, npad);
     // rows >= N (and, in the last row, columns >= C) read as zero
@@ -413,7 +425,7 @@ __global__ __launch_bounds__(256) void lora_colsum_mfma_kernel(const bf16 *__res
     uint32_t coff[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) coff[dt] = col_frag_off<128>(0, 0, dt, lane);
-    const bf16 *ub = ut + (int64_t)n * npad + g * 8;
+    const bf16 *ub = ut + lane * 8;  // fragment-major: 512 values per 16-token step
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -422,7 +434,7 @@ __global__ __launch_bounds__(256) void lora_colsum_mfma_kernel(const bf16 *__res
     constexpr int KS = kCsRows / 16;
     auto loadu = [&](int t0, bf16x8 (&b)[KS]) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) b[ks] = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
+        for (int ks = 0; ks < KS; ++ks) b[ks] = as_bf16x8(ld_global_16(ub + ((t0 >> 4) + ks) * 512));
     };
     auto stage = [&](const char *tile, const bf16x8 (&b)[KS]) {
 #pragma unroll
@@ -512,9 +524,8 @@ __global__ void lora_ut_many_kernel(GradMany g) {
     const GradProblem &q = g.p[blockIdx.y];
     const int e = blockIdx.x * 256 + threadIdx.x;
     if (e >= q.rw * g.npad) return;
-    const int j = e / g.npad, p = e - j * g.npad;
-    const int grp = p >> 4, r = p & 15;
-    const int n = grp * 16 + ((r & 4) ? 8 : 0) + ((r & 8) ? 4 : 0) + (r & 3);
+    int j, n;
+    ut_frag_coords(e, g.npad, j, n);
     q.ut[e] = j < q.R && n < g.N ? q.u[(int64_t)n * q.ldu + j] : (bf16)0.f;
 }
 
@@ -528,7 +539,7 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     __shared__ __align__(16) char st0[T::BYTES], st1[T::BYTES];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = lane & 31, gh = lane >> 5;
+    const int n = lane & 31;
     const int C = q.C, N = g.N, npad = g.npad;
     const int64_t ldx = q.ldx;
     const int c0 = ((int)blockIdx.x - q.tile0) * kCsCols;
@@ -547,8 +558,8 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     uint32_t coff[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) coff[dt] = col_frag_off<128>(0, 0, dt, lane);
-    const bf16 *ub = q.ut + (int64_t)n * npad + gh * 8;
-    const bf16 *ub2 = ub + (int64_t)32 * npad;
+    const bf16 *ub = q.ut + lane * 8;            // fragment-major: 512 values per 16-token step
+    const bf16 *ub2 = ub + (int64_t)32 * npad;   // rows 32..63
     f32x16 acc, acc2;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -562,8 +573,8 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     auto loadu = [&](int t0, bf16x8 (&b)[2 * KS]) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            b[ks] = as_bf16x8(ld_global_16(ub + t0 + ks * 16));
-            if (two) b[KS + ks] = as_bf16x8(ld_global_16(ub2 + t0 + ks * 16));
+            b[ks] = as_bf16x8(ld_global_16(ub + ((t0 >> 4) + ks) * 512));
+            if (two) b[KS + ks] = as_bf16x8(ld_global_16(ub2 + ((t0 >> 4) + ks) * 512));
         }
     };
     auto stage = [&](const char *tile, const bf16x8 (&b)[2 * KS]) {
