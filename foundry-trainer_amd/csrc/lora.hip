@@ -112,14 +112,17 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(const float *__restric
 // in operand order.  Within a 64-byte row the chunk is XORed with (row / 4) %
 // 4, so that both the DMA (a quad still covers one segment) and the operand
 // reads (16 rows at one chunk hit 16 distinct bank groups) are conflict-free.
-// G k-steps per stage, two stages per wave in flight; no barrier (the
-// regions are private).  Rows >= N and j >= R load from a clamped (valid) row:
+// G k-steps per stage, two stages per wave in flight; no barrier inside the
+// loop (the regions are private).  Rows >= N and j >= R load from a clamped (valid) row:
 // output element (n, j) depends on row n of X and row j of W only, and those
 // outputs are not stored.  K % 32 == 16 leaves a half k-step whose upper 16
 // columns are zeroed in the operand.
+// One k-step per stage: two k-steps per stage (twice the LDS) was no faster
+// alone and slower in the c4 step, where a workgroup's LDS decides whether it
+// can share a CU with the other stream's kernels.
 template <int NT>
 struct RowdotStage {
-    static constexpr int G = NT <= 3 ? 2 : 1;          // k-steps per stage
+    static constexpr int G = 1;                        // k-steps per stage
     static constexpr int STEP = 1024 * (1 + NT);       // LDS bytes per k-step: X, then NT W tiles
     static constexpr int WAVE = G * STEP;              // one wave's stage
     static constexpr int BYTES = 8 * WAVE;             // the workgroup's stage
@@ -134,7 +137,9 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
     // two distinct LDS objects: the compiler then tells the DMA into one
     // stage from the reads of the other
     __shared__ __align__(16) char sa[RS::BYTES], sb[RS::BYTES];
-    __shared__ float part[8][NT][4][64];
+    // the 8 partial tiles reuse sa once the k-steps are done
+    static_assert(sizeof(float) * 8 * NT * 4 * 64 <= RS::BYTES, "partials fit in a stage");
+    float (*part)[NT][4][64] = reinterpret_cast<float (*)[NT][4][64]>(sa);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, q = lane >> 4;
@@ -206,6 +211,7 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stages issued past J land before LDS is reused
     }
+    __syncthreads();  // every wave is done with sa
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
