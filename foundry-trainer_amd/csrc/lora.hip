@@ -535,18 +535,32 @@ __global__ void lora_ut_many_kernel(GradMany g) {
     q.ut[e] = j < q.R && n < g.N ? q.u[(int64_t)n * q.ldu + j] : (bf16)0.f;
 }
 
+// One workgroup: column tile, token split of product q.  DIRECT (every
+// product's U 16-byte aligned with 16-byte rows): U's rows for a stage (64
+// tokens x 64 columns) come into LDS by DMA beside the X tile, and the B operand is a column
+// fragment of that tile -- the same transpose read, hence the same token
+// order, as X's A operand; columns j >= R hold whatever follows U's rows and
+// only reach outputs j >= R, which are not stored.  Otherwise the B operand
+// is read from the staged fragment-major U^T.  The values multiplied are the
+// same either way, so are the bits.
+// The LDS arrays are the kernel's own (not pointer arguments of a helper):
+// the compiler then tells the DMA into one stage from the reads of the other.
+template <bool DIRECT>
 __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     int k = 0;
     while (k + 1 < g.count && g.p[k + 1].tile0 <= (int)blockIdx.x) ++k;
     const GradProblem &q = g.p[k];
     if ((int)blockIdx.y >= q.splits) return;  // uniform over the workgroup
     using T = LdsTile<128, kCsRows>;
-    constexpr int WI = T::WAVE_INSTS / 4;
+    using UT = LdsTile<64, kCsRows>;
+    constexpr int WI = T::WAVE_INSTS / 4, UWI = UT::WAVE_INSTS / 4;
     __shared__ __align__(16) char st0[T::BYTES], st1[T::BYTES];
+    __shared__ __align__(16) char uu0[DIRECT ? UT::BYTES : 16], uu1[DIRECT ? UT::BYTES : 16];
+    const int N = g.N, npad = g.npad;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 31;
-    const int C = q.C, N = g.N, npad = g.npad;
+    const int C = q.C;
     const int64_t ldx = q.ldx;
     const int c0 = ((int)blockIdx.x - q.tile0) * kCsCols;
     const int t_begin = blockIdx.y * q.chunk, t_end = min(t_begin + q.chunk, npad);
@@ -556,14 +570,32 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     const uint32_t xvo = tile_src_off<128>(wave, lane, ldx);
     const uint32_t row_step = tile_inst_row_step<128>(ldx);
     const uint32_t stage_step = (uint32_t)(kCsRows * ldx * 2);
-    auto issue = [&](int t0, char *dst) {
+    // U rows >= N read as zero.  The range ends at a whole dword: the
+    // buffer range check zeroes a dword that crosses it, which for odd R
+    // would drop the last row's column R - 1 (column R, the dword's other
+    // half, lies in the row's 16-byte stride).
+    const __amdgpu_buffer_rsrc_t urs =
+        make_rsrc(q.u, (uint32_t)((int64_t)(N - 1) * q.ldu * 2 + ((q.R * 2 + 3) & ~3)));
+    const uint32_t uvo = DIRECT ? tile_src_off<64>(wave, lane, q.ldu) : 0u;
+    const uint32_t urow_step = tile_inst_row_step<64>(q.ldu);
+    const uint32_t ustage_step = (uint32_t)(kCsRows * q.ldu * 2);
+    auto issue = [&](int t0, char *dst, char *udst) {
 #pragma unroll
         for (int i = 0; i < WI; ++i)
             buffer_to_lds_16(xrs, dst + (i * 4 + wave) * 1024, xvo, (uint32_t)(t0 / kCsRows) * stage_step + i * row_step);
+        if constexpr (DIRECT) {
+#pragma unroll
+            for (int i = 0; i < UWI; ++i)
+                buffer_to_lds_16(urs, udst + (i * 4 + wave) * 1024, uvo,
+                                 (uint32_t)(t0 / kCsRows) * ustage_step + i * urow_step);
+        }
     };
     uint32_t coff[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) coff[dt] = col_frag_off<128>(0, 0, dt, lane);
+    uint32_t cu[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) cu[f] = col_frag_off<64>(0, 0, f, lane);
     const bf16 *ub = q.ut + lane * 8;            // fragment-major: 512 values per 16-token step
     const bf16 *ub2 = ub + (int64_t)32 * npad;   // rows 32..63
     f32x16 acc, acc2;
@@ -572,38 +604,69 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
         acc[r] = 0.f;
         acc2[r] = 0.f;
     }
-    // A stage's U^T fragments are loaded before the next stage's DMA is
-    // issued: memory operations complete in issue order, so waiting for them
-    // then leaves that DMA in flight during this stage's MFMAs.
+    // Staged: a stage's U^T fragments are loaded before the next stage's DMA
+    // is issued: memory operations complete in issue order, so waiting for
+    // them then leaves that DMA in flight during this stage's MFMAs.
     constexpr int KS = kCsRows / 16;
     auto loadu = [&](int t0, bf16x8 (&b)[2 * KS]) {
+        if constexpr (!DIRECT) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            b[ks] = as_bf16x8(ld_global_16(ub + ((t0 >> 4) + ks) * 512));
-            if (two) b[KS + ks] = as_bf16x8(ld_global_16(ub2 + ((t0 >> 4) + ks) * 512));
+            for (int ks = 0; ks < KS; ++ks) {
+                b[ks] = as_bf16x8(ld_global_16(ub + ((t0 >> 4) + ks) * 512));
+                if (two) b[KS + ks] = as_bf16x8(ld_global_16(ub2 + ((t0 >> 4) + ks) * 512));
+            }
         }
     };
-    auto stage = [&](const char *tile, const bf16x8 (&b)[2 * KS]) {
+    auto stage = [&](const char *tile, const char *utile, const bf16x8 (&b)[2 * KS]) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
                                                col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
-            acc = mfma_32x32x16(a, b[ks], acc);
-            if (two) acc2 = mfma_32x32x16(a, b[KS + ks], acc2);
+            bf16x8 b0;
+            if constexpr (DIRECT)
+                b0 = lds_read_col_frag(utile, cu[0] + ks * 16 * UT::ROWB, col_frag_hi8<64>(cu, 0) + ks * 16 * UT::ROWB);
+            else
+                b0 = b[ks];
+            acc = mfma_32x32x16(a, b0, acc);
+            if (two) {
+                bf16x8 b1;
+                if constexpr (DIRECT)
+                    b1 = lds_read_col_frag(utile, cu[1] + ks * 16 * UT::ROWB,
+                                           col_frag_hi8<64>(cu, 1) + ks * 16 * UT::ROWB);
+                else
+                    b1 = b[KS + ks];
+                acc2 = mfma_32x32x16(a, b1, acc2);
+            }
         }
     };
     bf16x8 bu[2 * KS];
-    issue(t_begin, st0);
-    for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
-        barrier_keep_dma<0>();
-        loadu(t0, bu);
-        if (t0 + kCsRows < t_end) issue(t0 + kCsRows, st1);
-        stage(st0, bu);
-        if (t0 + kCsRows < t_end) {
+    issue(t_begin, st0, uu0);
+    if constexpr (DIRECT) {
+        // Each stage's refill goes out unconditionally (past the split's
+        // range it reads rows of the next split or zeros, never used): a
+        // conditional issue made the compiler wait for the refill of one
+        // stage before reading the other.  Only the second stage's reads
+        // are conditional.
+        for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
             barrier_keep_dma<0>();
-            loadu(t0 + kCsRows, bu);
-            if (t0 + 2 * kCsRows < t_end) issue(t0 + 2 * kCsRows, st0);
-            stage(st1, bu);
+            issue(t0 + kCsRows, st1, uu1);
+            stage(st0, uu0, bu);
+            barrier_keep_dma<0>();
+            issue(t0 + 2 * kCsRows, st0, uu0);
+            if (t0 + kCsRows < t_end) stage(st1, uu1, bu);
+        }
+    } else {
+        for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
+            barrier_keep_dma<0>();
+            loadu(t0, bu);
+            if (t0 + kCsRows < t_end) issue(t0 + kCsRows, st1, uu1);
+            stage(st0, uu0, bu);
+            if (t0 + kCsRows < t_end) {
+                barrier_keep_dma<0>();
+                loadu(t0 + kCsRows, bu);
+                if (t0 + 2 * kCsRows < t_end) issue(t0 + 2 * kCsRows, st0, uu0);
+                stage(st1, uu1, bu);
+            }
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -855,11 +918,13 @@ hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int 
         g.npad = npad;
         char *ws = static_cast<char *>(work);
         int tiles = 0, max_splits = 1, max_out = 1;
+        bool staged = false;
         for (int k = 0; k < g.count; ++k) {
             const LoraGradItem &it = items[k0 + k];
             GradProblem &q = g.p[k];
             q.u = static_cast<const bf16 *>(it.u);
             q.ldu = it.ldu;
+            staged = staged || reinterpret_cast<uintptr_t>(it.u) % 16 != 0 || (it.ldu * 2) % 16 != 0;
             q.x = static_cast<const bf16 *>(it.x);
             q.ldx = it.ldx;
             q.out = it.grad;
@@ -881,10 +946,15 @@ hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int 
             max_splits = q.splits > max_splits ? q.splits : max_splits;
             max_out = it.C * q.rw > max_out ? it.C * q.rw : max_out;
         }
-        hipLaunchKernelGGL(lora_ut_many_kernel, dim3((unsigned)((64 * npad + 255) / 256), (unsigned)g.count),
-                           dim3(256), 0, st, g);
-        hipLaunchKernelGGL(lora_colsum_many_kernel, dim3((unsigned)tiles, (unsigned)max_splits), dim3(256), 0, st,
-                           g);
+        if (staged)
+            hipLaunchKernelGGL(lora_ut_many_kernel, dim3((unsigned)((64 * npad + 255) / 256), (unsigned)g.count),
+                               dim3(256), 0, st, g);
+        if (staged)
+            hipLaunchKernelGGL(lora_colsum_many_kernel<false>, dim3((unsigned)tiles, (unsigned)max_splits), dim3(256), 0,
+                               st, g);
+        else
+            hipLaunchKernelGGL(lora_colsum_many_kernel<true>, dim3((unsigned)tiles, (unsigned)max_splits), dim3(256), 0,
+                               st, g);
         hipLaunchKernelGGL(lora_colsum_reduce_many_kernel, dim3((unsigned)((max_out + 255) / 256), (unsigned)g.count),
                            dim3(256), 0, st, g);
         const hipError_t e = hipGetLastError();

@@ -270,7 +270,8 @@ def test_lora_grad_many_matches_separate_calls():
     """fa_lora_grad_many: ten products of one token count (ranks 4..64, so
     one- and two-accumulator products, dA and dB layouts, strided u and x
     views, two sets of launches) give the bits of separate fa_lora_grad
-    calls, and one of them matches an f64 product of the same values."""
+    calls, with U staged or read directly, and one of them matches an f64
+    product of the same values."""
     from foundry_attn.ops import lora_grad, lora_grad_many
     rng = np.random.default_rng(321)
     N, bf = 300, torch.bfloat16
@@ -286,9 +287,21 @@ def test_lora_grad_many_matches_separate_calls():
         items.append((ue[:, 3:3 + r], xe[:, :C], 0.5 + 0.25 * k, tr))
     many = lora_grad_many(items)
     one = [lora_grad(*it) for it in items]
+    # The views above start 6 bytes into their rows, so the colsum reads a
+    # staged U^T.  The same values in 16-byte aligned rows (every product
+    # aligned) take the direct path, U read by DMA inside the colsum kernel
+    # with no staging launch: the same bits.
+    aligned = []
+    for u, x, sc, tr in items:
+        buf = torch.zeros(N, 72, dtype=bf, device="cuda")
+        buf[:, :u.shape[1]] = u
+        aligned.append((buf[:, :u.shape[1]], x, sc, tr))
+    direct = lora_grad_many(aligned)
     torch.cuda.synchronize()
     for k, (a, b) in enumerate(zip(many, one)):
         assert a.shape == b.shape and torch.equal(a, b), k
+    for k, (a, b) in enumerate(zip(direct, many)):
+        assert torch.equal(a, b), k
     u, x, sc, tr = items[3]
     want = sc * host(x).astype(np.float64).T @ host(u).astype(np.float64)  # [C, r]
     np.testing.assert_allclose(host(many[3]), want, rtol=1e-4, atol=1e-3)
