@@ -200,7 +200,8 @@ def memory_bound_bench(torch, fa, cfg):
     the joint buffer; backward reads x and dy, writes dx; both read the
     per-token cos/sin rows and the weights), and the LoRA down / up pieces at
     the c4 img stream's shape (x [4096, 3072], r = 16: down reads x and A,
-    writes u; up reads u and B and updates y in place)."""
+    writes u; up reads u and B and updates y in place), and the stream's
+    q/k/v adapter gradients as the block forms them (one grouped call)."""
     from foundry_attn.configs import C4
     g = torch.Generator(device="cuda").manual_seed(7)
     bf = torch.bfloat16
@@ -220,11 +221,21 @@ def memory_bound_bench(torch, fa, cfg):
     lb = (1e-3 * torch.randn((C, r), device="cuda", generator=g)).to(bf)
     lu = torch.empty((N, r), device="cuda", dtype=bf)
     ly = torch.randn((N, C), device="cuda", generator=g).to(bf)
+    # the c4 stream's q/k/v adapter gradients in one fa_lora_grad_many call:
+    # dA_qkv [3r, C] = t^T h and dB_j [C, r] = dy_j^T su_j (j = q, k, v)
+    gh = torch.randn((N, C), device="cuda", generator=g).to(bf)
+    gdy = [torch.randn((N, C), device="cuda", generator=g).to(bf) for _ in range(3)]
+    gt = torch.randn((N, 3 * r), device="cuda", generator=g).to(bf)
+    gsu = [torch.randn((N, r), device="cuda", generator=g).to(bf) for _ in range(3)]
+    gout = [torch.empty((3 * r, C), device="cuda")] + [torch.empty((C, r), device="cuda") for _ in range(3)]
+    gitems = [(gt, gh, 1.0, False, gout[0])] + [(gsu[j], gdy[j], 1.0, True, gout[1 + j]) for j in range(3)]
+    gbytes = 4 * N * C * 2 + N * 6 * r * 2 + 6 * r * C * 4
     cases = {
         "qk_prologue_fwd": (lambda: fa.qk_prologue_multi(fwd_segs), 4 * row + tables),
         "qk_prologue_bwd": (lambda: fa.qk_prologue_bwd_multi(bwd_segs), 6 * row + tables),
         "lora_down": (lambda: fa.lora_down(lx, la, 1.0, out=lu), N * C * 2 + r * C * 2 + N * r * 2),
         "lora_up": (lambda: fa.lora_up(lu, lb, ly, 1.0), 2 * N * C * 2 + N * r * 2 + C * r * 2),
+        "lora_grad_qkv": (lambda: fa.lora_grad_many(gitems), gbytes),
     }
     out = {}
     for name, (fn, nbytes) in cases.items():
@@ -234,7 +245,8 @@ def memory_bound_bench(torch, fa, cfg):
         out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(gbs, 1),
                      "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2), "eager_ms": round(eager, 4)}
     out["shapes"] = (f"prologue: Q and K in one launch, each B={B} S={S} H={H} D={D} bf16; "
-                     f"lora: N={N} C={C} r={r} bf16")
+                     f"lora: N={N} C={C} r={r} bf16; lora_grad_qkv: dA [{3 * r}, {C}] and three dB [{C}, {r}] "
+                     f"in one call (reads h and three dy, f32 grads)")
     out["timing"] = ("ms: HIP events over 5 replays of a HIP graph of 20 calls (kernel time); "
                      "eager_ms: HIP events over 20 eager calls, which includes the host's per-call time")
     return out
