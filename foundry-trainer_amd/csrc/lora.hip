@@ -5,17 +5,22 @@
 // produce its gradients.
 //
 //   rowdot  out[n][j] = s * sum_k X[n][k] W[j][k]      (x A^T, and dy B as
-//           dy (B^T)^T): skinny GEMM on v_mfma_f32_32x32x16_bf16, one wave
-//           per 32 rows, operands straight from global memory (16-byte loads,
-//           both run along k).  HBM-bound: one read of X.
+//           dy (B^T)^T): a skinny GEMM.  bf16 (lora_rowdot16_kernel): 16 rows
+//           per 8-wave workgroup on v_mfma_f32_16x16x32_bf16, each wave's
+//           k-steps of X and W staged in its own LDS region by DMA in
+//           row-segment lane order and read back in operand order.  f32 (the
+//           parity path): one wave per 32 rows, operands from global memory.
+//           HBM-bound: one read of X.
 //   expand  Y[n][c] += s * sum_j U[n][j] Wt[c][j]       (y += s u B^T, and
 //           dx += du A): one thread per output column and row phase, Wt rows
 //           staged in LDS.  HBM-bound: one read and one write of Y.
 //   colsum  out[j][c] = s * sum_n U[n][j] X[n][c]      (dB^T = s u^T dy and
 //           dA = du^T x).  bf16: a skinny MFMA GEMM, X^T (by transpose reads
-//           of 64-token x 128-column tiles streamed into LDS) times U^T (bf16,
-//           tokens contiguous), split over tokens; the splits are summed in a
-//           fixed order by a second kernel — deterministic, no atomics.  f32
+//           of 64-token x 128-column tiles streamed into LDS) times U^T (read
+//           the same way from U's rows streamed beside them, or from a staged
+//           fragment-major copy when U is not 16-byte aligned), split over
+//           tokens; the splits are summed in a fixed order by a second kernel
+//           — deterministic, no atomics.  f32
 //           (the parity path): each workgroup owns 64 columns and sweeps all
 //           rows in a fixed order.
 #include "fa_device.hpp"
