@@ -222,6 +222,33 @@ def test_lora_bf16_ranks_ragged(r):
     assert rel_l2(host(dx), want_dx) <= 1e-2
 
 
+@pytest.mark.parametrize("K", [16, 208, 3088])
+@pytest.mark.parametrize("r", [16, 33, 48, 64])
+def test_lora_down_k_tails(K, r):
+    """fa_lora_down where K is not a multiple of 32 (the last 32-wide k-step
+    is half, its upper 16 columns zeroed in the operand), where some waves of
+    a workgroup have no k-step (K = 16, 208), and where a wave's k-steps run
+    over several LDS stages with a remainder (K = 3088); ranks over 1 to 4
+    16-column tiles, and a token count that is not a multiple of 16.  Against
+    the f64 product of the same bf16 values, rounded to bf16 as the kernel
+    writes it."""
+    from foundry_attn.ops import lora_down
+    rng = np.random.default_rng(300 + K + r)
+    N, s = 333, 0.5
+    rnd = oracle.bf16_round
+    x = rnd(rng.standard_normal((N, K)).astype(np.float32))
+    A = rnd(rng.standard_normal((r, K)).astype(np.float32) / np.sqrt(K))
+    bf = torch.bfloat16
+    # x with columns past K holding large values: a wrongly read column shows
+    xe = torch.full((N, K + 48), 1e4, dtype=bf, device="cuda")
+    xe[:, :K] = dev(x, bf)
+    u = lora_down(xe[:, :K], dev(A, bf), s, out=torch.empty((N, r), dtype=bf, device="cuda"))
+    want = (s * (x.astype(np.float64) @ A.T.astype(np.float64))).astype(np.float32)
+    got = host(u)
+    peak = np.abs(want).max()
+    assert max_abs(got, want) <= 2 ** -7 * peak + 1e-6 and rel_l2(got, want) <= 4e-3, (K, r)
+
+
 @pytest.mark.parametrize("r", [4, 16, 32, 40, 48, 64])
 def test_lora_pieces_strided_views(r):
     """fa_lora_down / fa_lora_up / fa_lora_grad on the rank-column views a
