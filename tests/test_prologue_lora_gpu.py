@@ -294,11 +294,11 @@ def test_lora_pieces_strided_views(r):
 
 
 def test_lora_grad_many_matches_separate_calls():
-    """fa_lora_grad_many: ten products of one token count (ranks 4..64, so
+    """fa_lora_grad_many: eleven products of one token count (ranks 4..64, so
     one- and two-accumulator products, dA and dB layouts, strided u and x
-    views, two sets of launches) give the bits of separate fa_lora_grad
-    calls, with U staged or read directly, and one of them matches an f64
-    product of the same values."""
+    views, a partial last column tile, two sets of launches) give the bits of
+    separate fa_lora_grad calls, with U staged or read directly, and two of
+    them match f64 products of the same values."""
     from foundry_attn.ops import lora_grad, lora_grad_many
     rng = np.random.default_rng(321)
     N, bf = 300, torch.bfloat16
@@ -306,7 +306,7 @@ def test_lora_grad_many_matches_separate_calls():
     items = []
     for k, (r, C, tr) in enumerate([(4, 256, False), (16, 384, True), (40, 128, False), (48, 3072, True),
                                      (64, 256, False), (12, 512, True), (33, 256, True), (16, 3072, False),
-                                     (8, 128, False), (64, 384, True)]):
+                                     (8, 128, False), (64, 384, True), (20, 208, True)]):
         ue = torch.zeros(N, r + 8, dtype=bf, device="cuda")
         ue[:, 3:3 + r] = dev(rnd(rng.standard_normal((N, r)).astype(np.float32)), bf)
         xe = torch.zeros(N, C + 16, dtype=bf, device="cuda")
@@ -329,9 +329,11 @@ def test_lora_grad_many_matches_separate_calls():
         assert a.shape == b.shape and torch.equal(a, b), k
     for k, (a, b) in enumerate(zip(direct, many)):
         assert torch.equal(a, b), k
-    u, x, sc, tr = items[3]
-    want = sc * host(x).astype(np.float64).T @ host(u).astype(np.float64)  # [C, r]
-    np.testing.assert_allclose(host(many[3]), want, rtol=1e-4, atol=1e-3)
+    for k in (3, 10):  # C = 3072, and C = 208 (a partial last column tile)
+        u, x, sc, tr = items[k]
+        want = sc * host(x).astype(np.float64).T @ host(u).astype(np.float64)  # [C, r]
+        np.testing.assert_allclose(host(many[k]), want, rtol=1e-4, atol=1e-3)
+        np.testing.assert_allclose(host(direct[k]), want, rtol=1e-4, atol=1e-3)
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
