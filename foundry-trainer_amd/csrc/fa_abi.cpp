@@ -775,6 +775,7 @@ static fa::LoraGradItem grad_item(const fa_lora_grad_args *a) {
     it.ldu = a->ldu;
     it.x = a->x;
     it.ldx = a->ldx;
+    it.N = a->tokens;
     it.C = a->features;
     it.R = a->rank;
     it.scale = a->scale;
@@ -790,24 +791,28 @@ static fa_status check_lora_grad(const fa_lora_grad_args *a) {
     if (!a->x || !aligned(a->x, 16) || a->ldx < a->features || (a->ldx * 2) % 16)
         return fail(FA_ERR_INVALID_ARG, "x is NULL, misaligned, or ldx < features");
     if (!a->grad || !aligned(a->grad, 4)) return fail(FA_ERR_INVALID_ARG, "grad is NULL or misaligned");
+    // the kernel reads u and x through buffer descriptors with 32-bit ranges
+    const int64_t xspan = ((int64_t)(a->tokens - 1) * a->ldx + a->features) * 2;
+    const int64_t uspan = ((int64_t)(a->tokens - 1) * a->ldu + a->rank) * 2 + 2;
+    if (xspan >= (int64_t(1) << 32) || uspan >= (int64_t(1) << 32))
+        return fail(FA_ERR_UNSUPPORTED, "u or x spans 4 GiB or more; this build addresses less per operand");
     return FA_OK;
 }
 
 size_t fa_lora_grad_workspace_size(const fa_lora_grad_args *a) {
     if (!a || a->tokens < 1 || a->features < 1 || a->rank < 1 || a->rank > 64) return 0;
     const fa::LoraGradItem it = grad_item(a);
-    return fa::lora_grad_many_workspace_bytes(&it, 1, a->tokens);
+    return fa::lora_grad_many_workspace_bytes(&it, 1);
 }
 
 fa_status fa_lora_grad(const fa_lora_grad_args *a, void *stream) {
     FA_TRY(check_lora_grad(a));
     const fa::LoraGradItem it = grad_item(a);
-    const size_t need = fa::lora_grad_many_workspace_bytes(&it, 1, a->tokens);
+    const size_t need = fa::lora_grad_many_workspace_bytes(&it, 1);
     if (!a->workspace || !aligned(a->workspace, 256) || a->workspace_bytes < need)
         return fail(FA_ERR_INVALID_ARG, "workspace is NULL, not 256-byte aligned, or smaller than %zu bytes", need);
     FA_TRY(init_current());
-    const hipError_t e = fa::launch_lora_grad_many_bf16(&it, 1, a->tokens, a->workspace,
-                                                        static_cast<hipStream_t>(stream));
+    const hipError_t e = fa::launch_lora_grad_many_bf16(&it, 1, a->workspace, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lora grad launch");
     return ok();
 }
@@ -819,10 +824,10 @@ size_t fa_lora_grad_many_workspace_size(const fa_lora_grad_args *args, int32_t c
     fa::LoraGradItem items[kGradManyMax];
     for (int32_t i = 0; i < count; ++i) {
         const fa_lora_grad_args &a = args[i];
-        if (a.tokens != args[0].tokens || a.tokens < 1 || a.features < 1 || a.rank < 1 || a.rank > 64) return 0;
+        if (a.tokens < 1 || a.features < 1 || a.rank < 1 || a.rank > 64) return 0;
         items[i] = grad_item(&a);
     }
-    return fa::lora_grad_many_workspace_bytes(items, count, args[0].tokens);
+    return fa::lora_grad_many_workspace_bytes(items, count);
 }
 
 fa_status fa_lora_grad_many(const fa_lora_grad_args *args, int32_t count, void *workspace, size_t workspace_bytes,
@@ -832,17 +837,13 @@ fa_status fa_lora_grad_many(const fa_lora_grad_args *args, int32_t count, void *
     fa::LoraGradItem items[kGradManyMax];
     for (int32_t i = 0; i < count; ++i) {
         FA_TRY(check_lora_grad(&args[i]));
-        if (args[i].tokens != args[0].tokens)
-            return fail(FA_ERR_INVALID_ARG, "product %d: tokens %d differ from product 0's %d", i, args[i].tokens,
-                        args[0].tokens);
         items[i] = grad_item(&args[i]);
     }
-    const size_t need = fa::lora_grad_many_workspace_bytes(items, count, args[0].tokens);
+    const size_t need = fa::lora_grad_many_workspace_bytes(items, count);
     if (!workspace || !aligned(workspace, 256) || workspace_bytes < need)
         return fail(FA_ERR_INVALID_ARG, "workspace is NULL, not 256-byte aligned, or smaller than %zu bytes", need);
     FA_TRY(init_current());
-    const hipError_t e = fa::launch_lora_grad_many_bf16(items, count, args[0].tokens, workspace,
-                                                        static_cast<hipStream_t>(stream));
+    const hipError_t e = fa::launch_lora_grad_many_bf16(items, count, workspace, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lora grad launch");
     return ok();
 }

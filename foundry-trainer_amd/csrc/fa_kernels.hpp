@@ -124,13 +124,13 @@ struct LoraGradItem {
     int64_t ldu;
     const void *x;
     int64_t ldx;
-    int C, R;
+    int N, C, R;
     float scale;
     float *grad;
     bool transpose;
 };
-size_t lora_grad_many_workspace_bytes(const LoraGradItem *items, int count, int N);
-hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int N, void *work, hipStream_t st);
+size_t lora_grad_many_workspace_bytes(const LoraGradItem *items, int count);
+hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, void *work, hipStream_t st);
 
 // LayerNorm-modulation over [N, C] rows (C % 8 == 0, C <= 4096).
 struct LnModParams {

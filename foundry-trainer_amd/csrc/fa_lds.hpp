@@ -188,12 +188,14 @@ __device__ __forceinline__ void set_half(bf16x8 &v, int half, u32x2 w) {
 // is linear and invertible over GF(2) (r0 = k2, r1 = k1, r2 = k0^k1,
 // r3 = k3^k1), and over the 4 rows of a transpose read (r2, r3 fixed) bits
 // 1..2 take (r1, r0) and bits 2..3 take (r0, r1^r3): all distinct.  It depends
-// on r % 16 only.  D = 64 tiles have 8 chunks per row and use bits 0..2.
+// on r % 16 only.  D = 64 tiles have 8 chunks per row and use bits 0..2,
+// D = 32 tiles (4 chunks) bits 0..1.
 template <int D>
 __device__ __forceinline__ int chunk_swz(int row) {
+    static_assert(D == 32 || D == 64 || D == 128, "tile widths of 32, 64 or 128 features");
     const int r0 = row & 1, r1 = (row >> 1) & 1, r2 = (row >> 2) & 1, r3 = (row >> 3) & 1;
     const int k = (r2 ^ r1) | (r1 << 1) | (r0 << 2);
-    return D >= 128 ? (k | ((r1 ^ r3) << 3)) : k;
+    return D >= 128 ? (k | ((r1 ^ r3) << 3)) : D == 64 ? k : (k & 3);
 }
 
 // Tile geometry for a D-feature bf16 tile of `ROWS` rows.

@@ -23,6 +23,8 @@
 //           — deterministic, no atomics.  f32
 //           (the parity path): each workgroup owns 64 columns and sweeps all
 //           rows in a fixed order.
+#include <type_traits>
+
 #include "fa_device.hpp"
 #include "fa_kernels.hpp"
 #include "fa_lds.hpp"
@@ -507,13 +509,13 @@ __global__ void lora_colsum_reduce_kernel(const float *__restrict__ part, float 
 }
 
 // ---- colsum over several products in one set of launches -----------------
-// Products k = 0..count-1 of one token count N: out_k = s_k * U_k^T X_k (or
-// its transpose), U_k bf16 [N, R_k <= 64].  The same three steps as above,
+// Products k = 0..count-1, each of its own token count N_k: out_k = s_k *
+// U_k^T X_k (or its transpose), U_k bf16 [N_k, R_k <= 64].  The same three steps as above,
 // each one launch for all products: U^T in operand order (rw = 32 or 64 rows),
 // split partials over [splits_k][C_k][rw] (R_k > 32: a second accumulator
 // over U^T rows 32..63 shares each X tile), fixed-order sum.  Per output the
 // arithmetic is that of the single-product kernels, so the same bits.
-constexpr int kGradMany = 8;
+constexpr int kGradMany = 16;
 struct GradProblem {
     const bf16 *u;
     int64_t ldu;
@@ -524,20 +526,21 @@ struct GradProblem {
     bf16 *ut;     // [rw][npad]
     float *part;  // [splits][C][rw]
     float s;
-    int C, R, rw, splits, chunk, tile0;
+    int C, R, rw, splits, chunk, wg0;  // wg0: the product's first colsum workgroup
+    int N, npad;  // tokens, and tokens rounded up to whole 64-token stages
 };
 struct GradMany {
     GradProblem p[kGradMany];
-    int count, N, npad;
+    int count;
 };
 
 __global__ void lora_ut_many_kernel(GradMany g) {
     const GradProblem &q = g.p[blockIdx.y];
     const int e = blockIdx.x * 256 + threadIdx.x;
-    if (e >= q.rw * g.npad) return;
+    if (e >= q.rw * q.npad) return;
     int j, n;
-    ut_frag_coords(e, g.npad, j, n);
-    q.ut[e] = j < q.R && n < g.N ? q.u[(int64_t)n * q.ldu + j] : (bf16)0.f;
+    ut_frag_coords(e, q.npad, j, n);
+    q.ut[e] = j < q.R && n < q.N ? q.u[(int64_t)n * q.ldu + j] : (bf16)0.f;
 }
 
 // One workgroup: column tile, token split of product q.  DIRECT (every
@@ -552,23 +555,26 @@ __global__ void lora_ut_many_kernel(GradMany g) {
 // the compiler then tells the DMA into one stage from the reads of the other.
 template <bool DIRECT>
 __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
+    // one workgroup per (product, split, column tile): product k's
+    // workgroups start at wg0, split-major
     int k = 0;
-    while (k + 1 < g.count && g.p[k + 1].tile0 <= (int)blockIdx.x) ++k;
+    while (k + 1 < g.count && g.p[k + 1].wg0 <= (int)blockIdx.x) ++k;
     const GradProblem &q = g.p[k];
-    if ((int)blockIdx.y >= q.splits) return;  // uniform over the workgroup
+    const int ntiles = (q.C + kCsCols - 1) / kCsCols;
+    const int wi = (int)blockIdx.x - q.wg0, split = wi / ntiles, tile = wi - split * ntiles;
     using T = LdsTile<128, kCsRows>;
-    using UT = LdsTile<64, kCsRows>;
-    constexpr int WI = T::WAVE_INSTS / 4, UWI = UT::WAVE_INSTS / 4;
+    using UT = LdsTile<64, kCsRows>;  // the widest U tile (R > 32)
+    constexpr int WI = T::WAVE_INSTS / 4;
     __shared__ __align__(16) char st0[T::BYTES], st1[T::BYTES];
     __shared__ __align__(16) char uu0[DIRECT ? UT::BYTES : 16], uu1[DIRECT ? UT::BYTES : 16];
-    const int N = g.N, npad = g.npad;
+    const int N = q.N, npad = q.npad;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 31;
     const int C = q.C;
     const int64_t ldx = q.ldx;
-    const int c0 = ((int)blockIdx.x - q.tile0) * kCsCols;
-    const int t_begin = blockIdx.y * q.chunk, t_end = min(t_begin + q.chunk, npad);
+    const int c0 = tile * kCsCols;
+    const int t_begin = split * q.chunk, t_end = min(t_begin + q.chunk, npad);
     const bool two = q.rw == 64;
     // rows >= N (and, in the last row, columns >= C) read as zero
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(q.x + c0, (uint32_t)(((int64_t)(N - 1) * ldx + (C - c0)) * 2));
@@ -581,26 +587,15 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     // half, lies in the row's 16-byte stride).
     const __amdgpu_buffer_rsrc_t urs =
         make_rsrc(q.u, (uint32_t)((int64_t)(N - 1) * q.ldu * 2 + ((q.R * 2 + 3) & ~3)));
-    const uint32_t uvo = DIRECT ? tile_src_off<64>(wave, lane, q.ldu) : 0u;
-    const uint32_t urow_step = tile_inst_row_step<64>(q.ldu);
     const uint32_t ustage_step = (uint32_t)(kCsRows * q.ldu * 2);
-    auto issue = [&](int t0, char *dst, char *udst) {
+    auto issue_x = [&](int t0, char *dst) {
 #pragma unroll
         for (int i = 0; i < WI; ++i)
             buffer_to_lds_16(xrs, dst + (i * 4 + wave) * 1024, xvo, (uint32_t)(t0 / kCsRows) * stage_step + i * row_step);
-        if constexpr (DIRECT) {
-#pragma unroll
-            for (int i = 0; i < UWI; ++i)
-                buffer_to_lds_16(urs, udst + (i * 4 + wave) * 1024, uvo,
-                                 (uint32_t)(t0 / kCsRows) * ustage_step + i * urow_step);
-        }
     };
     uint32_t coff[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) coff[dt] = col_frag_off<128>(0, 0, dt, lane);
-    uint32_t cu[2];
-#pragma unroll
-    for (int f = 0; f < 2; ++f) cu[f] = col_frag_off<64>(0, 0, f, lane);
     const bf16 *ub = q.ut + lane * 8;            // fragment-major: 512 values per 16-token step
     const bf16 *ub2 = ub + (int64_t)32 * npad;   // rows 32..63
     f32x16 acc, acc2;
@@ -622,45 +617,74 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
             }
         }
     };
-    auto stage = [&](const char *tile, const char *utile, const bf16x8 (&b)[2 * KS]) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
-                                               col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
-            bf16x8 b0;
-            if constexpr (DIRECT)
-                b0 = lds_read_col_frag(utile, cu[0] + ks * 16 * UT::ROWB, col_frag_hi8<64>(cu, 0) + ks * 16 * UT::ROWB);
-            else
-                b0 = b[ks];
-            acc = mfma_32x32x16(a, b0, acc);
-            if (two) {
-                bf16x8 b1;
-                if constexpr (DIRECT)
-                    b1 = lds_read_col_frag(utile, cu[1] + ks * 16 * UT::ROWB,
-                                           col_frag_hi8<64>(cu, 1) + ks * 16 * UT::ROWB);
-                else
-                    b1 = b[KS + ks];
-                acc2 = mfma_32x32x16(a, b1, acc2);
-            }
-        }
-    };
-    bf16x8 bu[2 * KS];
-    issue(t_begin, st0, uu0);
     if constexpr (DIRECT) {
-        // Each stage's refill goes out unconditionally (past the split's
-        // range it reads rows of the next split or zeros, never used): a
-        // conditional issue made the compiler wait for the refill of one
-        // stage before reading the other.  Only the second stage's reads
-        // are conditional.
-        for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
-            barrier_keep_dma<0>();
-            issue(t0 + kCsRows, st1, uu1);
-            stage(st0, uu0, bu);
-            barrier_keep_dma<0>();
-            issue(t0 + 2 * kCsRows, st0, uu0);
-            if (t0 + kCsRows < t_end) stage(st1, uu1, bu);
-        }
+        // The U tile is as wide as the product needs: 32 columns (R <= 32,
+        // 4 KiB a stage) or 64 (8 KiB); body<UW> is the whole pipeline for
+        // one width, so each keeps its loop free of conditions.
+        auto body = [&](auto uwc) {
+            constexpr int UW = decltype(uwc)::value;
+            using U = LdsTile<UW, kCsRows>;
+            constexpr int UWI = U::WAVE_INSTS / 4;
+            const uint32_t uvo = tile_src_off<UW>(wave, lane, q.ldu);
+            const uint32_t urow_step = tile_inst_row_step<UW>(q.ldu);
+            uint32_t cu[UW / 32];
+#pragma unroll
+            for (int f = 0; f < UW / 32; ++f) cu[f] = col_frag_off<UW>(0, 0, f, lane);
+            auto issue = [&](int t0, char *dst, char *udst) {
+                issue_x(t0, dst);
+#pragma unroll
+                for (int i = 0; i < UWI; ++i)
+                    buffer_to_lds_16(urs, udst + (i * 4 + wave) * 1024, uvo,
+                                     (uint32_t)(t0 / kCsRows) * ustage_step + i * urow_step);
+            };
+            auto stage = [&](const char *tile, const char *utile) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
+                                                       col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
+                    const bf16x8 b0 = lds_read_col_frag(utile, cu[0] + ks * 16 * U::ROWB,
+                                                        col_frag_hi8<UW>(cu, 0) + ks * 16 * U::ROWB);
+                    acc = mfma_32x32x16(a, b0, acc);
+                    if constexpr (UW == 64) {
+                        const bf16x8 b1 = lds_read_col_frag(utile, cu[1] + ks * 16 * U::ROWB,
+                                                            col_frag_hi8<UW>(cu, 1) + ks * 16 * U::ROWB);
+                        acc2 = mfma_32x32x16(a, b1, acc2);
+                    }
+                }
+            };
+            // Each stage's refill goes out unconditionally (past the split's
+            // range it reads rows of the next split or zeros, never used): a
+            // conditional issue made the compiler wait for the refill of one
+            // stage before reading the other.  Only the second stage's reads
+            // are conditional.  (A ring of three stages, two in flight, ran
+            // slower: 72 KiB of LDS leaves two workgroups per CU, not three.)
+            issue(t_begin, st0, uu0);
+            for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
+                barrier_keep_dma<0>();
+                issue(t0 + kCsRows, st1, uu1);
+                stage(st0, uu0);
+                barrier_keep_dma<0>();
+                issue(t0 + 2 * kCsRows, st0, uu0);
+                if (t0 + kCsRows < t_end) stage(st1, uu1);
+            }
+        };
+        if (two)
+            body(std::integral_constant<int, 64>{});
+        else
+            body(std::integral_constant<int, 32>{});
     } else {
+        auto issue = [&](int t0, char *dst, char *) { issue_x(t0, dst); };
+        auto stage = [&](const char *tile, const char *, const bf16x8 (&b)[2 * KS]) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const bf16x8 a = lds_read_col_frag(tile, coff[wave] + ks * 16 * T::ROWB,
+                                                   col_frag_hi8<128>(coff, wave) + ks * 16 * T::ROWB);
+                acc = mfma_32x32x16(a, b[ks], acc);
+                if (two) acc2 = mfma_32x32x16(a, b[KS + ks], acc2);
+            }
+        };
+        bf16x8 bu[2 * KS];
+        issue(t_begin, st0, uu0);
         for (int t0 = t_begin; t0 < t_end; t0 += 2 * kCsRows) {
             barrier_keep_dma<0>();
             loadu(t0, bu);
@@ -677,7 +701,7 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // acc element r: column c0 + wave*32 + acc_row(r, lane), j = n (acc2: j = 32 + n)
     const int rw = q.rw;
-    float *pp = q.part + (int64_t)blockIdx.y * C * rw;
+    float *pp = q.part + (int64_t)split * C * rw;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int c = c0 + wave * 32 + acc_row(r, lane);
@@ -749,16 +773,19 @@ hipError_t expand(const float *U, int64_t ldu, const T *Wt, T *Y, int64_t ldy, i
     return hipGetLastError();
 }
 
-// Token splits of the bf16 colsum: about 256 workgroups (one per CU), each
-// split a multiple of 64 tokens.  At the c4 shapes (N = 4096, C = 3072: 24
-// column tiles) that is 11 splits of 384 tokens; targeting 512 workgroups
-// (shorter splits, twice the partials) measured ~1% slower over the whole
-// double-block step, 1024 slower still.
+// Token splits of the bf16 colsum: up to about 256 workgroups per product,
+// each split a multiple of 64 tokens and at least 16 stages (1024 tokens)
+// long.  A workgroup's fixed part (first stage's wait, partial store) and the
+// partial bytes the reduce reads favour long splits: the c4 double block's 12
+// products (4096 and 512 tokens, C = 3072) in one call took 48.0 us with
+// splits of at least 4 stages (11 splits of 384 tokens at 4096), 45.2 with 8,
+// 40.8 with 16 and 40.8-43 with 32 (but its q/k/v group alone 23.8 us at 16
+// against 28.1 at 32); a ring of three stages lost to the occupancy it cost.
 inline int colsum_splits(int N, int C) {
     const int tiles = (C + kCsCols - 1) / kCsCols;
     const int stages = (N + kCsRows - 1) / kCsRows;
     int sp = (256 + tiles - 1) / tiles;
-    if (sp > stages) sp = stages;
+    if (sp > stages / 16) sp = stages / 16;
     return sp < 1 ? 1 : sp;
 }
 inline int colsum_npad(int N) { return (N + kCsRows - 1) / kCsRows * kCsRows; }
@@ -903,26 +930,24 @@ inline size_t grad_item_bytes(int N, int C, int R) {
 }
 }  // namespace
 
-size_t lora_grad_many_workspace_bytes(const LoraGradItem *items, int count, int N) {
+size_t lora_grad_many_workspace_bytes(const LoraGradItem *items, int count) {
     // sets of kGradMany products run one after another over the same bytes
     size_t most = 0;
     for (int k0 = 0; k0 < count; k0 += kGradMany) {
         size_t b = 0;
-        for (int k = k0; k < count && k < k0 + kGradMany; ++k) b += grad_item_bytes(N, items[k].C, items[k].R);
+        for (int k = k0; k < count && k < k0 + kGradMany; ++k)
+            b += grad_item_bytes(items[k].N, items[k].C, items[k].R);
         most = b > most ? b : most;
     }
     return most;
 }
 
-hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int N, void *work, hipStream_t st) {
-    const int npad = colsum_npad(N), stages = npad / kCsRows;
+hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, void *work, hipStream_t st) {
     for (int k0 = 0; k0 < count; k0 += kGradMany) {
         GradMany g{};
         g.count = count - k0 < kGradMany ? count - k0 : kGradMany;
-        g.N = N;
-        g.npad = npad;
         char *ws = static_cast<char *>(work);
-        int tiles = 0, max_splits = 1, max_out = 1;
+        int wgs = 0, max_out = 1, max_npad = kCsRows;
         bool staged = false;
         for (int k = 0; k < g.count; ++k) {
             const LoraGradItem &it = items[k0 + k];
@@ -940,26 +965,26 @@ hipError_t launch_lora_grad_many_bf16(const LoraGradItem *items, int count, int 
             q.C = it.C;
             q.R = it.R;
             q.rw = grad_rows(it.R);
-            q.splits = colsum_splits(N, it.C);
-            q.chunk = (stages + q.splits - 1) / q.splits * kCsRows;
-            q.tile0 = tiles;
+            q.N = it.N;
+            q.npad = colsum_npad(it.N);
+            q.splits = colsum_splits(it.N, it.C);
+            q.chunk = (q.npad / kCsRows + q.splits - 1) / q.splits * kCsRows;
+            q.wg0 = wgs;
             q.ut = reinterpret_cast<bf16 *>(ws);
-            ws += al256((size_t)q.rw * npad * 2);
+            ws += al256((size_t)q.rw * q.npad * 2);
             q.part = reinterpret_cast<float *>(ws);
             ws += al256((size_t)q.splits * it.C * q.rw * 4);
-            tiles += (it.C + kCsCols - 1) / kCsCols;
-            max_splits = q.splits > max_splits ? q.splits : max_splits;
+            wgs += (it.C + kCsCols - 1) / kCsCols * q.splits;
             max_out = it.C * q.rw > max_out ? it.C * q.rw : max_out;
+            max_npad = q.npad > max_npad ? q.npad : max_npad;
         }
         if (staged)
-            hipLaunchKernelGGL(lora_ut_many_kernel, dim3((unsigned)((64 * npad + 255) / 256), (unsigned)g.count),
+            hipLaunchKernelGGL(lora_ut_many_kernel, dim3((unsigned)((64 * max_npad + 255) / 256), (unsigned)g.count),
                                dim3(256), 0, st, g);
         if (staged)
-            hipLaunchKernelGGL(lora_colsum_many_kernel<false>, dim3((unsigned)tiles, (unsigned)max_splits), dim3(256), 0,
-                               st, g);
+            hipLaunchKernelGGL(lora_colsum_many_kernel<false>, dim3((unsigned)wgs), dim3(256), 0, st, g);
         else
-            hipLaunchKernelGGL(lora_colsum_many_kernel<true>, dim3((unsigned)tiles, (unsigned)max_splits), dim3(256), 0,
-                               st, g);
+            hipLaunchKernelGGL(lora_colsum_many_kernel<true>, dim3((unsigned)wgs), dim3(256), 0, st, g);
         hipLaunchKernelGGL(lora_colsum_reduce_many_kernel, dim3((unsigned)((max_out + 255) / 256), (unsigned)g.count),
                            dim3(256), 0, st, g);
         const hipError_t e = hipGetLastError();

@@ -764,7 +764,7 @@ class DoubleBlockLoRA:
                 self.capture[f"{name}.q"] = B["q"][0, off:off + n].clone()
                 self.capture[f"{name}.k"] = B["k"][0, off:off + n].clone()
 
-    def _out_phase(self, name, x, dy, o_t, y, saved):
+    def _out_phase(self, name, x, dy, o_t, y, saved, grads):
         """Out projection, gated residuals, MLP; with dy, the backward down to dO."""
         B, C, s = self._buf, self.C, self.lora_scale
         w, off, n = self.w[name], self.offset[name], self.rows[name]
@@ -831,8 +831,10 @@ class DoubleBlockLoRA:
             du = lora_down(dout, self._b_out_t[name], s, out=dox[:, C:C + r])  # s dout B_out
             rhs = self._out_ext_t[name].t() if self._wt is not None else self._out_ext[name]
             torch.mm(dox, rhs, out=do_rows)  # dout W_out + du A_out
-            # dA_out = du^T a, dB_out = s dout^T u
-            saved[(name, "out", "grad")] = tuple(lora_grad_many([(du, a, 1.0, False), (u_out, dout, s, True)]))
+            # dA_out = du^T a, dB_out = s dout^T u: formed with the step's other
+            # factor gradients (_grad_pending)
+            self._grad_pending.append(([(du, a, 1.0, False), (u_out, dout, s, True)],
+                                       lambda res, name=name: grads.__setitem__((name, "out"), tuple(res))))
             return
         torch.mm(dout, self._dx_weight(name, "w_out"), out=do_rows)
         if u_out is not None:
@@ -866,12 +868,14 @@ class DoubleBlockLoRA:
                     lora_down(drows[:, j * C:(j + 1) * C], self._b_t[name][t], 1.0, out=tq[:, j * r:(j + 1) * r])
             if dh is not None:
                 lora_up(tq, self._a_qkv_t[name], dh, s)  # dh += s t A_qkv
-            # dA_qkv [3r, C] = s t^T h and dB_j = dy_j^T (s u_j), one set of launches
-            da, *dbs = lora_grad_many([(tq, h, s, False)] +
-                                      [(su[:, j * r:(j + 1) * r], drows[:, j * C:(j + 1) * C], 1.0, True)
-                                       for j in range(len(QKV))])
-            for j, t in enumerate(QKV):
-                grads[(name, t)] = (da[j * r:(j + 1) * r], dbs[j])
+            # dA_qkv [3r, C] = s t^T h and dB_j = dy_j^T (s u_j)
+            def place(res, name=name):
+                da, *dbs = res
+                for j, t in enumerate(QKV):
+                    grads[(name, t)] = (da[j * r:(j + 1) * r], dbs[j])
+            self._grad_pending.append(([(tq, h, s, False)] +
+                                       [(su[:, j * r:(j + 1) * r], drows[:, j * C:(j + 1) * C], 1.0, True)
+                                        for j in range(len(QKV))], place))
         else:
             for j, t in enumerate(QKV):
                 if t in w.lora_a:
@@ -889,6 +893,7 @@ class DoubleBlockLoRA:
         C, S, H, D = self.C, self.S, self.H, self.D
         main = torch.cuda.current_stream(self.device)
         saved, y, grads = {}, {}, {}
+        self._grad_pending = []
         order = CAPTURE_ORDER if torch.cuda.is_current_stream_capturing() else ISSUE_ORDER
         self._fork()
         for name in order:
@@ -908,7 +913,7 @@ class DoubleBlockLoRA:
         self._fork()
         for name in order:
             with self._on(name):
-                self._out_phase(name, x, dy, o_t, y, saved)
+                self._out_phase(name, x, dy, o_t, y, saved, grads)
         self._join()
         if dy is None:
             return y, kept
@@ -925,6 +930,16 @@ class DoubleBlockLoRA:
             with self._on(name):
                 self._qkv_bwd_phase(name, x, want_dx, saved, grads)
         self._join()
+        if self._grad_pending:
+            # The LoRA factor gradients of both streams (q/k/v and out) in one
+            # fa_lora_grad_many call: their inputs stay in the step's buffers,
+            # and only AdamW reads the results.
+            items = [it for its, _ in self._grad_pending for it in its]
+            res = lora_grad_many(items)
+            k = 0
+            for its, place in self._grad_pending:
+                place(res[k:k + len(its)])
+                k += len(its)
         if self._side is not None:
             # tensors made on the side stream and consumed on this one
             for key, g in grads.items():
@@ -1187,7 +1202,11 @@ class SingleBlockLoRA:
             dout = gated_residual(None, g, dy, out=dout_ext[:, :C])
             du_out = lora_down(dout, self.b_out_t, s, out=dout_ext[:, C:C + r])
             torch.mm(dout_ext, self.w_out_ext if self.w_out_ext_t is None else self.w_out_ext_t.t(), out=djoined)
-            grads = {"to_out": tuple(lora_grad_many([(du_out, joined, 1.0, False), (u_out, dout, s, True)]))}
+            # dA_out = du_out^T joined, dB_out = s dout^T u_out: formed with
+            # to_in's in one fa_lora_grad_many call at the end (the inputs are
+            # not written again)
+            out_items = [(du_out, joined, 1.0, False), (u_out, dout, s, True)]
+            grads = {}
         else:
             dout = gated_residual(None, g, dy, out=B["dout"])
             torch.mm(dout, w.w_out, out=djoined)
@@ -1210,7 +1229,8 @@ class SingleBlockLoRA:
             else:
                 dnh = None
                 t_in = lora_down(dfused, w.lora_b["to_in"].t().contiguous(), 1.0, out=B["t_in"])
-            grads["to_in"] = tuple(lora_grad_many([(t_in, nh, s, False), (su_in, dfused, 1.0, True)]))
+            res = lora_grad_many(out_items + [(t_in, nh, s, False), (su_in, dfused, 1.0, True)])
+            grads["to_out"], grads["to_in"] = tuple(res[:2]), tuple(res[2:])
         else:
             dnh = torch.mm(dfused, w.w_in, out=B["dnh"]) if want_dx else None
             grads["to_in"] = lora_bwd(nh, w.lora_a["to_in"], w.lora_b["to_in"], u_in, dfused, s, dx=dnh)

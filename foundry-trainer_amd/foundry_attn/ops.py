@@ -559,9 +559,10 @@ def lora_grad(u, x, scale: float, transpose: bool, out: Optional[torch.Tensor] =
 
 
 def lora_grad_many(items):
-    """Several lora_grad products of one token count in one set of launches:
-    items are (u, x, scale, transpose) or (u, x, scale, transpose, out); the
-    results (same bits as separate lora_grad calls) come back in order."""
+    """Several lora_grad products, each of its own token count, in one set of
+    launches: items are (u, x, scale, transpose) or (u, x, scale, transpose,
+    out); the results (same bits as separate lora_grad calls) come back in
+    order."""
     if not items:
         return []
     built = [_lora_grad_args(*it[:4], it[4] if len(it) > 4 else None) for it in items]

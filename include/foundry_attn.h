@@ -376,15 +376,15 @@ size_t fa_lora_grad_workspace_size(const fa_lora_grad_args *args);
 /* grad = scale * u^T x (or its transpose), deterministic split-K reduction. */
 fa_status fa_lora_grad(const fa_lora_grad_args *args, void *stream);
 
-/* Several fa_lora_grad products of one token count in one set of launches
- * (up to 8 products per set; count <= 64): each grad gets the bits of its own
+/* Several fa_lora_grad products, each of its own token count, in one set of
+ * launches (up to 16 products per set; count <= 64): each grad gets the bits of its own
  * fa_lora_grad call.  The products' own workspace fields are ignored; the
  * call takes one workspace of fa_lora_grad_many_workspace_size bytes (0 for
  * invalid arguments).  The reference forms each adapter's dA and dB through
  * autograd, one matmul each (linear_scaled, lib.rs:270-287, applied by
  * throughput.rs:254-256 and differentiated by the backward at
- * throughput.rs:799); the blocks call this for the q, k, v (and out)
- * adapters of a stream at once. */
+ * throughput.rs:799); the double block calls this once per step for the q,
+ * k, v and out adapters of both streams. */
 size_t fa_lora_grad_many_workspace_size(const fa_lora_grad_args *args, int32_t count);
 fa_status fa_lora_grad_many(const fa_lora_grad_args *args, int32_t count, void *workspace,
                             size_t workspace_bytes, void *stream);

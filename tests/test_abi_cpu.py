@@ -421,7 +421,7 @@ def test_lora_pieces_validate_before_device_work():
     assert L.fa_lora_grad_workspace_size(ctypes.byref(gr)) > 0
     assert L.fa_lora_grad(ctypes.byref(gr), None) == _abi.FA_ERR_INVALID_ARG  # no workspace
     assert b"workspace" in L.fa_last_error()
-    # the grouped form: one workspace for all products, one token count
+    # the grouped form: one workspace for all products
     arr = (_abi.LoraGradArgs * 3)(*[_abi.LoraGradArgs.from_buffer_copy(gr) for _ in range(3)])
     arr[1].rank, arr[2].transpose = 48, 1
     need = L.fa_lora_grad_many_workspace_size(arr, 3)
@@ -430,12 +430,19 @@ def test_lora_pieces_validate_before_device_work():
     assert b"workspace" in L.fa_last_error()
     assert L.fa_lora_grad_many(arr, 3, _FAKE, need - 256, None) == _abi.FA_ERR_INVALID_ARG
     assert L.fa_lora_grad_many(arr, 0, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
-    arr[2].tokens = 65
+    # products may differ in token count: a longer one needs more workspace
+    arr[2].tokens = 4096
+    assert L.fa_lora_grad_many_workspace_size(arr, 3) > need
+    arr[2].tokens = 0
     assert L.fa_lora_grad_many_workspace_size(arr, 3) == 0
     assert L.fa_lora_grad_many(arr, 3, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
     assert b"tokens" in L.fa_last_error()
     arr[2].tokens, arr[1].rank = 64, 65
     assert L.fa_lora_grad_many(arr, 3, _FAKE, need, None) == _abi.FA_ERR_INVALID_ARG
+    # an x whose rows span 4 GiB or more is refused before any launch
+    arr[1].rank, arr[0].tokens, arr[0].ldx = 16, 1 << 20, 4096
+    assert L.fa_lora_grad_many(arr, 3, _FAKE, 1 << 40, None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"4 GiB" in L.fa_last_error()
 
 
 def test_copy2d_many_validates_before_device_work():

@@ -294,19 +294,22 @@ def test_lora_pieces_strided_views(r):
 
 
 def test_lora_grad_many_matches_separate_calls():
-    """fa_lora_grad_many: eleven products of one token count (ranks 4..64, so
-    one- and two-accumulator products, dA and dB layouts, strided u and x
-    views, a partial last column tile, two sets of launches) give the bits of
-    separate fa_lora_grad calls, with U staged or read directly, and two of
-    them match f64 products of the same values."""
+    """fa_lora_grad_many: eighteen products of several token counts (1 to
+    4096; ranks 4..64, so one- and two-accumulator products, dA and dB
+    layouts, strided u and x views, a partial last column tile, two sets of
+    launches) give the bits of separate fa_lora_grad calls, with U staged or
+    read directly, and three of them match f64 products of the same values."""
     from foundry_attn.ops import lora_grad, lora_grad_many
     rng = np.random.default_rng(321)
-    N, bf = 300, torch.bfloat16
+    bf = torch.bfloat16
     rnd = oracle.bf16_round
     items = []
-    for k, (r, C, tr) in enumerate([(4, 256, False), (16, 384, True), (40, 128, False), (48, 3072, True),
-                                     (64, 256, False), (12, 512, True), (33, 256, True), (16, 3072, False),
-                                     (8, 128, False), (64, 384, True), (20, 208, True)]):
+    for k, (N, r, C, tr) in enumerate([(300, 4, 256, False), (300, 16, 384, True), (64, 40, 128, False),
+                                        (300, 48, 3072, True), (517, 64, 256, False), (1, 12, 512, True),
+                                        (300, 33, 256, True), (4096, 16, 3072, False), (77, 8, 128, False),
+                                        (300, 64, 384, True), (300, 20, 208, True), (512, 48, 3072, False),
+                                        (512, 16, 3072, True), (4096, 48, 1024, False), (130, 16, 128, True),
+                                        (300, 4, 256, True), (1000, 32, 640, False), (63, 64, 128, True)]):
         ue = torch.zeros(N, r + 8, dtype=bf, device="cuda")
         ue[:, 3:3 + r] = dev(rnd(rng.standard_normal((N, r)).astype(np.float32)), bf)
         xe = torch.zeros(N, C + 16, dtype=bf, device="cuda")
@@ -320,7 +323,7 @@ def test_lora_grad_many_matches_separate_calls():
     # with no staging launch: the same bits.
     aligned = []
     for u, x, sc, tr in items:
-        buf = torch.zeros(N, 72, dtype=bf, device="cuda")
+        buf = torch.zeros(u.shape[0], 72, dtype=bf, device="cuda")
         buf[:, :u.shape[1]] = u
         aligned.append((buf[:, :u.shape[1]], x, sc, tr))
     direct = lora_grad_many(aligned)
@@ -329,7 +332,7 @@ def test_lora_grad_many_matches_separate_calls():
         assert a.shape == b.shape and torch.equal(a, b), k
     for k, (a, b) in enumerate(zip(direct, many)):
         assert torch.equal(a, b), k
-    for k in (3, 10):  # C = 3072, and C = 208 (a partial last column tile)
+    for k in (3, 10, 12):  # C = 3072, C = 208 (a partial last column tile), 512 tokens
         u, x, sc, tr = items[k]
         want = sc * host(x).astype(np.float64).T @ host(u).astype(np.float64)  # [C, r]
         np.testing.assert_allclose(host(many[k]), want, rtol=1e-4, atol=1e-3)
