@@ -201,7 +201,8 @@ def memory_bound_bench(torch, fa, cfg):
     per-token cos/sin rows and the weights), and the LoRA down / up pieces at
     the c4 img stream's shape (x [4096, 3072], r = 16: down reads x and A,
     writes u; up reads u and B and updates y in place), and the stream's
-    q/k/v adapter gradients as the block forms them (one grouped call)."""
+    q/k/v adapter gradients in one grouped call, and every factor gradient of
+    a c4 step (both streams) in the one call the block makes."""
     from foundry_attn.configs import C4
     g = torch.Generator(device="cuda").manual_seed(7)
     bf = torch.bfloat16
@@ -230,12 +231,31 @@ def memory_bound_bench(torch, fa, cfg):
     gout = [torch.empty((3 * r, C), device="cuda")] + [torch.empty((C, r), device="cuda") for _ in range(3)]
     gitems = [(gt, gh, 1.0, False, gout[0])] + [(gsu[j], gdy[j], 1.0, True, gout[1 + j]) for j in range(3)]
     gbytes = 4 * N * C * 2 + N * 6 * r * 2 + 6 * r * C * 4
+    # every LoRA factor gradient of a c4 double-block step in one call, as
+    # the block forms them: per stream (img N rows, txt T rows) the q/k/v
+    # group above plus the out adapter's pair (dA_out = du^T a, dB_out =
+    # dout^T u), 12 products
+    T = C4.txt_tokens
+    sitems, sbytes = [], 0
+    for rows, qkv in ((N, gitems), (T, None)):
+        if qkv is None:
+            th = torch.randn((rows, C), device="cuda", generator=g).to(bf)
+            qkv = [(torch.randn((rows, 3 * r), device="cuda", generator=g).to(bf), th, 1.0, False)] + \
+                  [(torch.randn((rows, r), device="cuda", generator=g).to(bf),
+                    torch.randn((rows, C), device="cuda", generator=g).to(bf), 1.0, True) for _ in range(3)]
+        sa_ = torch.randn((rows, C), device="cuda", generator=g).to(bf)
+        sdo = torch.randn((rows, C), device="cuda", generator=g).to(bf)
+        sdu = torch.randn((rows, r), device="cuda", generator=g).to(bf)
+        su = torch.randn((rows, r), device="cuda", generator=g).to(bf)
+        sitems += [it[:4] for it in qkv] + [(sdu, sa_, 1.0, False), (su, sdo, 1.0, True)]
+        sbytes += 6 * rows * C * 2 + 8 * rows * r * 2 + 8 * r * C * 4
     cases = {
         "qk_prologue_fwd": (lambda: fa.qk_prologue_multi(fwd_segs), 4 * row + tables),
         "qk_prologue_bwd": (lambda: fa.qk_prologue_bwd_multi(bwd_segs), 6 * row + tables),
         "lora_down": (lambda: fa.lora_down(lx, la, 1.0, out=lu), N * C * 2 + r * C * 2 + N * r * 2),
         "lora_up": (lambda: fa.lora_up(lu, lb, ly, 1.0), 2 * N * C * 2 + N * r * 2 + C * r * 2),
         "lora_grad_qkv": (lambda: fa.lora_grad_many(gitems), gbytes),
+        "lora_grad_step": (lambda: fa.lora_grad_many(sitems), sbytes),
     }
     out = {}
     for name, (fn, nbytes) in cases.items():
@@ -246,7 +266,8 @@ def memory_bound_bench(torch, fa, cfg):
                      "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2), "eager_ms": round(eager, 4)}
     out["shapes"] = (f"prologue: Q and K in one launch, each B={B} S={S} H={H} D={D} bf16; "
                      f"lora: N={N} C={C} r={r} bf16; lora_grad_qkv: dA [{3 * r}, {C}] and three dB [{C}, {r}] "
-                     f"in one call (reads h and three dy, f32 grads)")
+                     f"in one call (reads h and three dy, f32 grads); lora_grad_step: the c4 step's 12 factor "
+                     f"gradients (q/k/v and out of the img ({N} rows) and txt ({T} rows) streams) in one call")
     out["timing"] = ("ms: HIP events over 5 replays of a HIP graph of 20 calls (kernel time); "
                      "eager_ms: HIP events over 20 eager calls, which includes the host's per-call time")
     return out
