@@ -12,17 +12,21 @@
 //           parity path): one wave per 32 rows, operands from global memory.
 //           HBM-bound: one read of X.
 //   expand  Y[n][c] += s * sum_j U[n][j] Wt[c][j]       (y += s u B^T, and
-//           dx += du A): one thread per output column and row phase, Wt rows
-//           staged in LDS.  HBM-bound: one read and one write of Y.
+//           dx += du A).  bf16 (lora_expand_mfma_kernel): one wave per 32
+//           rows x 64 columns on v_mfma_f32_32x32x16_bf16, the result
+//           transposed through LDS so Y is updated with 16-byte accesses.  f32
+//           (the parity path): one thread per output column and row phase,
+//           Wt rows staged in LDS.  HBM-bound: one read and one write of Y.
 //   colsum  out[j][c] = s * sum_n U[n][j] X[n][c]      (dB^T = s u^T dy and
 //           dA = du^T x).  bf16: a skinny MFMA GEMM, X^T (by transpose reads
 //           of 64-token x 128-column tiles streamed into LDS) times U^T (read
-//           the same way from U's rows streamed beside them, or from a staged
-//           fragment-major copy when U is not 16-byte aligned), split over
-//           tokens; the splits are summed in a fixed order by a second kernel
-//           — deterministic, no atomics.  f32
-//           (the parity path): each workgroup owns 64 columns and sweeps all
-//           rows in a fixed order.
+//           the same way from a 32- or 64-column tile of U's rows streamed
+//           beside them, or from a staged fragment-major copy when U is not
+//           16-byte aligned), split over tokens; the splits are summed in a
+//           fixed order by a second kernel — deterministic, no atomics.  One
+//           set of launches serves up to 16 products of any token counts.
+//           f32 (the parity path): each workgroup owns 64 columns and sweeps
+//           all rows in a fixed order.
 #include <type_traits>
 
 #include "fa_device.hpp"
