@@ -242,7 +242,7 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
 }
 
 // expand: Y[n][c] += s * sum_j U[n][j] Wt[c][j], U f32 [N, R] rounded to bf16
-// for the MFMA, Wt [C, R] bf16 contiguous, R <= 32.  One wave per 32 rows x
+// for the MFMA, Wt [C, R] bf16 contiguous, R <= 64.  One wave per 32 rows x
 // 64 columns (two 32x32 output tiles, k = j).  VEC (16-byte loads of U and
 // Wt rows) needs R % 8 == 0 and 16-byte aligned U and Wt.
 template <bool VEC>
@@ -282,12 +282,14 @@ __device__ __forceinline__ bf16x8 load8_guarded_bf16(const bf16 *p, int j0, int 
     return o;
 }
 
-template <bool VEC, bool Y16, typename TU>
+template <bool VEC, bool Y16, typename TU, int KS>
 __global__ __launch_bounds__(256) void lora_expand_mfma_kernel(const TU *__restrict__ U, int64_t ldu,
                                                                const bf16 *__restrict__ Wt, bf16 *Y, int64_t ldy,
                                                                int N, int C, int R, float s) {
-    // per-wave 32 x 64 f32 result tile; rows padded to 68 floats (16-byte aligned)
-    __shared__ __attribute__((aligned(16))) float tile[4][32][68];
+    // per-wave half (16 rows x 64 columns) of the f32 result tile, used twice;
+    // rows padded to 68 floats (16-byte aligned).  17 KiB per workgroup lets
+    // six workgroups share a CU, so the c4 grids run in one round.
+    __shared__ __attribute__((aligned(16))) float tile[4][16][68];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 31, g = lane >> 5;
@@ -295,57 +297,81 @@ __global__ __launch_bounds__(256) void lora_expand_mfma_kernel(const TU *__restr
     const int col0 = (blockIdx.x * 4 + wave) * 64;
     const bool active = col0 < C;  // wave-uniform
     const int urow = min(row0 + n, N - 1);
+    // Every load goes out before the first is used: the Y chunks this lane
+    // updates at the end (they do not depend on the product), then the U and
+    // Wt operands of all KS = ceil(R / 16) rank steps, so the kernel waits on
+    // memory once rather than once per rank step and again for Y.
+    bf16x8 yv[4];
+    if constexpr (Y16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int row = row0 + (lane >> 3) + 8 * k, col = col0 + 8 * (lane & 7);
+            yv[k] = active && row < N && col < C ? as_bf16x8(ld_global_16(Y + (int64_t)row * ldy + col))
+                                                 : as_bf16x8(u32x4{0, 0, 0, 0});
+        }
+    }
+    bf16x8 a[KS], b[KS][2];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int ja = ks * 16 + g * 8;
+        const bool in = active && ja < R;
+        a[ks] = in ? load8_u_as_bf16<VEC>(U + (int64_t)urow * ldu + ja, ja, R) : as_bf16x8(u32x4{0, 0, 0, 0});
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int col = min(col0 + t * 32 + n, C - 1);
+            b[ks][t] = in ? load8_guarded_bf16<VEC>(Wt + (int64_t)col * R + ja, ja, R) : as_bf16x8(u32x4{0, 0, 0, 0});
+        }
+    }
+    if (!active) return;  // wave-uniform; the LDS buffer below is the wave's own
     f32x16 acc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-    if (active) {
-        for (int j0 = 0; j0 < R; j0 += 16) {
-            const int ja = j0 + g * 8;
-            const bf16x8 a = ja < R ? load8_u_as_bf16<VEC>(U + (int64_t)urow * ldu + ja, ja, R)
-                                    : as_bf16x8(u32x4{0, 0, 0, 0});
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int col = min(col0 + t * 32 + n, C - 1);
-                const bf16x8 b = ja < R ? load8_guarded_bf16<VEC>(Wt + (int64_t)col * R + ja, ja, R)
-                                        : as_bf16x8(u32x4{0, 0, 0, 0});
-                acc[t] = mfma_32x32x16(a, b, acc[t]);
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[t] = mfma_32x32x16(a[ks], b[ks][t], acc[t]);
+    // acc[t] element r: row acc_row(r, lane), column t*32 + n of the wave's
+    // tile.  Elements r < 8 hold rows 0..15, r >= 8 rows 16..31: half h goes
+    // through the buffer in pass h.  Each lane updates four 8-column chunks:
+    // chunk c = lane + 64k covers tile row c / 8, columns 8 * (c % 8) .. + 7
+    // (C % 16 == 0 keeps a chunk whole); chunks k = 2h, 2h + 1 lie in half h.
+    // Lanes exchange values through the wave's own buffer: a wait for the
+    // LDS operations with a compiler memory barrier separates each pass's
+    // writes from its reads, and pass 0's reads from pass 1's writes.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 8 * h; r < 8 * h + 8; ++r) tile[wave][acc_row(r, lane) - 16 * h][t * 32 + n] = acc[t][r];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k = 2 * h; k < 2 * h + 2; ++k) {
+            const int tr = (lane >> 3) + 8 * k, tc = 8 * (lane & 7);
+            const int row = row0 + tr, col = col0 + tc;
+            if (row >= N || col >= C) continue;
+            const f32x4 lo = *reinterpret_cast<const f32x4 *>(&tile[wave][tr - 16 * h][tc]);
+            const f32x4 hi = *reinterpret_cast<const f32x4 *>(&tile[wave][tr - 16 * h][tc + 4]);
+            bf16 *y = Y + (int64_t)row * ldy + col;
+            if constexpr (Y16) {
+                bf16x8 v = yv[k];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = f32_to_bf16((float)v[e] + s * lo[e]);
+                    v[4 + e] = f32_to_bf16((float)v[4 + e] + s * hi[e]);
+                }
+                st_global_16(y, as_u32x4(v));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = f32_to_bf16((float)y[e] + s * lo[e]);
+                    y[4 + e] = f32_to_bf16((float)y[4 + e] + s * hi[e]);
+                }
             }
         }
-    }
-    // acc[t] element r: row acc_row(r, lane), column t*32 + n of the wave's tile
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tile[wave][acc_row(r, lane)][t * 32 + n] = acc[t][r];
-    __syncthreads();
-    if (!active) return;
-    // each lane updates four 8-column chunks: chunk c = lane + 64k covers tile
-    // row c / 8, columns 8 * (c % 8) .. + 7; C % 16 == 0 keeps a chunk whole
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int tr = (lane >> 3) + 8 * k, tc = 8 * (lane & 7);
-        const int row = row0 + tr, col = col0 + tc;
-        if (row >= N || col >= C) continue;
-        const f32x4 lo = *reinterpret_cast<const f32x4 *>(&tile[wave][tr][tc]);
-        const f32x4 hi = *reinterpret_cast<const f32x4 *>(&tile[wave][tr][tc + 4]);
-        bf16 *y = Y + (int64_t)row * ldy + col;
-        if constexpr (Y16) {
-            bf16x8 v = as_bf16x8(ld_global_16(y));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] = f32_to_bf16((float)v[e] + s * lo[e]);
-                v[4 + e] = f32_to_bf16((float)v[4 + e] + s * hi[e]);
-            }
-            st_global_16(y, as_u32x4(v));
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                y[e] = f32_to_bf16((float)y[e] + s * lo[e]);
-                y[4 + e] = f32_to_bf16((float)y[4 + e] + s * hi[e]);
-            }
-        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 }
 
@@ -756,12 +782,24 @@ hipError_t rowdot(const T *X, int64_t ldx, const T *W, float *out, int64_t ldo, 
 template <typename TU>
 hipError_t expand_mfma(const TU *U, int64_t ldu, const bf16 *Wt, bf16 *Y, int64_t ldy, int N, int C, int R, float s,
                        hipStream_t st) {
+    if (R < 1 || R > 64) return hipErrorInvalidValue;  // one to four 16-wide rank steps
     const dim3 grid((unsigned)((C + 255) / 256), (unsigned)((N + 31) / 32)), block(256);
     const bool vec = R % 8 == 0 && (ldu * (int64_t)sizeof(TU)) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(U) % 16 == 0 && reinterpret_cast<uintptr_t>(Wt) % 16 == 0;
     const bool y16 = ldy % 8 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0;
-    auto kern = vec ? (y16 ? lora_expand_mfma_kernel<true, true, TU> : lora_expand_mfma_kernel<true, false, TU>)
-                    : (y16 ? lora_expand_mfma_kernel<false, true, TU> : lora_expand_mfma_kernel<false, false, TU>);
+    // the rank steps are a template argument, so a rank-16 launch holds the
+    // registers of one step's operands (more waves per SIMD), not four
+    auto pick = [&](auto ksc) {
+        constexpr int KS = decltype(ksc)::value;
+        return vec ? (y16 ? lora_expand_mfma_kernel<true, true, TU, KS> : lora_expand_mfma_kernel<true, false, TU, KS>)
+                   : (y16 ? lora_expand_mfma_kernel<false, true, TU, KS>
+                          : lora_expand_mfma_kernel<false, false, TU, KS>);
+    };
+    const int ks = (R + 15) / 16;
+    auto kern = ks == 1   ? pick(std::integral_constant<int, 1>{})
+                : ks == 2 ? pick(std::integral_constant<int, 2>{})
+                : ks == 3 ? pick(std::integral_constant<int, 3>{})
+                          : pick(std::integral_constant<int, 4>{});
     hipLaunchKernelGGL(kern, grid, block, 0, st, U, ldu, Wt, Y, ldy, N, C, R, s);
     return hipGetLastError();
 }
