@@ -249,6 +249,36 @@ def test_lora_down_k_tails(K, r):
     assert max_abs(got, want) <= 2 ** -7 * peak + 1e-6 and rel_l2(got, want) <= 4e-3, (K, r)
 
 
+@pytest.mark.parametrize("r", [1, 16, 17, 48, 64])
+@pytest.mark.parametrize("y_aligned", [True, False])
+def test_lora_up_rank_steps_and_y_alignment(r, y_aligned):
+    """fa_lora_up over one to four 16-wide rank steps (the kernel's rank-step
+    count is a template argument chosen per call), a token count that is not a
+    multiple of 32, a column count that leaves idle waves in the last
+    workgroup, and y either 16-byte aligned (16-byte loads and stores, loaded
+    before the product) or at a 2-byte offset (the element path).  Against y
+    plus the f64 product of the same bf16 values."""
+    from foundry_attn.ops import lora_up
+    rng = np.random.default_rng(700 + r)
+    N, M, s = 77, 336, 0.75
+    rnd = oracle.bf16_round
+    u = rnd(rng.standard_normal((N, r)).astype(np.float32))
+    B = rnd(0.05 * rng.standard_normal((M, r)).astype(np.float32))
+    y0 = rnd(rng.standard_normal((N, M)).astype(np.float32))
+    bf = torch.bfloat16
+    ldy = M + 24 if y_aligned else M + 1
+    yb = torch.zeros(N * ldy + 8, dtype=bf, device="cuda")
+    yv = yb[(0 if y_aligned else 1):][:N * ldy].view(N, ldy)[:, :M]
+    yv.copy_(dev(y0, bf))
+    lora_up(dev(u, bf), dev(B, bf), yv, s)
+    want = y0.astype(np.float64) + s * (u.astype(np.float64) @ B.T.astype(np.float64))
+    got = host(yv)
+    assert max_abs(got, want) <= 2 ** -7 * np.abs(want).max() + 1e-6 and rel_l2(got, want) <= 4e-3, (r, y_aligned)
+    # columns between rows (the row padding) are untouched
+    pad = yb[(0 if y_aligned else 1):][:N * ldy].view(N, ldy)[:, M:]
+    assert float(pad.abs().max()) == 0.0
+
+
 @pytest.mark.parametrize("r", [4, 16, 32, 40, 48, 64])
 def test_lora_pieces_strided_views(r):
     """fa_lora_down / fa_lora_up / fa_lora_grad on the rank-column views a
