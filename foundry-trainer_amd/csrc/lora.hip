@@ -19,7 +19,7 @@
 //           Wt rows staged in LDS.  HBM-bound: one read and one write of Y.
 //   colsum  out[j][c] = s * sum_n U[n][j] X[n][c]      (dB^T = s u^T dy and
 //           dA = du^T x).  bf16: a skinny MFMA GEMM, X^T (by transpose reads
-//           of 64-token x 128-column tiles streamed into LDS) times U^T (read
+//           of 32-token x 128-column tiles streamed into LDS) times U^T (read
 //           the same way from a 32- or 64-column tile of U's rows streamed
 //           beside them, or from a staged fragment-major copy when U is not
 //           16-byte aligned), split over tokens; the splits are summed in a
@@ -440,7 +440,11 @@ __global__ void lora_ut_kernel(const TU *__restrict__ U, int64_t ldu, bf16 *ut, 
 }
 
 constexpr int kCsCols = 128;  // columns per workgroup (4 waves x 32)
-constexpr int kCsRows = 64;   // tokens per LDS stage
+// Tokens per LDS stage.  32 rather than 64: 24 KiB of LDS per workgroup
+// (two stages of X and U) lets six workgroups share a CU instead of three;
+// the c4 step's 12 gradient products 41.0 -> 38.4 us, the single block's
+// four 110.3 -> 103.8 us, same bits (a 4-product q/k/v set 23.7 -> 24.9 us).
+constexpr int kCsRows = 32;
 
 // Workgroup (column tile ct, token split sp): part[sp][c][j] = sum over the
 // split's tokens of X[n][c] U[n][j], for the tile's 128 columns and j < 32.
@@ -557,7 +561,7 @@ struct GradProblem {
     float *part;  // [splits][C][rw]
     float s;
     int C, R, rw, splits, chunk, wg0;  // wg0: the product's first colsum workgroup
-    int N, npad;  // tokens, and tokens rounded up to whole 64-token stages
+    int N, npad;  // tokens, and tokens rounded up to whole stages (kCsRows)
 };
 struct GradMany {
     GradProblem p[kGradMany];
@@ -574,9 +578,10 @@ __global__ void lora_ut_many_kernel(GradMany g) {
 }
 
 // One workgroup: column tile, token split of product q.  DIRECT (every
-// product's U 16-byte aligned with 16-byte rows): U's rows for a stage (64
-// tokens x 64 columns) come into LDS by DMA beside the X tile, and the B operand is a column
-// fragment of that tile -- the same transpose read, hence the same token
+// product's U 16-byte aligned with 16-byte rows): U's rows for a stage
+// (kCsRows tokens x 32 or 64 columns) come into LDS by DMA beside the X tile,
+// and the B operand is a column fragment of that tile -- the same transpose
+// read, hence the same token
 // order, as X's A operand; columns j >= R hold whatever follows U's rows and
 // only reach outputs j >= R, which are not stored.  Otherwise the B operand
 // is read from the staged fragment-major U^T.  The values multiplied are the
@@ -662,10 +667,15 @@ __global__ __launch_bounds__(256) void lora_colsum_many_kernel(GradMany g) {
             for (int f = 0; f < UW / 32; ++f) cu[f] = col_frag_off<UW>(0, 0, f, lane);
             auto issue = [&](int t0, char *dst, char *udst) {
                 issue_x(t0, dst);
+                if constexpr (UWI == 0) {
+                    if (wave < U::WAVE_INSTS)
+                        buffer_to_lds_16(urs, udst + wave * 1024, uvo, (uint32_t)(t0 / kCsRows) * ustage_step);
+                } else {
 #pragma unroll
-                for (int i = 0; i < UWI; ++i)
-                    buffer_to_lds_16(urs, udst + (i * 4 + wave) * 1024, uvo,
-                                     (uint32_t)(t0 / kCsRows) * ustage_step + i * urow_step);
+                    for (int i = 0; i < UWI; ++i)
+                        buffer_to_lds_16(urs, udst + (i * 4 + wave) * 1024, uvo,
+                                         (uint32_t)(t0 / kCsRows) * ustage_step + i * urow_step);
+                }
             };
             auto stage = [&](const char *tile, const char *utile) {
 #pragma unroll
@@ -816,8 +826,7 @@ hipError_t expand(const float *U, int64_t ldu, const T *Wt, T *Y, int64_t ldy, i
 }
 
 // Token splits of the bf16 colsum: up to about 256 workgroups per product,
-// each split a multiple of 64 tokens and at least 16 stages (1024 tokens)
-// long.  A workgroup's fixed part (first stage's wait, partial store) and the
+// each split a whole number of stages and at least 1024 tokens long.  A workgroup's fixed part (first stage's wait, partial store) and the
 // partial bytes the reduce reads favour long splits: the c4 double block's 12
 // products (4096 and 512 tokens, C = 3072) in one call took 48.0 us with
 // splits of at least 4 stages (11 splits of 384 tokens at 4096), 45.2 with 8,
@@ -827,7 +836,7 @@ inline int colsum_splits(int N, int C) {
     const int tiles = (C + kCsCols - 1) / kCsCols;
     const int stages = (N + kCsRows - 1) / kCsRows;
     int sp = (256 + tiles - 1) / tiles;
-    if (sp > stages / 16) sp = stages / 16;
+    if (sp > stages / (1024 / kCsRows)) sp = stages / (1024 / kCsRows);  // splits of >= 1024 tokens
     return sp < 1 ? 1 : sp;
 }
 inline int colsum_npad(int N) { return (N + kCsRows - 1) / kCsRows * kCsRows; }
