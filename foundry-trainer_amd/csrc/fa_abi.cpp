@@ -528,6 +528,16 @@ static void fill_prologue(const fa_qk_prologue_args *a, fa::QkPrologueParams &p)
     for (int i = 0; i < FA_MAX_ROPE_AXES; ++i) p.axes[i] = i < a->n_axes ? a->axes[i] : 0;
 }
 
+// The bf16 rowdot (u = x·Aᵀ) addresses one workgroup's rows of x, up to 64,
+// and the whole [r, K] factor with 32-bit buffer offsets.
+static fa_status check_rowdot_span(const char *name, int64_t ld, int32_t rows, int32_t k, int32_t r) {
+    const int64_t span = ((int64_t)(std::min(rows, 64) - 1) * ld + k) * 2;
+    if (span >= (int64_t(1) << 32) || (int64_t)r * k * 2 >= (int64_t(1) << 32))
+        return fail(FA_ERR_UNSUPPORTED, "%s: 64 rows of stride %lld, or the rank factor, span 4 GiB or more", name,
+                    (long long)ld);
+    return FA_OK;
+}
+
 static fa_status check_lora(const fa_lora_args *a) {
     if (!a) return fail(FA_ERR_INVALID_ARG, "args is NULL");
     if (a->dtype != FA_DTYPE_BF16 && a->dtype != FA_DTYPE_F32)
@@ -546,6 +556,7 @@ static fa_status check_lora(const fa_lora_args *a) {
     if (!a->a || !aligned(a->a, 16)) return fail(FA_ERR_INVALID_ARG, "a is NULL or misaligned");
     if (!a->b || !aligned(a->b, elt)) return fail(FA_ERR_INVALID_ARG, "b is NULL or misaligned");
     if (!a->u || !aligned(a->u, 4)) return fail(FA_ERR_INVALID_ARG, "u is NULL or misaligned");
+    if (a->dtype == FA_DTYPE_BF16) FA_TRY(check_rowdot_span("x", a->ldx, a->tokens, a->in_features, a->rank));
     return FA_OK;
 }
 
@@ -709,6 +720,8 @@ fa_status fa_lora_bwd(const fa_lora_bwd_args *a, void *stream) {
     const size_t elt = a->fwd.dtype == FA_DTYPE_BF16 ? 2 : 4;
     if (!a->dy || !aligned(a->dy, 16) || a->ldy < a->fwd.out_features || (a->ldy * (int64_t)elt) % 16)
         return fail(FA_ERR_INVALID_ARG, "dy is NULL, misaligned, or ldy < out_features");
+    if (a->fwd.dtype == FA_DTYPE_BF16)
+        FA_TRY(check_rowdot_span("dy", a->ldy, a->fwd.tokens, a->fwd.out_features, a->fwd.rank));
     if (!a->da || !a->db || !aligned(a->da, 4) || !aligned(a->db, 4))
         return fail(FA_ERR_INVALID_ARG, "da/db is NULL or misaligned");
     if (a->dx && (!aligned(a->dx, elt) || a->ldx < a->fwd.in_features))
@@ -748,6 +761,7 @@ fa_status fa_lora_down(const fa_lora_down_args *a, void *stream) {
         return fail(FA_ERR_INVALID_ARG, "x is NULL, misaligned, or ldx < in_features");
     if (!a->a || !aligned(a->a, 16)) return fail(FA_ERR_INVALID_ARG, "a is NULL or not 16-byte aligned");
     FA_TRY(check_rank_view("u", a->u, a->ldu, a->rank));
+    FA_TRY(check_rowdot_span("x", a->ldx, a->tokens, a->in_features, a->rank));
     FA_TRY(init_current());
     const hipError_t e = fa::launch_lora_down_bf16(a->x, a->ldx, a->a, a->tokens, a->in_features, a->rank, a->scale,
                                                    a->u, a->ldu, static_cast<hipStream_t>(stream));

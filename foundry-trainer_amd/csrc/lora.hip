@@ -5,8 +5,9 @@
 // produce its gradients.
 //
 //   rowdot  out[n][j] = s * sum_k X[n][k] W[j][k]      (x A^T, and dy B as
-//           dy (B^T)^T): a skinny GEMM.  bf16 (lora_rowdot16_kernel): 16 rows
-//           per 8-wave workgroup on v_mfma_f32_16x16x32_bf16, each wave's
+//           dy (B^T)^T): a skinny GEMM.  bf16 (lora_rowdot16_kernel): 1, 2
+//           or 4 16-row slabs per 8-wave workgroup (chosen per call from the
+//           grid's fit to the CUs) on v_mfma_f32_16x16x32_bf16, each wave's
 //           k-steps of X and W staged in its own LDS region by DMA in
 //           row-segment lane order and read back in operand order.  f32 (the
 //           parity path): one wave per 32 rows, operands from global memory.
@@ -131,39 +132,44 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(const float *__restric
 // One k-step per stage: two k-steps per stage (twice the LDS) was no faster
 // alone and slower in the c4 step, where a workgroup's LDS decides whether it
 // can share a CU with the other stream's kernels.
-template <int NT>
+template <int NT, int MT = 1>
 struct RowdotStage {
     static constexpr int G = 1;                        // k-steps per stage
-    static constexpr int STEP = 1024 * (1 + NT);       // LDS bytes per k-step: X, then NT W tiles
+    static constexpr int STEP = 1024 * (MT + NT);      // LDS bytes per k-step: MT X slabs, then NT W tiles
     static constexpr int WAVE = G * STEP;              // one wave's stage
     static constexpr int BYTES = 8 * WAVE;             // the workgroup's stage
 };
 
-template <int NT, typename TO>
+// MT: 16-row slabs per workgroup.  Each k-step's W tiles are then read once
+// for MT slabs of X; at rank 48 the W bytes (from L2) outweigh X's three to
+// one for a single slab.
+template <int NT, typename TO, int MT = 1>
 __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restrict__ X, int64_t ldx,
                                                             const bf16 *__restrict__ W, TO *out, int64_t ldo,
                                                             int N, int K, int R, float s) {
-    using RS = RowdotStage<NT>;
+    using RS = RowdotStage<NT, MT>;
     constexpr int G = RS::G;
     // two distinct LDS objects: the compiler then tells the DMA into one
     // stage from the reads of the other
     __shared__ __align__(16) char sa[RS::BYTES], sb[RS::BYTES];
-    // the 8 partial tiles reuse sa once the k-steps are done
+    // the 8 partial tiles of one slab reuse sa once the k-steps are done
     static_assert(sizeof(float) * 8 * NT * 4 * 64 <= RS::BYTES, "partials fit in a stage");
     float (*part)[NT][4][64] = reinterpret_cast<float (*)[NT][4][64]>(sa);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, q = lane >> 4;
-    const int row0 = blockIdx.x * 16;
+    const int row0 = blockIdx.x * 16 * MT;
 
     // DMA source offsets: lane 4 r + p fetches chunk p ^ ((r / 4) % 4) of row
     // r of a 16-row, 32-column k-step (the k-step itself goes in soffset)
     const int r = lane >> 2, c = (lane & 3) ^ ((r >> 2) & 3);
-    const int xrows = min(16, N - row0);
+    const int xrows = min(16 * MT, N - row0);
     const __amdgpu_buffer_rsrc_t xrs =
         make_rsrc(X + (int64_t)row0 * ldx, (uint32_t)(((int64_t)(xrows - 1) * ldx + K) * 2));
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint32_t)((int64_t)R * K * 2));
-    const uint32_t xvo = (uint32_t)((min(r, xrows - 1) * ldx + c * 8) * 2);
+    uint32_t xvo[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xvo[mt] = (uint32_t)((min(mt * 16 + r, xrows - 1) * ldx + c * 8) * 2);
     uint32_t wvo[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) wvo[t] = (uint32_t)((min(t * 16 + r, R - 1) * (int64_t)K + c * 8) * 2);
@@ -181,30 +187,39 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int ks = wave + 8 * min(j0 + g, J - 1);
-            buffer_to_lds_16(xrs, d + g * RS::STEP, xvo, (uint32_t)ks * 64);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) buffer_to_lds_16(wrs, d + g * RS::STEP + 1024 * (1 + t), wvo[t], (uint32_t)ks * 64);
+            for (int mt = 0; mt < MT; ++mt)
+                buffer_to_lds_16(xrs, d + g * RS::STEP + 1024 * mt, xvo[mt], (uint32_t)ks * 64);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                buffer_to_lds_16(wrs, d + g * RS::STEP + 1024 * (MT + t), wvo[t], (uint32_t)ks * 64);
         }
     };
     const u32x4 zero = {0, 0, 0, 0};
-    f32x4 acc[NT];
+    f32x4 acc[MT][NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto consume = [&](int j0, const char *src) {
         const char *d = src + wave * RS::WAVE;
 #pragma unroll
         for (int g = 0; g < G; ++g)
             if (j0 + g < J) {
-                u32x4 a = ld_lds_16(d + g * RS::STEP, rd);
-                if (half && wave + 8 * (j0 + g) == nks - 1 && q >= 2) a = zero;  // columns past K
+                u32x4 wf[NT];
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    acc[t] = mfma_16x16x32(as_bf16x8(a), as_bf16x8(ld_lds_16(d + g * RS::STEP + 1024 * (1 + t), rd)),
-                                           acc[t]);
+                for (int t = 0; t < NT; ++t) wf[t] = ld_lds_16(d + g * RS::STEP + 1024 * (MT + t), rd);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    u32x4 a = ld_lds_16(d + g * RS::STEP + 1024 * mt, rd);
+                    if (half && wave + 8 * (j0 + g) == nks - 1 && q >= 2) a = zero;  // columns past K
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) acc[mt][t] = mfma_16x16x32(as_bf16x8(a), as_bf16x8(wf[t]), acc[mt][t]);
+                }
             }
     };
     if (J > 0) {
-        constexpr int VM = G * (1 + NT);  // loads per stage
+        constexpr int VM = G * (MT + NT);  // loads per stage
         issue(0, sa);
         issue(G, sb);
         // No exit between the halves: with one, the compiler's wait-count
@@ -222,21 +237,26 @@ __global__ __launch_bounds__(512) void lora_rowdot16_kernel(const bf16 *__restri
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stages issued past J land before LDS is reused
     }
-    __syncthreads();  // every wave is done with sa
+    // one slab at a time through sa: the 8 waves' partial tiles, summed in a
+    // fixed order
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int mt = 0; mt < MT; ++mt) {
+        __syncthreads();  // every wave is done with sa (its stage, or the previous slab's partials)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) part[wave][t][e][lane] = acc[t][e];
-    __syncthreads();
-    if (wave < NT) {
-        const int t = wave, col = t * 16 + m;
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float v = part[0][t][e][lane];
+            for (int e = 0; e < 4; ++e) part[wave][t][e][lane] = acc[mt][t][e];
+        __syncthreads();
+        if (wave < NT) {
+            const int t = wave, col = t * 16 + m;
 #pragma unroll
-            for (int w = 1; w < 8; ++w) v += part[w][t][e][lane];
-            const int row = row0 + 4 * q + e;
-            if (row < N && col < R) out[(int64_t)row * ldo + col] = (TO)(v * s);
+            for (int e = 0; e < 4; ++e) {
+                float v = part[0][t][e][lane];
+#pragma unroll
+                for (int w = 1; w < 8; ++w) v += part[w][t][e][lane];
+                const int row = row0 + mt * 16 + 4 * q + e;
+                if (row < N && col < R) out[(int64_t)row * ldo + col] = (TO)(v * s);
+            }
         }
     }
 }
@@ -771,15 +791,45 @@ __global__ void lora_transpose_kernel(const T *__restrict__ src, T *dst, int R, 
     dst[(int64_t)c * R + r] = src[e];
 }
 
+// 16-row slabs per rowdot workgroup, 1, 2 or 4.  A CU's LDS-DMA rate bounds
+// these kernels, so the time goes as the most bytes any one CU stages:
+// (workgroups on the busiest CU) x (MT X slabs + NT W tiles) per k-step.  More
+// slabs per workgroup share each W tile among more rows but leave CUs idle
+// once the grid is smaller than the chip (4096 rows: 256 workgroups of one
+// slab fill 256 CUs once; 4608 rows: 288 of one slab put two on 32 CUs, 144
+// of two slabs put at most one on any).  Which slab count runs changes no
+// bits: each 16-row tile's k-steps are the same, in the same order.
+int rowdot_slabs(int N, int NT) {
+    const int cus = device_cu_count();
+    int best = 1;
+    int64_t best_cost = -1;
+    for (int mt : {1, 2, 4}) {
+        const int64_t wgs = (N + 16 * mt - 1) / (16 * mt);
+        const int64_t cost = (wgs + cus - 1) / cus * (mt + NT);
+        if (best_cost < 0 || cost < best_cost) best = mt, best_cost = cost;
+    }
+    return best;
+}
+
 template <typename T>
 hipError_t rowdot(const T *X, int64_t ldx, const T *W, float *out, int64_t ldo, int N, int K,
                   int R, float s, hipStream_t st) {
     if constexpr (sizeof(T) == 2) {
-        const dim3 grid((unsigned)((N + 15) / 16)), block(512);
-        if (R <= 16)
-            hipLaunchKernelGGL((lora_rowdot16_kernel<1, float>), grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
-        else
-            hipLaunchKernelGGL((lora_rowdot16_kernel<2, float>), grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
+        auto go = [&](auto mtc) {
+            constexpr int MT = decltype(mtc)::value;
+            const dim3 grid((unsigned)((N + 16 * MT - 1) / (16 * MT))), block(512);
+            if (R <= 16)
+                hipLaunchKernelGGL((lora_rowdot16_kernel<1, float, MT>), grid, block, 0, st, X, ldx, W, out, ldo, N, K,
+                                   R, s);
+            else
+                hipLaunchKernelGGL((lora_rowdot16_kernel<2, float, MT>), grid, block, 0, st, X, ldx, W, out, ldo, N, K,
+                                   R, s);
+        };
+        switch (rowdot_slabs(N, (R + 15) / 16)) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        default: go(std::integral_constant<int, 4>{}); break;
+        }
     } else {
         const dim3 grid((N + 127) / 128), block(256);
         hipLaunchKernelGGL(lora_rowdot_kernel<T>, grid, block, 0, st, X, ldx, W, out, ldo, N, K, R, s);
@@ -951,19 +1001,27 @@ hipError_t launch_lora_bwd(const LoraParams &p, int dtype, hipStream_t s) {
 // ---- bf16 pieces for adapters folded into the base GEMMs -----------------
 hipError_t launch_lora_down_bf16(const void *x, int64_t ldx, const void *a, int N, int K, int R, float scale,
                                  void *u, int64_t ldu, hipStream_t st) {
-    const dim3 grid((unsigned)((N + 15) / 16)), block(512);
     const bf16 *X = static_cast<const bf16 *>(x), *A = static_cast<const bf16 *>(a);
     bf16 *U = static_cast<bf16 *>(u);
-    // R <= 64: up to four 16-column tiles per workgroup (a stack of adapters
-    // that share x, e.g. q/k/v, runs as one product)
-    if (R <= 16)
-        hipLaunchKernelGGL((lora_rowdot16_kernel<1, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
-    else if (R <= 32)
-        hipLaunchKernelGGL((lora_rowdot16_kernel<2, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
-    else if (R <= 48)
-        hipLaunchKernelGGL((lora_rowdot16_kernel<3, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
-    else
-        hipLaunchKernelGGL((lora_rowdot16_kernel<4, bf16>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+    auto go = [&](auto mtc) {
+        constexpr int MT = decltype(mtc)::value;
+        const dim3 grid((unsigned)((N + 16 * MT - 1) / (16 * MT))), block(512);
+        // R <= 64: up to four 16-column tiles per workgroup (a stack of adapters
+        // that share x, e.g. q/k/v, runs as one product)
+        if (R <= 16)
+            hipLaunchKernelGGL((lora_rowdot16_kernel<1, bf16, MT>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+        else if (R <= 32)
+            hipLaunchKernelGGL((lora_rowdot16_kernel<2, bf16, MT>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+        else if (R <= 48)
+            hipLaunchKernelGGL((lora_rowdot16_kernel<3, bf16, MT>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+        else
+            hipLaunchKernelGGL((lora_rowdot16_kernel<4, bf16, MT>), grid, block, 0, st, X, ldx, A, U, ldu, N, K, R, scale);
+    };
+    switch (rowdot_slabs(N, (R + 15) / 16)) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    default: go(std::integral_constant<int, 4>{}); break;
+    }
     return hipGetLastError();
 }
 

@@ -409,6 +409,15 @@ def test_lora_pieces_validate_before_device_work():
         bad = _abi.LoraDownArgs.from_buffer_copy(dn)
         setattr(bad, field, val)
         assert L.fa_lora_down(ctypes.byref(bad), None) == code, field
+    # a workgroup addresses up to 64 rows of x with 32-bit offsets: 64 rows
+    # spanning 4 GiB are refused, 16 rows of the same stride are not
+    bad = _abi.LoraDownArgs.from_buffer_copy(dn)
+    bad.ldx = 1 << 26
+    assert L.fa_lora_down(ctypes.byref(bad), None) == _abi.FA_ERR_UNSUPPORTED
+    assert b"4 GiB" in L.fa_last_error()
+    if not gpu_available():
+        bad.tokens = 16
+        assert L.fa_lora_down(ctypes.byref(bad), None) == ok_dev
     up = _abi.LoraUpArgs(dtype=0, tokens=64, out_features=3072, rank=16, scale=1.0, u=_FAKE, ldu=3136, b=_FAKE,
                          y=_FAKE, ldy=3136)
     if not gpu_available():

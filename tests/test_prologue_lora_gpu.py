@@ -249,6 +249,36 @@ def test_lora_down_k_tails(K, r):
     assert max_abs(got, want) <= 2 ** -7 * peak + 1e-6 and rel_l2(got, want) <= 4e-3, (K, r)
 
 
+@pytest.mark.parametrize("N", [4096, 4613, 9219])
+@pytest.mark.parametrize("r", [16, 48])
+def test_lora_down_slab_counts(N, r):
+    """Token counts whose rowdot launches take one, two and four 16-row slabs
+    per workgroup on a 256-CU device (4096: 256 workgroups of one slab; 4613:
+    two slabs, the last workgroup ragged; 9219: four slabs, three of the last
+    workgroup's slabs wholly past N).  At rank 16 the f32-output rowdot of
+    fa_lora_fwd (its u) goes through the same choice.  Against the f64 product
+    of the same bf16 values."""
+    from foundry_attn.ops import lora_down, lora_fwd
+    rng = np.random.default_rng(900 + N + r)
+    K, s = 208, 0.5
+    rnd = oracle.bf16_round
+    x = rnd(rng.standard_normal((N, K)).astype(np.float32))
+    A = rnd(rng.standard_normal((r, K)).astype(np.float32) / np.sqrt(K))
+    bf = torch.bfloat16
+    xe = torch.full((N, K + 48), 1e4, dtype=bf, device="cuda")
+    xe[:, :K] = dev(x, bf)
+    u = lora_down(xe[:, :K], dev(A, bf), s, out=torch.empty((N, r), dtype=bf, device="cuda"))
+    want = x.astype(np.float64) @ A.T.astype(np.float64)
+    got = host(u)
+    assert max_abs(got, s * want) <= 2 ** -7 * np.abs(s * want).max() + 1e-6 and rel_l2(got, s * want) <= 4e-3
+    if r <= 32:
+        M = 32
+        B = rnd(0.05 * rng.standard_normal((M, r)).astype(np.float32))
+        y = torch.zeros((N, M), dtype=bf, device="cuda")
+        uf = lora_fwd(xe[:, :K], dev(A, bf), dev(B, bf), y, s)
+        np.testing.assert_allclose(host(uf), want, rtol=1e-4, atol=1e-3)
+
+
 @pytest.mark.parametrize("r", [1, 16, 17, 48, 64])
 @pytest.mark.parametrize("y_aligned", [True, False])
 def test_lora_up_rank_steps_and_y_alignment(r, y_aligned):
