@@ -392,7 +392,7 @@ class DoubleBlockLoRA:
                  lora_scale: float = 1.0, eps: float = 1e-6, overlap_streams: bool = True,
                  tuned_gemms: bool = True, batch_qkv_adapters: bool = True, mlp: str = "gelu",
                  positions: Optional[np.ndarray] = None, dx_weights_t: bool = True,
-                 fold_qkv_adapters: bool = True, fold_mlp_gate: bool = True, fused_gelu: bool = False):
+                 fold_qkv_adapters: bool = True, fold_mlp_gate: bool = True, fused_gelu=False):
         """positions: [S, n_axes] RoPE position ids of the joint sequence (txt
         rows first); None gives txt (l, 0, 0), img (0, r, c).
 
@@ -428,7 +428,8 @@ class DoubleBlockLoRA:
         (fa_gemm_bf16) with the GELU and GELU-gradient epilogues, in place of
         the library GEMM followed by a separate GELU / GELU-backward pass.
         The backward's operand is W2's (or W2g's) transposed copy, so it also
-        needs dx_weights_t."""
+        needs dx_weights_t.  True fuses both streams; an iterable of stream
+        names ("img", "txt") fuses only those."""
         if mlp not in ("gelu", "swiglu"):
             raise ValueError(f"mlp must be 'gelu' or 'swiglu', not {mlp!r}")
         self.w = weights
@@ -467,7 +468,7 @@ class DoubleBlockLoRA:
         self._wt = {name: {} for name in STREAMS} if dx_weights_t else None
         self._fold_g2 = fold_mlp_gate and all(weights[name].b2 is None for name in STREAMS)
         self._w2g, self._w2g_t = {}, {}
-        self._fused_gelu = fused_gelu
+        self._fused_gelu = ({"img", "txt"} if fused_gelu is True else set(fused_gelu) if fused_gelu else set())
         if tuned_gemms and self.dtype == torch.bfloat16:
             gemm_tuning.enable()
         ranks = {int(a.shape[0]) for w in weights.values() for a in w.lora_a.values()}
@@ -580,7 +581,7 @@ class DoubleBlockLoRA:
         """Whether stream `name`'s MLP runs W1 (forward) or W2's dX product
         (backward) as fa_gemm_bf16 with the GELU epilogue."""
         w = self.w[name]
-        ok = (self._fused_gelu and self.mlp == "gelu" and self.dtype == torch.bfloat16 and w.b1 is None
+        ok = (name in self._fused_gelu and self.mlp == "gelu" and self.dtype == torch.bfloat16 and w.b1 is None
               and self.rows[name] % 256 == 0 and w.w1.shape[0] % 256 == 0 and self.C % 64 == 0)
         return ok and (not backward or self._wt is not None)
 
