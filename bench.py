@@ -513,7 +513,8 @@ def attention_bench(torch, fa, cfg, steps: int, warmup: int, settle_s: float):
     q, k, v, do, keep = make_inputs(cfg, torch, fa)
     lse = torch.empty((cfg.batch, cfg.heads, cfg.seq), dtype=torch.float32, device="cuda")
     o = torch.empty_like(q)
-    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    # the full backward workspace: dQ reads the stored dS where that path applies
+    ws = torch.empty(max(fa.attn_workspace_bytes(q)[1], 256), dtype=torch.uint8, device="cuda")
     stream = torch.cuda.current_stream()
     grads = (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q))
     ph = [(fa._abi.FA_BWD_PREPASS, None), (fa._abi.FA_BWD_DKDV, None), (fa._abi.FA_BWD_DQ, None)]

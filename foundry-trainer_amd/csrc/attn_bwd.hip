@@ -36,6 +36,11 @@
 namespace fa {
 namespace {
 
+// Cache policy of the dS stores and loads: non-temporal (each byte is
+// written once and read once; measured 2-4% off the backward at c2 and c5
+// against the default policy).
+constexpr int kDsCachePolicy = 2;
+
 // ---------------------------------------------------------------------------
 // 1. delta = rowsum(dO * O) in f32, written [B,H,S]; also lse2 = LSE*log2(e)
 //    (+inf for a fully masked row, so P = exp2(s*c - lse2) = 0 there)
@@ -103,8 +108,16 @@ struct DkvTile {
 
 // SPLIT: the workgroup streams only its partition's query blocks and leaves
 // unscaled f32 partial dK, dV (the reduce pass applies the mask and scale).
-template <int D, int NW, bool SPLIT>
+// DS: also store every (key, query) element of dS for the dQ product (p.ds,
+// unsplit only; zero for an excluded key or a key past S), in 1 KiB blocks
+// of 32 keys (a wave's) x 16 queries: element (key, q) of block (key / 32,
+// q / 16) at ((key % 32) + 32 * (q % 16 / 8)) * 16 + (q % 8) * 2, blocks
+// [key / 32][q / 16] with ds_ld / 16 blocks per row.  One permlane32 swap per
+// word puts 8 consecutive queries of the lane's key in each lane, so a wave
+// stores a whole block with one 16-byte store per lane.
+template <int D, int NW, bool SPLIT, bool DS = false>
 __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
+    static_assert(!(SPLIT && DS), "dS is stored by the unsplit kernel only");
     using F = DkvTile<D, NW>;
     constexpr int kKT = F::KT;
     using T = typename F::T;
@@ -140,6 +153,13 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
     const int tkey = kt * kKT + tid;
     const uint32_t tkeep =
         test_keys && tid < kKT ? (uint32_t)p.keep[(int64_t)b * S + min(tkey, S - 1)] & (tkey < S ? 0xffu : 0u) : 0u;
+    // dS^T rows of this head; rows past S (keys of the last tile) lie past
+    // the descriptor's range and are dropped
+    const int64_t ds_head = (int64_t)((S + 31) / 32) * 32 * p.ds_ld;  // elements per head
+    const __amdgpu_buffer_rsrc_t dsrs = make_rsrc(DS ? static_cast<bf16 *>(p.ds) + bh * ds_head : nullptr,
+                                                  DS ? (uint32_t)(ds_head * 2) : 0u);
+    const uint32_t ds_row = (uint32_t)(kt * (kKT / 32) + wave) * (uint32_t)(p.ds_ld / 16);  // this wave's first block
+    const bool dkeep = !DS || (kj < S && (!p.keep || p.keep[(int64_t)b * S + kj]));
 
     // K and V rows of this lane's key (B operands): features kd*16 + g*8 .. +8
     bf16x8 kf[D / 16], vf[D / 16];
@@ -198,9 +218,27 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
         if (!live) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stage lands before the exit
     }
     const int qend = live ? qb1 : qb0;
+    if constexpr (DS) {
+        // a workgroup streaming no queries still leaves its keys' dS blocks
+        // (zero) for the dQ product
+        if (!live) {
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            for (int blk = 0; blk < p.ds_ld / 16; ++blk) {
+                __builtin_amdgcn_raw_buffer_store_b128(z, dsrs, (uint32_t)lane * 16, (ds_row + (uint32_t)blk) * 1024,
+                                                       kDsCachePolicy);
+                asm volatile("s_nop 1" ::"v"(z));  // see the stores below
+            }
+        }
+    }
     auto stage = [&](auto par, int qb) {
         constexpr int P = decltype(par)::value;  // (qb - qb0) % 2
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // Vector memory operations complete in issue order, so with DS the
+        // stage's DMA (issued before the previous stage's 4 dS stores) has
+        // landed once at most 4 operations are outstanding.
+        if (DS && qb != qb0)
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (qb + 1 < qb1) issue(qb + 1, P ^ 1);
         const char *st = P ? stage1 : stage0;
@@ -240,6 +278,27 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
                 dw[1] = pack_bf16x2(dsv[2], dsv[3]);
                 set_half(pf[grp >> 1], grp & 1, pw);
                 set_half(df[grp >> 1], grp & 1, dw);
+            }
+            if constexpr (DS) {
+                // df[j]: queries 16j + {4g .. 4g+3} (words 0, 1) and 16j + 8 + {4g ..} (words 2, 3);
+                // after the swap lane (n, g) holds queries 16j + 8g .. +8 of key n
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const u32x4 u = as_u32x4(df[j]);
+                    const auto r0 = __builtin_amdgcn_permlane32_swap(u[0], u[2], false, false);
+                    const auto r1 = __builtin_amdgcn_permlane32_swap(u[1], u[3], false, false);
+                    const u32x4 w = dkeep ? u32x4{r0[0], r1[0], r0[1], r1[1]} : u32x4{0u, 0u, 0u, 0u};
+                    __builtin_amdgcn_raw_buffer_store_b128(w, dsrs, (uint32_t)lane * 16,
+                                                           (ds_row + (uint32_t)(qb * 4 + sub * 2 + j)) * 1024,
+                                                           kDsCachePolicy);
+                    // A VALU write to a data VGPR of a 16-byte store in the
+                    // next cycle corrupted the stored first dword (measured:
+                    // every dword 0 of the blocks, nondeterministically; the
+                    // compiler emitted the write right after the store).
+                    // Holding the data live across wait states keeps the
+                    // write back.
+                    asm volatile("s_nop 1" ::"v"(w));
+                }
             }
             // dV += P^T dO, dK += dS^T Q  (contraction over the 32 queries)
 #pragma unroll
@@ -608,10 +667,146 @@ __device__ __forceinline__ void dq_block(const AttnBwdParams &p, int work) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// 3'. dQ from the stored dS (p.ds): dQ^T = K^T dS^T.  A workgroup of 8 waves
+//     owns 256 queries of one (b, h) and streams 64-key blocks: the K tile
+//     and the dS blocks of the 64 keys x 256 queries (two runs of 16
+//     contiguous 1 KiB blocks) go HBM -> LDS by DMA, three blocks deep.  Both
+//     MFMA operands are transpose reads: K^T column fragments of the
+//     row-major K tile, and dS^T fragments gathered from the blocks (the
+//     transpose read takes any 8-byte address per lane: lane j of a 16-lane
+//     group reads key +j/4, queries 4(j%4) .. +3, and receives query j's four
+//     keys).  Keys past S read as zero in both.  The same products in the
+//     same key order as the recomputing dQ kernel's dQ^T MFMAs.
+// ---------------------------------------------------------------------------
+constexpr int kDsKB = 64;  // keys per block
+
+template <int D>
+struct DqDsTile {
+    using KT = LdsTile<D, kDsKB>;  // K: 64 keys x D features
+    static constexpr int NW = 8;
+    static constexpr int QT = 256;                     // queries per workgroup
+    static constexpr int SBYTES = kDsKB * QT * 2;      // dS of a block: 32 KiB
+    static constexpr int KWI = KT::WAVE_INSTS / NW;    // K wave-instructions per wave
+    static constexpr int SWI = SBYTES / 1024 / NW;     // dS wave-instructions per wave
+    static constexpr int LOADS = KWI + SWI;            // per wave per block
+    static_assert(KWI >= 1 && KWI * NW == KT::WAVE_INSTS, "K tile split over waves");
+};
+
+template <int D>
+__global__ __launch_bounds__(512) void attn_bwd_dq_ds_kernel(AttnBwdParams p) {
+    using F = DqDsTile<D>;
+    using KT = typename F::KT;
+    constexpr int NW = F::NW;
+    const int work = xcd_remap(blockIdx.x, gridDim.x);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int S = p.S, H = p.H;
+    const int nq = (S + F::QT - 1) / F::QT;
+    const int qt = work % nq, bh = work / nq;
+    const int h = bh % H, b = bh / H;
+    const int nkb = (S + kDsKB - 1) / kDsKB;
+
+    const bf16 *kbase = static_cast<const bf16 *>(p.k) + b * p.k_sb + h * p.k_sh;
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, (uint32_t)(((S - 1) * p.k_ss + D) * 2));
+    const uint32_t kvo = tile_src_off<D>(wave, lane, p.k_ss);
+    const uint32_t ki_step = tile_inst_row_step<D, NW>(p.k_ss);
+    const uint32_t kstep = (uint32_t)(kDsKB * p.k_ss * 2);
+    // dS blocks of this head: [S / 32 key tiles][ds_ld / 16 query blocks] x 1 KiB
+    const int64_t ds_head = (int64_t)((S + 31) / 32) * 32 * p.ds_ld;
+    const __amdgpu_buffer_rsrc_t srs =
+        make_rsrc(static_cast<const bf16 *>(p.ds) + bh * ds_head, (uint32_t)(ds_head * 2));
+    const uint32_t row_blocks = (uint32_t)(p.ds_ld / 16);
+
+    // distinct LDS objects per buffer: the compiler tells the DMA into one
+    // from the reads of another
+    __shared__ __align__(16) char k0[KT::BYTES], k1[KT::BYTES], k2[KT::BYTES];
+    __shared__ __align__(16) char s0[F::SBYTES], s1[F::SBYTES], s2[F::SBYTES];
+    auto issue = [&](int kb, char *kd, char *sd) {
+#pragma unroll
+        for (int i = 0; i < F::KWI; ++i)
+            buffer_to_lds_16(krs, kd + (i * NW + wave) * 1024, kvo, kb * kstep + i * ki_step);
+        // LDS block c = key tile c / 16 of the two, query block c % 16 of the 16
+#pragma unroll
+        for (int i = 0; i < F::SWI; ++i) {
+            const int c = i * NW + wave;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                srs, (__attribute__((address_space(3))) void *)(sd + c * 1024), 16, (uint32_t)lane * 16,
+                ((uint32_t)(2 * kb + c / 16) * row_blocks + (uint32_t)(qt * 16 + c % 16)) * 1024, 0, kDsCachePolicy);
+        }
+    };
+
+    // A operand K^T: column tile dt of the K tile.  B operand dS^T for this
+    // wave's 32 queries: lane j of 16-lane group G (g = G / 2, query half
+    // G % 2) reads key 4g + j/4 (+8 for the second half, +16 per k-step
+    // within a key tile), queries wave*32 + 16(G % 2) + 4(j % 4) .. +3.
+    uint32_t ko0[D / 32], ko1[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        ko0[dt] = col_frag_off<D>(0, 0, dt, lane);
+        ko1[dt] = col_frag_off<D>(0, 1, dt, lane);
+    }
+    const int jj = lane & 15, gg = lane >> 5, dh = (lane >> 4) & 1;
+    const uint32_t so = (uint32_t)((wave * 2 + dh) * 1024 + (4 * gg + (jj >> 2) + 32 * ((jj & 3) >> 1)) * 16 +
+                                   8 * (jj & 1));
+
+    f32x16 dq[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dq[dt][r] = 0.f;
+
+    // block kb in (kt, st): wait for it (block kb+1 may stay in flight), then
+    // refill the buffers block kb-1 used with block kb+2 (unconditionally:
+    // past the last block the tiles read as zero)
+    auto stage = [&](int kb, const char *kt, const char *st, char *kn, char *sn) {
+        barrier_keep_dma<F::LOADS>();
+        issue(kb + 2, kn, sn);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < kDsKB / 16; ++ks) {
+            // key tile ks / 2 (16 KiB apart), keys 16 (ks % 2) + 8 half
+            const uint32_t o = so + (ks >> 1) * 16384 + (ks & 1) * 256;
+            const bf16x8 bfr = lds_read_col_frag(st, o, o + 128);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+                dq[dt] = mfma_32x32x16(
+                    lds_read_col_frag(kt, ko0[dt] + ks * 16 * KT::ROWB, ko1[dt] + ks * 16 * KT::ROWB), bfr, dq[dt]);
+        }
+    };
+    issue(0, k0, s0);
+    issue(1, k1, s1);
+    // whole groups of three blocks (the padding blocks read zeros), so every
+    // buffer is a compile-time LDS object
+    for (int kb = 0; kb < nkb; kb += 3) {
+        stage(kb, k0, s0, k2, s2);
+        stage(kb + 1, k1, s1, k0, s0);
+        stage(kb + 2, k2, s2, k1, s1);
+    }
+    // the prefetches past the last block are still writing LDS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const int qi = qt * F::QT + wave * 32 + n;
+    if (qi < S) {
+        bf16 *row = static_cast<bf16 *>(p.dq) + b * p.dq_sb + h * p.dq_sh + qi * p.dq_ss;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int d = dt * 32 + grp * 8 + g * 4;
+                u32x2 w;
+                w[0] = pack_bf16x2(dq[dt][grp * 4 + 0] * p.scale, dq[dt][grp * 4 + 1] * p.scale);
+                w[1] = pack_bf16x2(dq[dt][grp * 4 + 2] * p.scale, dq[dt][grp * 4 + 3] * p.scale);
+                *reinterpret_cast<u32x2 *>(row + d) = w;
+            }
+    }
+}
+
 // 2 waves per SIMD (<= 256 VGPRs) for either workgroup size.
-template <int D, int NW, bool SPLIT>
+template <int D, int NW, bool SPLIT, bool DS = false>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dkdv_bf16_kernel(AttnBwdParams p) {
-    dkdv_block<D, NW, SPLIT>(p, xcd_remap(blockIdx.x, gridDim.x));
+    dkdv_block<D, NW, SPLIT, DS>(p, xcd_remap(blockIdx.x, gridDim.x));
 }
 
 template <int D, bool KEEP, int NW, bool DELTA, bool SPLIT>
@@ -879,8 +1074,41 @@ hipError_t launch_attn_bwd_split(const AttnBwdParams &p, int D, int phase, hipSt
     return phase == 0 ? launch_reduce(p, D, 0, 3, s) : launch_reduce(p, D, 1, 2, s);
 }
 
+// Unsplit backward through the stored dS^T (p.ds): pre-pass, dK/dV storing
+// dS^T, then dQ from it -- in this order (dQ reads what dK/dV stored).
+hipError_t launch_attn_bwd_ds(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
+    hipError_t e = hipSuccess;
+    if (phase == 0 || phase == 1) {
+        e = D == 128 ? launch_delta<bf16, 128>(p, s) : launch_delta<bf16, 64>(p, s);
+        if (e != hipSuccess) return e;
+    }
+    if (phase == 0 || phase == 2) {
+        const int nw = attn_waves(p.B, p.H, p.S);
+        const dim3 grid(p.B * p.H * ((p.S + nw * 32 - 1) / (nw * 32))), block(nw * 64);
+        if (D == 128 && nw == 8)
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 8, false, true>), grid, block, 0, s, p);
+        else if (D == 128)
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 4, false, true>), grid, block, 0, s, p);
+        else if (nw == 8)
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 8, false, true>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 4, false, true>), grid, block, 0, s, p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (phase == 0 || phase == 3) {
+        const dim3 grid(p.B * p.H * ((p.S + DqDsTile<128>::QT - 1) / DqDsTile<128>::QT)), block(512);
+        if (D == 128)
+            hipLaunchKernelGGL(attn_bwd_dq_ds_kernel<128>, grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dq_ds_kernel<64>, grid, block, 0, s, p);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
 hipError_t launch_attn_bwd_bf16(const AttnBwdParams &p, int D, int phase, hipStream_t s) {
     if (p.split > 1) return launch_attn_bwd_split(p, D, phase, s);
+    if (p.ds) return launch_attn_bwd_ds(p, D, phase, s);
     // workgroup shape as for the forward (attn_waves); dQ at D = 64 streams
     // 4 KiB units, too small to split over 8 waves.
     const int nw = attn_waves(p.B, p.H, p.S);

@@ -180,11 +180,31 @@ int split_for(int32_t dtype, int32_t B, int32_t S, int32_t H) {
 }
 
 // backward workspace: delta [B,H,S] f32, lse2 [B,H,S] f32, then for a split
-// call the f32 partials of dQ, dK and dV ([split][B,H,S][D] each)
-size_t bwd_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D) {
+// call the f32 partials of dQ, dK and dV ([split][B,H,S][D] each).  This much
+// runs the backward that recomputes S and dP in the dQ kernel.
+size_t bwd_min_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D) {
     const int split = split_for(dtype, B, S, H);
     return 2 * round256((size_t)B * H * S * sizeof(float)) +
            3 * round256(fa::attn_split_elems(B, H, S, D, split) * sizeof(float));
+}
+
+// dS after that, for the backward whose dQ reads the dK/dV kernel's dS
+// (bf16, unsplit, 8-wave grids): per (b, h) S rounded up to 32 keys x ds_ld
+// queries bf16 (S rounded up to 256), in 1 KiB blocks of 32 keys x 16
+// queries.  0 where that path does not apply: f32, split calls, 4-wave grids
+// (there the 4-wave dK/dV kernel's stores cost what dQ saves: c3 431 against
+// 450 us), or a head's blocks spanning 4 GiB (the kernels' buffer offsets
+// are 32-bit).
+int ds_ld_for(int32_t S) { return (S + 255) / 256 * 256; }
+size_t bwd_ds_bytes(int32_t dtype, int32_t B, int32_t S, int32_t H) {
+    if (dtype != FA_DTYPE_BF16 || split_for(dtype, B, S, H) > 1 || fa::attn_waves(B, H, S) != 8) return 0;
+    const int64_t head = (int64_t)(S + 31) / 32 * 32 * ds_ld_for(S) * 2;
+    if (head >= (int64_t(1) << 32)) return 0;
+    return round256((size_t)B * H * head);
+}
+
+size_t bwd_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D) {
+    return bwd_min_workspace(dtype, B, S, H, D) + bwd_ds_bytes(dtype, B, S, H);
 }
 
 // forward workspace of a split call: O partials [split][B,H,S][D] f32, then
@@ -287,6 +307,11 @@ size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *a) {
     return bwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
 }
 
+size_t fa_attn_bwd_min_workspace_size(const fa_attn_bwd_args *a) {
+    if (!a || a->batch < 1 || a->seq < 1 || a->heads < 1 || (a->head_dim != 64 && a->head_dim != 128)) return 0;
+    return bwd_min_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+}
+
 fa_status fa_attn_bwd(const fa_attn_bwd_args *a, void *stream) {
     return fa_attn_bwd_phase(a, FA_BWD_ALL, stream);
 }
@@ -344,7 +369,8 @@ hipError_t fork_for_current(BwdFork **out) {
 // waits for dQ, so everything the caller queues on s afterwards sees all
 // three results (and may reuse the workspace).
 hipError_t launch_bwd_forked(const fa::AttnBwdParams &p, int D, hipStream_t s) {
-    if (fa::attn_waves(p.B, p.H, p.S) == 8) return fa::launch_attn_bwd_bf16(p, D, FA_BWD_ALL, s);
+    // through the stored dS, dQ follows dK/dV
+    if (p.ds || fa::attn_waves(p.B, p.H, p.S) == 8) return fa::launch_attn_bwd_bf16(p, D, FA_BWD_ALL, s);
     BwdFork *f = nullptr;
     if (fork_for_current(&f) != hipSuccess) return fa::launch_attn_bwd_bf16(p, D, FA_BWD_ALL, s);
     hipError_t e = fa::launch_attn_bwd_bf16(p, D, FA_BWD_PREPASS, s);
@@ -380,8 +406,9 @@ fa_status check_bwd_args(const fa_attn_bwd_args *a) {
 }
 
 // Kernel parameters of a validated backward call whose scratch starts at ws
-// (delta rows, lse2 rows, then, for split > 1, the three partial arrays).
-void fill_bwd_params(const fa_attn_bwd_args *a, char *ws, int split, fa::AttnBwdParams &p) {
+// (delta rows, lse2 rows, then, for split > 1, the three partial arrays, and
+// with ds the dS^T rows: the caller passed the full workspace).
+void fill_bwd_params(const fa_attn_bwd_args *a, char *ws, int split, bool ds, fa::AttnBwdParams &p) {
     p = fa::AttnBwdParams{};
     const size_t rows = round256((size_t)a->batch * a->heads * a->seq * sizeof(float));
     p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.dout = a->dout; p.lse = a->lse;
@@ -408,6 +435,10 @@ void fill_bwd_params(const fa_attn_bwd_args *a, char *ws, int split, fa::AttnBwd
         p.part_dk = reinterpret_cast<float *>(base + part);
         p.part_dv = reinterpret_cast<float *>(base + 2 * part);
     }
+    if (ds) {
+        p.ds = ws + bwd_min_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+        p.ds_ld = ds_ld_for(a->seq);
+    }
 }
 }  // namespace
 
@@ -418,7 +449,8 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stre
     if (phase < FA_BWD_ALL || phase > FA_BWD_DQ)
         return fail(FA_ERR_INVALID_ARG, "unknown backward phase %d", phase);
     FA_TRY(check_bwd_args(a));
-    const size_t need = bwd_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+    const size_t need = bwd_min_workspace(a->dtype, a->batch, a->seq, a->heads, a->head_dim);
+    const size_t ds = bwd_ds_bytes(a->dtype, a->batch, a->seq, a->heads);
     if (!a->workspace || !aligned(a->workspace, 256))
         return fail(FA_ERR_INVALID_ARG, "workspace is NULL or not 256-byte aligned");
     if (a->workspace_bytes < need)
@@ -427,7 +459,8 @@ fa_status fa_attn_bwd_phase(const fa_attn_bwd_args *a, int32_t phase, void *stre
     FA_TRY(init_current());
 
     fa::AttnBwdParams p;
-    fill_bwd_params(a, static_cast<char *>(a->workspace), split_for(a->dtype, a->batch, a->seq, a->heads), p);
+    fill_bwd_params(a, static_cast<char *>(a->workspace), split_for(a->dtype, a->batch, a->seq, a->heads),
+                    ds > 0 && a->workspace_bytes >= need + ds, p);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t e = a->dtype != FA_DTYPE_BF16 ? fa::launch_attn_bwd_f32(p, a->head_dim, phase, s)
                          : phase == FA_BWD_ALL     ? launch_bwd_forked(p, a->head_dim, s)
@@ -455,7 +488,7 @@ fa_status fa_attn_bwd_noalloc(const fa_attn_bwd_args *a, void *stream) {
     // never split (the split partials would not fit), every launch in order on
     // the caller's stream (no side stream to create)
     fa::AttnBwdParams p;
-    fill_bwd_params(a, ws, 1, p);
+    fill_bwd_params(a, ws, 1, false, p);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const hipError_t e = a->dtype != FA_DTYPE_BF16 ? fa::launch_attn_bwd_f32(p, a->head_dim, FA_BWD_ALL, s)
                                                    : fa::launch_attn_bwd_bf16(p, a->head_dim, FA_BWD_ALL, s);

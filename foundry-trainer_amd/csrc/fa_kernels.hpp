@@ -48,6 +48,12 @@ struct AttnBwdParams {
     // ([split][B*H*S][D] per gradient) here and a reduce pass writes dq, dk, dv.
     int split;
     float *part_dq, *part_dk, *part_dv;
+    // dS through the workspace (ds != nullptr, unsplit bf16 only): dK/dV also
+    // stores the unscaled bf16 dS^T = (P * (dP - delta))^T of every (key,
+    // query) as [B*H][S keys][ds_ld queries], and dQ = scale * dS K is a
+    // streaming product over it instead of recomputing S and dP.
+    void *ds;
+    int ds_ld;  // queries per dS^T row: S rounded up to a multiple of 256
 };
 
 // Returns hipSuccess or the launch error.  `D` is 64 or 128.

@@ -21,7 +21,8 @@ FA_MAX_ROPE_AXES = 8
 
 EXPORTED = [
     "fa_version", "fa_last_error", "fa_op_name", "fa_init",
-    "fa_attn_fwd", "fa_attn_fwd_workspace_size", "fa_attn_bwd_workspace_size", "fa_attn_bwd",
+    "fa_attn_fwd", "fa_attn_fwd_workspace_size", "fa_attn_bwd_workspace_size", "fa_attn_bwd_min_workspace_size",
+    "fa_attn_bwd",
     "fa_attn_bwd_phase", "fa_attn_bwd_noalloc",
     "fa_qk_prologue_fwd", "fa_qk_prologue_bwd", "fa_rope_tables_host",
     "fa_qk_prologue_fwd_multi", "fa_qk_prologue_bwd_multi",
@@ -249,6 +250,8 @@ def lib() -> ctypes.CDLL:
     L.fa_attn_fwd_workspace_size.argtypes = [ctypes.POINTER(AttnFwdArgs)]
     L.fa_attn_bwd_workspace_size.restype = ctypes.c_size_t
     L.fa_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnBwdArgs)]
+    L.fa_attn_bwd_min_workspace_size.restype = ctypes.c_size_t
+    L.fa_attn_bwd_min_workspace_size.argtypes = [ctypes.POINTER(AttnBwdArgs)]
     L.fa_lora_bwd_workspace_size.restype = ctypes.c_size_t
     L.fa_lora_bwd_workspace_size.argtypes = [ctypes.POINTER(LoraBwdArgs)]
     for name, st in (("fa_ln_mod_fwd", LnModArgs), ("fa_ln_mod_bwd", LnModBwdArgs),

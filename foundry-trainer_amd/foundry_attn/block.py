@@ -45,7 +45,8 @@ import torch
 
 from . import _abi, gemm_tuning
 from ._abi import FoundryAttnError, check, lib
-from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_fwd, lora_bwd, lora_down, lora_fwd, lora_grad,
+from .ops import (_dtype_code, _ptr, _stream, attn_bwd, attn_bwd_workspace_bytes, attn_fwd, lora_bwd, lora_down,
+                  lora_fwd, lora_grad,
                   lora_grad_many,
                   lora_up, qk_prologue_bwd_multi, qk_prologue_multi, rope_tables)
 
@@ -652,7 +653,8 @@ class DoubleBlockLoRA:
                  "o": torch.empty((1, S, H, D), **kw), "do": torch.empty((1, S, H, D), **kw),
                  "dq": torch.empty((1, S, H, D), **kw), "dk": torch.empty((1, S, H, D), **kw),
                  "lse": torch.empty((1, H, S), dtype=torch.float32, device=self.device),
-                 "ws": torch.empty(2 * ((H * S * 4 + 255) // 256) * 256, dtype=torch.uint8, device=self.device)}
+                 "ws": torch.empty(attn_bwd_workspace_bytes(1, S, H, D, self.dtype), dtype=torch.uint8,
+                                  device=self.device)}
             for name in STREAMS:
                 n = self.rows[name]
                 for key, width in (("h", C), ("out", C), ("x1", C), ("h2", C), ("y", C), ("t1", C),
@@ -1128,7 +1130,8 @@ class SingleBlockLoRA:
                 "q": torch.empty((1, S, H, D), **kw), "k": torch.empty((1, S, H, D), **kw),
                 "dq": torch.empty((1, S, H, D), **kw), "dk": torch.empty((1, S, H, D), **kw),
                 "lse": torch.empty((1, H, S), dtype=torch.float32, device=self.device),
-                "ws": torch.empty(2 * ((H * S * 4 + 255) // 256) * 256, dtype=torch.uint8, device=self.device)}
+                "ws": torch.empty(attn_bwd_workspace_bytes(1, S, H, D, self.dtype), dtype=torch.uint8,
+                                  device=self.device)}
             if self.fused:
                 P = ADAPTER_PAD
                 for key in ("nh_ext", "out_ext", "dout_ext", "dnh_ext"):  # padding columns stay zero

@@ -122,6 +122,16 @@ def attn_fwd(q, k, v, scale: Optional[float] = None, key_keep=None, out=None, ls
     return (o4[0] if squeeze else o4), lse_t
 
 
+def attn_bwd_workspace_bytes(B: int, S: int, H: int, D: int, dtype=torch.bfloat16, minimum: bool = False) -> int:
+    """Backward workspace bytes for (B, S, H, D) on the current device: the
+    full size (dQ reads the dK/dV kernel's stored dS where that path applies)
+    or, with minimum, the least fa_attn_bwd accepts (dQ recomputes S and dP).
+    Both give the same bits."""
+    ba = _abi.AttnBwdArgs(dtype=_dtype_code(torch.empty(0, dtype=dtype)), batch=B, seq=S, heads=H, head_dim=D)
+    f = lib().fa_attn_bwd_min_workspace_size if minimum else lib().fa_attn_bwd_workspace_size
+    return int(f(ctypes.byref(ba)))
+
+
 def attn_workspace_bytes(q) -> Tuple[int, int]:
     """(forward, backward) workspace bytes the library asks for q's shape
     (B,S,H,D) or (S,H,D) and dtype on its device: the forward's is 0 unless
@@ -174,13 +184,17 @@ def attn_bwd(q, k, v, o, dout, lse, scale: Optional[float] = None, key_keep=None
                          dv=_ptr(dv), q_stride=_strides(q4), k_stride=_strides(k4),
                          v_stride=_strides(v4), o_stride=_strides(o4), do_stride=_strides(do4),
                          dq_stride=_strides(dq), dk_stride=_strides(dk), dv_stride=_strides(dv))
+    # a given workspace of at least the minimum is used as it is (below the
+    # full size: dQ recomputes S and dP); none gets the full size (dQ reads
+    # the dK/dV kernel's stored dS)
     need = lib().fa_attn_bwd_workspace_size(ctypes.byref(a))
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
+    least = lib().fa_attn_bwd_min_workspace_size(ctypes.byref(a))
+    if workspace is None or workspace.numel() * workspace.element_size() < least:
         if workspace is not None and phases is not None:
             # separate phase calls share the pre-pass rows through it
             raise FoundryAttnError(_abi.FA_ERR_INVALID_ARG,
                                    f"workspace of {workspace.numel() * workspace.element_size()} bytes is "
-                                   f"smaller than the {need} these shapes need")
+                                   f"smaller than the {least} these shapes need")
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q4.device)
     a.workspace = workspace.data_ptr()
     a.workspace_bytes = workspace.numel() * workspace.element_size()

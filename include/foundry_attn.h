@@ -134,11 +134,24 @@ typedef struct fa_attn_bwd_args {
     fa_strides dq_stride, dk_stride, dv_stride;
 } fa_attn_bwd_args;
 
-/* Bytes of workspace fa_attn_bwd needs for these shapes (0 on bad args): the
+/* Bytes of workspace fa_attn_bwd takes for these shapes (0 on bad args): the
  * pre-pass rows, plus, for the shapes fa_attn_fwd_workspace_size splits, f32
  * partial sums of dQ, dK and dV (dQ's key range and dK/dV's query range are
- * split the same way, and a reduce pass adds the partials in a fixed order). */
+ * split the same way, and a reduce pass adds the partials in a fixed order),
+ * plus, for unsplit bf16 calls with 8-wave workgroups, the bf16 dS of every
+ * (key, query) pair ([B*H][seq rounded up to 32][seq rounded up to 256]),
+ * through which dQ reads the dK/dV kernel's dS instead of recomputing S and
+ * dP (about 1 GB at B1 H24 S4608).  No reference counterpart: AttnBwd::bwd
+ * (lib.rs:216-263) allocates its own tensors. */
 size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
+
+/* The least workspace fa_attn_bwd accepts (0 on bad args): without the dS^T
+ * rows, so dQ recomputes S and dP.  A workspace of at least
+ * fa_attn_bwd_workspace_size bytes takes the stored-dS path, a smaller one
+ * (of at least this size) the recomputing one.  Both multiply the same bf16
+ * dS by K in the same key order, so they give the same bits.  No reference
+ * counterpart. */
+size_t fa_attn_bwd_min_workspace_size(const fa_attn_bwd_args *args);
 
 /* dQ, dK, dV of the forward above: P is recomputed from Q, K and the saved
  * LSE; dS = P * (dP - rowsum(dO * O)) * scale; dQ = dS K, dK = dS^T Q,
@@ -147,9 +160,11 @@ size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
  * round would be under half full -- the dQ kernel runs on a library-owned
  * side stream (one per host thread and device, default priority) beside
  * dK/dV, joined back to `stream` by events before the call returns.  With
- * 8-wave workgroups the launches run in order on `stream`: dQ (which also
- * forms the pre-pass for its queries), then dK/dV; a split call adds one
- * reduce of the partials.  Either way everything queued on `stream`
+ * 8-wave workgroups the launches run in order on `stream`: with the full
+ * workspace the pre-pass, dK/dV (also storing dS), then dQ = dS K * scale
+ * read from the stored dS; with the minimum one dQ (which also forms the
+ * pre-pass for its queries, recomputing S and dP), then dK/dV; a split call
+ * adds one reduce of the partials.  Either way everything queued on `stream`
  * afterwards sees the results.  Replaces AttnBwd::bwd (lib.rs:216-263). */
 fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
 
@@ -157,10 +172,14 @@ fa_status fa_attn_bwd(const fa_attn_bwd_args *args, void *stream);
  * two independent gradient kernels on separate streams:
  *   FA_BWD_PREPASS  rowsum(dO * O) and LSE*log2(e) into the workspace
  *   FA_BWD_DKDV     dK and dV (needs the pre-pass)
- *   FA_BWD_DQ       dQ        (needs the pre-pass)
+ *   FA_BWD_DQ       dQ        (needs the pre-pass; through the stored dS,
+ *                             also dK/dV, whose dS it reads)
  * FA_BWD_ALL runs all three, as fa_attn_bwd.  The caller orders the pre-pass
- * before the other two (same stream, or an event).  No reference
- * counterpart: AttnBwd::bwd (lib.rs:216-263) is one call. */
+ * before the other two (same stream, or an event), and with a workspace of
+ * fa_attn_bwd_workspace_size bytes (the stored-dS path, see above) dK/dV
+ * before dQ; with fa_attn_bwd_min_workspace_size bytes dK/dV and dQ are
+ * independent.  No reference counterpart: AttnBwd::bwd (lib.rs:216-263) is
+ * one call. */
 typedef enum fa_bwd_phase {
     FA_BWD_ALL = 0,
     FA_BWD_PREPASS = 1,

@@ -174,11 +174,13 @@ static void run_case(const char *name, int dtype, int B, int S, int H, int D, in
     ba.q_stride = ba.k_stride = ba.v_stride = ba.o_stride = ba.do_stride = st;
     ba.dq_stride = ba.dk_stride = ba.dv_stride = st;
     const size_t ws_bytes = fa_attn_bwd_workspace_size(&ba);
-    expect(ws_bytes > 0, "fa_attn_bwd_workspace_size > 0");
-    ba.workspace_bytes = ws_bytes - 1;
+    const size_t ws_min = fa_attn_bwd_min_workspace_size(&ba);
+    expect(ws_bytes > 0 && ws_min > 0 && ws_min <= ws_bytes,
+           "fa_attn_bwd_workspace_size >= fa_attn_bwd_min_workspace_size > 0");
+    ba.workspace_bytes = ws_min - 1;
     HIP_OK(hipMalloc(&ba.workspace, ws_bytes));
     expect(fa_attn_bwd(&ba, NULL) == FA_ERR_INVALID_ARG && fa_last_error()[0] != 0,
-           "a workspace one byte short is refused with a message");
+           "a workspace one byte under the minimum is refused with a message");
     ba.workspace_bytes = ws_bytes;
     expect(fa_attn_bwd(&ba, NULL) == FA_OK, "fa_attn_bwd returns FA_OK");
     HIP_OK(hipDeviceSynchronize());

@@ -122,6 +122,29 @@ def test_bwd_workspace_size_and_validation():
     a.workspace, a.workspace_bytes = fake, need - 256
     assert lib().fa_attn_bwd(ctypes.byref(a), None) == _abi.FA_ERR_INVALID_ARG
     assert b"workspace" in lib().fa_last_error()
+    # 4-wave shapes and f32 have no stored-dS path: the full size is the least
+    assert lib().fa_attn_bwd_min_workspace_size(ctypes.byref(a)) == need
+    # an 8-wave bf16 shape (44 heads x 5 tiles: 220 workgroups) adds the dS
+    # blocks, [heads][S rounded up to 32][S rounded up to 256] bf16, and
+    # accepts any workspace of at least the minimum
+    b = _abi.AttnBwdArgs.from_buffer_copy(a)
+    b.batch, b.seq, b.heads = 1, 1100, 44
+    full = lib().fa_attn_bwd_workspace_size(ctypes.byref(b))
+    least = lib().fa_attn_bwd_min_workspace_size(ctypes.byref(b))
+    assert least == 2 * ((44 * 1100 * 4 + 255) // 256 * 256)
+    assert full - least == (44 * 1120 * 1280 * 2 + 255) // 256 * 256
+    b.dtype = 1
+    assert lib().fa_attn_bwd_workspace_size(ctypes.byref(b)) == lib().fa_attn_bwd_min_workspace_size(ctypes.byref(b))
+    b.dtype = 0
+    ok_dev = _abi.FA_OK if gpu_available() else _abi.FA_ERR_NO_DEVICE
+    st2 = _abi.Strides(128 * 44 * 1100, 128 * 44, 128)
+    for f in ("q_stride", "k_stride", "v_stride", "o_stride", "do_stride", "dq_stride", "dk_stride", "dv_stride"):
+        setattr(b, f, st2)
+    b.workspace, b.workspace_bytes = fake, least - 256
+    assert lib().fa_attn_bwd(ctypes.byref(b), None) == _abi.FA_ERR_INVALID_ARG
+    if not gpu_available():
+        b.workspace_bytes = least
+        assert lib().fa_attn_bwd(ctypes.byref(b), None) == ok_dev
 
 
 def test_bwd_noalloc_validates_before_device_work():

@@ -458,10 +458,14 @@ def test_attn_bwd_noncontiguous_lse():
 def test_backward_phases_match_single_call(B, S, H, D):
     """fa_attn_bwd_phase: pre-pass, dK/dV and dQ issued separately (one
     stream, then dK/dV and dQ on two streams) give the one-call bits.  With
-    8-wave kernels the one call is two launches (dQ doing the pre-pass for
-    its own queries, then dK/dV), whose row sums follow the pre-pass's order;
-    a split call adds the reduce, and its phases reduce their own partials."""
+    8-wave kernels the one call (full workspace) is the pre-pass, dK/dV
+    storing dS, then dQ from it; its phases on two streams run dQ after dK/dV.
+    With the minimum workspace dQ recomputes S and dP (and, in one call, also
+    does the pre-pass for its queries, in the pre-pass's order), so dK/dV and
+    dQ may run side by side -- with the same bits.  A split call adds the
+    reduce, and its phases reduce their own partials."""
     from foundry_attn import _abi
+    from foundry_attn.ops import attn_bwd_workspace_bytes
     torch.manual_seed(3)
     q, k, v, do = (torch.randn(B, S, H, D, device="cuda").to(torch.bfloat16) for _ in range(4))
     keep = torch.ones(B, S, dtype=torch.uint8, device="cuda")
@@ -473,7 +477,18 @@ def test_backward_phases_match_single_call(B, S, H, D):
                            (_abi.FA_BWD_DQ, None)])
     cur = torch.cuda.current_stream()
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()  # default priority
-    ws = torch.empty(attn_workspace_bytes(q)[1], dtype=torch.uint8, device="cuda")
+    full = torch.empty(attn_workspace_bytes(q)[1], dtype=torch.uint8, device="cuda")
+    out_f = tuple(torch.empty_like(q) for _ in range(3))
+    attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=full, out=out_f,
+             phases=[(_abi.FA_BWD_PREPASS, None)])
+    s1.wait_stream(cur)
+    attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=full, out=out_f,
+             phases=[(_abi.FA_BWD_DKDV, s1)])
+    s2.wait_stream(s1)
+    attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=full, out=out_f,
+             phases=[(_abi.FA_BWD_DQ, s2)])
+    cur.wait_stream(s2)
+    ws = torch.empty(attn_bwd_workspace_bytes(B, S, H, D, minimum=True), dtype=torch.uint8, device="cuda")
     out = tuple(torch.empty_like(q) for _ in range(3))
     attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=ws, out=out,
              phases=[(_abi.FA_BWD_PREPASS, None)])
@@ -486,8 +501,42 @@ def test_backward_phases_match_single_call(B, S, H, D):
     cur.wait_stream(s1)
     cur.wait_stream(s2)
     torch.cuda.synchronize()
-    for a, b, c in zip(ref, seq, out):
-        assert torch.equal(a, b) and torch.equal(a, c)
+    for a, b, c, f in zip(ref, seq, out, out_f):
+        assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, f)
+
+
+@pytest.mark.parametrize("B,S,H,D,masked", [(1, 1100, 44, 128, False), (1, 1037, 44, 128, True),
+                                            (1, 1100, 44, 64, True), (1, 4608, 24, 128, False)],
+                         ids=["8wave", "ragged_masked", "d64_masked", "c2"])
+def test_stored_ds_backward_matches_recompute(B, S, H, D, masked):
+    """With the full workspace the 8-wave backward stores dS from dK/dV and
+    forms dQ = dS K from it; with the minimum one dQ recomputes S and dP.
+    Both multiply the same bf16 dS by K in the same key order, so the
+    gradients are bit-identical -- including a key count that is not a
+    multiple of 32 or 64 (the last key tile and query block partly past S),
+    excluded keys (stored as zero dS), fully masked rows, and D = 64."""
+    from foundry_attn.ops import attn_bwd_workspace_bytes
+    torch.manual_seed(5)
+    q, k, v, do = (torch.randn(B, S, H, D, device="cuda").to(torch.bfloat16) for _ in range(4))
+    keep = None
+    if masked:
+        keep = torch.ones(B, S, dtype=torch.uint8, device="cuda")
+        keep[0, 37:301] = 0
+        keep[-1, S - 50:] = 0
+    o, lse = attn_fwd(q, k, v, key_keep=keep)
+    full_b, least_b = attn_bwd_workspace_bytes(B, S, H, D), attn_bwd_workspace_bytes(B, S, H, D, minimum=True)
+    assert full_b > least_b
+    res = []
+    for nbytes in (least_b, full_b, full_b):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        out = tuple(torch.empty_like(q) for _ in range(3))
+        attn_bwd(q, k, v, o, do, lse, key_keep=keep, workspace=ws, out=out)
+        torch.cuda.synchronize()
+        res.append(out)
+        del ws
+    for name, a, b, c in zip(("dq", "dk", "dv"), *res):
+        assert torch.equal(a, b), name
+        assert torch.equal(b, c), name  # repeatable
 
 
 @pytest.mark.parametrize("S,H", [(700, 4), (1100, 44), (1100, 4)], ids=["forked", "in_order", "split"])

@@ -31,10 +31,15 @@ def _splits(B, S, H, D, dtype=torch.bfloat16):
 
 def test_split_policy_and_workspace_sizes():
     """Split shapes ask for a forward workspace and a larger backward one;
-    full grids, short sequences and f32 ask for none beyond the pre-pass rows."""
+    full grids, short sequences and f32 ask for none beyond the pre-pass rows,
+    except the stored dS blocks of 8-wave bf16 grids (c2: [24 heads][4608
+    keys][4608 queries] bf16)."""
     def base(B, S, H):
         r = (B * H * S * 4 + 255) // 256 * 256
         return 2 * r
+
+    def ds(B, S, H):
+        return (B * H * ((S + 31) // 32 * 32) * ((S + 255) // 256 * 256) * 2 + 255) // 256 * 256
 
     fwd, bwd = _splits(1, 4608, 3, 128)  # one GPU's share of c2 over 8 GPUs
     assert fwd > 0 and bwd > base(1, 4608, 3)
@@ -43,7 +48,9 @@ def test_split_policy_and_workspace_sizes():
     split = min(cus // 54, 36 // 4, 16)
     assert fwd == (split * 3 * 4608 * 128 * 4 + 255) // 256 * 256 + (split * 3 * 4608 * 4 + 255) // 256 * 256
     assert bwd == base(1, 4608, 3) + 3 * ((split * 3 * 4608 * 128 * 4 + 255) // 256 * 256)
-    for shape in ((1, 4608, 24, 128), (4, 1536, 24, 128), (1, 900, 2, 128)):
+    f, b = _splits(1, 4608, 24, 128)
+    assert f == 0 and b == base(1, 4608, 24) + ds(1, 4608, 24)
+    for shape in ((4, 1536, 24, 128), (1, 900, 2, 128)):  # 4-wave grids: no stored dS
         f, b = _splits(*shape)
         assert f == 0 and b == base(shape[0], shape[1], shape[2]), shape
     f, b = _splits(1, 4608, 3, 128, torch.float32)
