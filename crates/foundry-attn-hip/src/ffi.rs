@@ -88,6 +88,7 @@ extern "C" {
     pub fn fa_attn_fwd(args: *const fa_attn_fwd_args, stream: *mut c_void) -> fa_status;
     pub fn fa_attn_fwd_workspace_size(args: *const fa_attn_fwd_args) -> usize;
     pub fn fa_attn_bwd_workspace_size(args: *const fa_attn_bwd_args) -> usize;
+    pub fn fa_attn_bwd_min_workspace_size(args: *const fa_attn_bwd_args) -> usize;
     pub fn fa_attn_bwd(args: *const fa_attn_bwd_args, stream: *mut c_void) -> fa_status;
     pub fn fa_attn_bwd_noalloc(args: *const fa_attn_bwd_args, stream: *mut c_void) -> fa_status;
 }
