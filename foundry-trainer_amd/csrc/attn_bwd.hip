@@ -160,6 +160,8 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
                                                   DS ? (uint32_t)(ds_head * 2) : 0u);
     const uint32_t ds_row = (uint32_t)(kt * (kKT / 32) + wave) * (uint32_t)(p.ds_ld / 16);  // this wave's first block
     const bool dkeep = !DS || (kj < S && (!p.keep || p.keep[(int64_t)b * S + kj]));
+    // wave-uniform: some lane of this wave has a key to zero (excluded, or past S)
+    const bool ds_zero = DS && (p.keep != nullptr || kt * kKT + wave * 32 + 32 > S);
 
     // K and V rows of this lane's key (B operands): features kd*16 + g*8 .. +8
     bf16x8 kf[D / 16], vf[D / 16];
@@ -279,15 +281,27 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
                 set_half(pf[grp >> 1], grp & 1, pw);
                 set_half(df[grp >> 1], grp & 1, dw);
             }
+            // dV += P^T dO, dK += dS^T Q  (contraction over the 32 queries)
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const uint32_t o0 = col_frag_at(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
+                    const uint32_t o1 = col_frag_at_hi8<D>(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
+                    dv[dt] = mfma_32x32x16(pf[ks], lds_read_col_frag(os_t, o0, o1), dv[dt]);
+                    dk[dt] = mfma_32x32x16(df[ks], lds_read_col_frag(qs_t, o0, o1), dk[dt]);
+                }
             if constexpr (DS) {
-                // df[j]: queries 16j + {4g .. 4g+3} (words 0, 1) and 16j + 8 + {4g ..} (words 2, 3);
+                // after the last MFMA that reads df, so the swaps work in its
+                // registers; df[j]: queries 16j + {4g .. 4g+3} (words 0, 1) and 16j + 8 + {4g ..} (words 2, 3);
                 // after the swap lane (n, g) holds queries 16j + 8g .. +8 of key n
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const u32x4 u = as_u32x4(df[j]);
                     const auto r0 = __builtin_amdgcn_permlane32_swap(u[0], u[2], false, false);
                     const auto r1 = __builtin_amdgcn_permlane32_swap(u[1], u[3], false, false);
-                    const u32x4 w = dkeep ? u32x4{r0[0], r1[0], r0[1], r1[1]} : u32x4{0u, 0u, 0u, 0u};
+                    u32x4 w = u32x4{r0[0], r1[0], r0[1], r1[1]};
+                    if (ds_zero && !dkeep) w = u32x4{0u, 0u, 0u, 0u};
                     __builtin_amdgcn_raw_buffer_store_b128(w, dsrs, (uint32_t)lane * 16,
                                                            (ds_row + (uint32_t)(qb * 4 + sub * 2 + j)) * 1024,
                                                            kDsCachePolicy);
@@ -300,16 +314,6 @@ __device__ __forceinline__ void dkdv_block(const AttnBwdParams &p, int work) {
                     asm volatile("s_nop 1" ::"v"(w));
                 }
             }
-            // dV += P^T dO, dK += dS^T Q  (contraction over the 32 queries)
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const uint32_t o0 = col_frag_at(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
-                    const uint32_t o1 = col_frag_at_hi8<D>(ca0, dt) + (sub * 2 + ks) * 16 * T::ROWB;
-                    dv[dt] = mfma_32x32x16(pf[ks], lds_read_col_frag(os_t, o0, o1), dv[dt]);
-                    dk[dt] = mfma_32x32x16(df[ks], lds_read_col_frag(qs_t, o0, o1), dk[dt]);
-                }
         }
     };
     for (int qb = qb0; qb < qend; qb += 2) {
