@@ -195,12 +195,15 @@ size_t bwd_min_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t
 // (there the 4-wave dK/dV kernel's stores cost what dQ saves: c3 431 against
 // 450 us), or a head's blocks spanning 4 GiB (the kernels' buffer offsets
 // are 32-bit).
+// Past FA_BWD_DS_MAX_BYTES of dS (16 GiB) a call keeps the recomputing path
+// rather than ask for a workspace of that size.
 int ds_ld_for(int32_t S) { return (S + 255) / 256 * 256; }
 size_t bwd_ds_bytes(int32_t dtype, int32_t B, int32_t S, int32_t H) {
     if (dtype != FA_DTYPE_BF16 || split_for(dtype, B, S, H) > 1 || fa::attn_waves(B, H, S) != 8) return 0;
     const int64_t head = (int64_t)(S + 31) / 32 * 32 * ds_ld_for(S) * 2;
     if (head >= (int64_t(1) << 32)) return 0;
-    return round256((size_t)B * H * head);
+    const size_t bytes = round256((size_t)B * H * head);
+    return bytes > (size_t)FA_BWD_DS_MAX_BYTES ? 0 : bytes;
 }
 
 size_t bwd_workspace(int32_t dtype, int32_t B, int32_t S, int32_t H, int32_t D) {

@@ -141,8 +141,11 @@ typedef struct fa_attn_bwd_args {
  * plus, for unsplit bf16 calls with 8-wave workgroups, the bf16 dS of every
  * (key, query) pair ([B*H][seq rounded up to 32][seq rounded up to 256]),
  * through which dQ reads the dK/dV kernel's dS instead of recomputing S and
- * dP (about 1 GB at B1 H24 S4608).  No reference counterpart: AttnBwd::bwd
- * (lib.rs:216-263) allocates its own tensors. */
+ * dP (about 1 GB at B1 H24 S4608; shapes whose dS would exceed
+ * FA_BWD_DS_MAX_BYTES keep the recomputing path and ask for no dS).  No
+ * reference counterpart: AttnBwd::bwd (lib.rs:216-263) allocates its own
+ * tensors. */
+#define FA_BWD_DS_MAX_BYTES (16ull << 30)
 size_t fa_attn_bwd_workspace_size(const fa_attn_bwd_args *args);
 
 /* The least workspace fa_attn_bwd accepts (0 on bad args): without the dS^T

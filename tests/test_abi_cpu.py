@@ -136,6 +136,10 @@ def test_bwd_workspace_size_and_validation():
     b.dtype = 1
     assert lib().fa_attn_bwd_workspace_size(ctypes.byref(b)) == lib().fa_attn_bwd_min_workspace_size(ctypes.byref(b))
     b.dtype = 0
+    # past 16 GiB of dS (here 8 x 44 heads at S 8192: 47 GiB) no dS is asked for
+    big = _abi.AttnBwdArgs.from_buffer_copy(b)
+    big.batch, big.seq = 8, 8192
+    assert lib().fa_attn_bwd_workspace_size(ctypes.byref(big)) == lib().fa_attn_bwd_min_workspace_size(ctypes.byref(big))
     ok_dev = _abi.FA_OK if gpu_available() else _abi.FA_ERR_NO_DEVICE
     st2 = _abi.Strides(128 * 44 * 1100, 128 * 44, 128)
     for f in ("q_stride", "k_stride", "v_stride", "o_stride", "do_stride", "dq_stride", "dk_stride", "dv_stride"):
