@@ -571,6 +571,11 @@ def attention_record(cfg, ms: float, kms: dict) -> dict:
         if nm in kflops:
             kernels[nm] = {"ms": round(t, 4), "tflops": round(tf(kflops[nm], t), 2),
                            "pct_of_peak": pct(tf(kflops[nm], t))}
+            # the HBM rate from the counter table's bytes per launch (dQ from
+            # the stored dS is HBM-bound)
+            hbm = TRAFFIC.get((cfg.name, nm))
+            if hbm:
+                kernels[nm]["hbm_gbs"] = round(hbm / (t * 1e-3) / 1e9, 1)
         else:
             gbs = pre_bytes / (t * 1e-3) / 1e9
             kernels[nm] = {"ms": round(t, 4), "gbs": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
