@@ -20,6 +20,10 @@
 //   3. dq:     one workgroup per NW*32 queries (NW waves x 32), looping over
 //              32-key LDS units.  S^T = K Q^T puts queries on the lanes, so
 //              dS^T feeds dQ^T = K^T dS^T as the B operand.
+// With a workspace for it (8-wave bf16 grids, p.ds), dK/dV also stores every
+// bf16 dS value and dQ becomes 3': an HBM-bound dQ^T = K^T dS^T over the
+// stored dS, the same products in the same key order as 3, so the same bits
+// without 3's recompute of S and dP (2 of its 3G of matrix work).
 // Tiles move HBM -> LDS with buffer_load ... lds (double-buffered, zero fill
 // past S); every transposed operand (dO^T, Q^T, K^T) is read from the same
 // row-major tile with ds_read_b64_tr_b16.  Eight-wave workgroups share each
